@@ -1,0 +1,130 @@
+/*
+ * yalm_hip.h -- C-ABI of the MI355X (gfx950) fp16 batch-1 decode path.
+ *
+ * This is the drop-in boundary behind the reference's C++ model API (allbilly/yalm):
+ * a host `Model`/`InferenceState` pair moved to `Device::HIP` owns one `yhip_ctx` and calls
+ * `yhip_forward` from `Model::forward`. Plain C types only: no HIP, torch or C++ types cross it.
+ *
+ * Conventions
+ *   - fp16 values travel as IEEE binary16 bit patterns in uint16_t.
+ *   - Weight matrices are row-major (out, in), exactly as stored in a .yalm file.
+ *   - KV caches use the reference layout (src/model.h:14-17, 266-268), per layer and kv head g:
+ *       K[g*hd*msl + (j/16)*16*msl + t*16 + j%16],   V[g*hd*msl + j*msl + t].
+ *   - Every entry point returns 0 on success and a negative code on failure; the library never
+ *     aborts. yhip_last_error() then describes the failure (thread-local for calls without a ctx).
+ *   - One context belongs to one host thread; all its work runs on the context's own stream.
+ *     Contexts on the same device are independent.
+ */
+#ifndef YALM_HIP_H
+#define YALM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define YHIP_OK 0
+#define YHIP_EINVAL (-1)   /* bad argument or unsupported shape */
+#define YHIP_EDEVICE (-2)  /* HIP runtime error */
+#define YHIP_ESTATE (-3)   /* missing upload or wrong call order */
+
+#define YHIP_MODE_HYDRATE 0 /* InferenceMode::HYDRATE_KV_CACHE (src/model.h:43-46) */
+#define YHIP_MODE_LOGITS 1  /* InferenceMode::OUTPUT_LOGITS */
+
+#define YHIP_ACT_GELU 0
+#define YHIP_ACT_SILU 1
+
+typedef struct yhip_ctx yhip_ctx;
+
+/* Mirrors the decode-relevant fields of the reference Config (src/model.h:56-82). */
+typedef struct {
+  int dim, hidden_dim, head_dim, n_layers, n_heads, n_kv_heads, vocab_size, max_seq_len, rotary_dim;
+  float rope_theta, norm_eps, qkv_clip;
+  int act; /* YHIP_ACT_* */
+} yhip_config;
+
+/* Context: device memory for weights, KV caches (zeroed) and activations, one stream.
+ * Replaces Model::cuda() + InferenceState::cuda() (src/model.cpp:342-361, 437-451) and the
+ * device-memory ABI upload_cuda/register_cuda_host/set_cuda_device/init_cuda_stream
+ * (src/model.h:48-54, src/infer.cu:60-91). */
+int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx** out);
+int yhip_destroy(yhip_ctx* ctx);
+
+/* Weight upload (host -> HBM), replaces Block::cuda() (src/model.cpp:217-241).
+ * Shapes: rms_* [dim] fp32; wq [n_heads*hd][dim]; wk, wv [n_kv_heads*hd][dim]; wo [dim][n_heads*hd];
+ * w1, w3 [hidden][dim]; w2 [dim][hidden]. */
+int yhip_upload_layer(yhip_ctx* ctx, int layer, const float* rms_att, const float* rms_ffn,
+                      const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, const uint16_t* wo,
+                      const uint16_t* w1, const uint16_t* w2, const uint16_t* w3);
+/* embed [vocab][dim]; rms_final [dim]; wcls [vocab][dim] or NULL for a tied lm_head
+ * (src/model.cpp:425-434). Replaces the global part of Model::cuda(). */
+int yhip_upload_globals(yhip_ctx* ctx, const uint16_t* embed, const float* rms_final, const uint16_t* wcls);
+
+/* One decode step: Model::forward(s, token, pos, mode) (src/model.cpp:479-494,
+ * src/infer.cu:1274-1294). Writes K/V of `pos` into every layer's cache. In YHIP_MODE_LOGITS it
+ * returns after `logits_host` [vocab] holds the next-token logits; in YHIP_MODE_HYDRATE it may
+ * return before the device finishes (stream order keeps later calls correct) and logits_host is
+ * ignored. `logits_host` may be the pointer from yhip_logits_host() (no extra host copy). */
+int yhip_forward(yhip_ctx* ctx, int token, int pos, int mode, float* logits_host);
+
+/* Greedy decode step: like yhip_forward(LOGITS) but returns only the argmax token id computed on
+ * the device with the reference tie rule (src/sampler.cpp:27-38). */
+int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_token);
+
+/* Pinned host buffer [vocab] that yhip_forward fills without an extra copy when passed back. */
+float* yhip_logits_host(yhip_ctx* ctx);
+
+/* KV cache copies in the reference layout (n_kv_heads*hd*max_seq_len fp16 each). */
+int yhip_kv_read(yhip_ctx* ctx, int layer, uint16_t* k_host, uint16_t* v_host);
+int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16_t* v_host);
+
+/* Options: "graph" (1 = replay a captured hipGraph per step, default; 0 = direct launches),
+ * "attn_splits" (KV slices per kv head, default 256/n_kv_heads clamped to [1,64]). */
+int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
+
+/* Debug read of a device activation after the last forward: which = 0 x [dim], 1 q [nh*hd],
+ * 2 attention output [nh*hd], 3 hb [hidden], 4 logits [vocab]. Mirrors the reference's
+ * DEBUG_MODEL tensor dumps (src/infer.cu:93-109). */
+int yhip_debug_read(yhip_ctx* ctx, int which, float* host, size_t n);
+
+const char* yhip_last_error(const yhip_ctx* ctx);
+
+/* ---- kernel-level hooks, mirroring matmul_cuda / mha_cuda / ffn_cuda (src/model.h:328-374).
+ * Host pointers in and out; each call allocates device buffers, launches, syncs and frees. ---- */
+
+/* out[d] = W[d][n] . xn, where xn = rmsnorm(x, gain, eps) if gain != NULL else x
+ * (src/infer.cpp:63-100 and 136-146). If resid != NULL, out = resid + W.xn. */
+int yhip_test_matvec(const float* x, const float* gain, float eps, const uint16_t* w, int n, int d,
+                     const float* resid, float* out);
+/* Gated FFN with fused pre-norm: hb = act(W1 xn) * (W3 xn); out = resid + W2 hb (resid may be
+ * NULL -> out = W2 hb). gain NULL disables the norm (src/infer.cpp:346-391, 424-455). */
+int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* w1, const uint16_t* w2,
+                  const uint16_t* w3, int hidden_dim, int dim, int act, const float* resid, float* out);
+/* GQA attention over reference-layout caches (src/infer.cpp:218-250, 394-415); `nsplit` KV slices
+ * per kv head (0 = default). att_out [n_heads*hd]. pos >= max_seq_len exercises sink rotation, which
+ * rewrites kcache (the updated K cache is copied back). kv_len is derived from pos. */
+int yhip_test_attention(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
+                        int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
+                        int rotary_dim, float* att_out);
+/* Fused pre-norm + QKV matvec + clip + RoPE + KV-cache write (src/infer.cpp:267-305).
+ * q_out [nh*hd]; kcache/vcache [n_kv*hd*msl] updated in place at kv_pos(pos). */
+int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* wq, const uint16_t* wk,
+                  const uint16_t* wv, int dim, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                  int rotary_dim, float rope_theta, float qkv_clip, int pos, float* q_out, uint16_t* kcache,
+                  uint16_t* vcache);
+/* Greedy argmax on the device with the reference tie rule. */
+int yhip_test_argmax(const float* logits, int n, int* out);
+
+/* ---- microbenchmark: one fused decode kernel at a given shape, weights rotated over `copies`
+ * device-resident copies (to keep the 256 MB last-level cache from serving them), timed with HIP
+ * events on the launching stream. kind: 0 = rmsnorm+QKV+RoPE (rows = q+k+v dims), 1 = O-proj +
+ * residual, 2 = rmsnorm + W1/W3 + SwiGLU, 3 = W2 + residual, 4 = rmsnorm + lm_head.
+ * Writes the mean kernel time in microseconds. ---- */
+int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, float* us_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* YALM_HIP_H */

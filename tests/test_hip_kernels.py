@@ -1,0 +1,207 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (reference src/infer.cpp semantics).
+
+Tolerances: integer/index work bit-exact; fp32-accumulated matvecs and attention within
+rel-L2 1e-5 of the oracle (both accumulate in fp32, only the summation order differs).
+"""
+import numpy as np
+import pytest
+
+from oracle import binding as O
+from tests import npref
+from tests.util import f16, h2f
+
+pytestmark = pytest.mark.gpu
+
+H = None
+
+
+def hip():
+    global H
+    if H is None:
+        from yalm_amd import hip as _h
+        _h.lib()
+        H = _h
+    return H
+
+
+RTOL = 1e-5
+
+
+@pytest.mark.parametrize("d,n", [(32, 64), (100, 256), (384, 768), (6144, 4096), (4096, 14336), (1000, 4096)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_matvec_parity(d, n, norm):
+    rng = np.random.default_rng(d * 7 + n)
+    w = f16(rng.standard_normal((d, n)) * 0.02)
+    x = rng.standard_normal(n).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32) if norm else None
+    got = hip().matvec(x, w, gain=g, eps=1e-5)
+    xin = O.rmsnorm(x, g, 1e-5) if norm else x
+    want = O.matmul_f16(xin, w)
+    assert npref.rel_l2(got, want) < RTOL
+    r = rng.standard_normal(d).astype(np.float32)
+    got_r = hip().matvec(x, w, gain=g, eps=1e-5, resid=r)
+    assert npref.rel_l2(got_r, want + r) < RTOL
+
+
+@pytest.mark.parametrize("n", [64, 4096, 14336])
+def test_matvec_one_hot_is_exact(n):
+    rng = np.random.default_rng(n)
+    w = f16(rng.standard_normal((64, n)))
+    for j in (0, n // 3, n - 1):
+        x = np.zeros(n, np.float32)
+        x[j] = 1.0
+        assert np.array_equal(hip().matvec(x, w), h2f(w[:, j]))
+
+
+@pytest.mark.parametrize("dim,hidden", [(64, 128), (256, 768), (4096, 14336)])
+@pytest.mark.parametrize("act", [1, 0])
+def test_ffn_parity(dim, hidden, act):
+    rng = np.random.default_rng(dim + hidden + act)
+    w1 = f16(rng.standard_normal((hidden, dim)) * 0.02)
+    w2 = f16(rng.standard_normal((dim, hidden)) * 0.02)
+    w3 = f16(rng.standard_normal((hidden, dim)) * 0.02)
+    x = rng.standard_normal(dim).astype(np.float32)
+    g = np.ones(dim, np.float32)
+    resid = rng.standard_normal(dim).astype(np.float32)
+    got = hip().ffn(x, w1, w2, w3, gain=g, eps=1e-5, act=act, resid=resid)
+    want = O.ffn(O.rmsnorm(x, g, 1e-5), w1, w2, w3, act) + resid
+    assert npref.rel_l2(got, want) < RTOL
+
+
+ATTN_CASES = [
+    # hd, nh, nkv, msl, kv_len, nsplit
+    (16, 4, 2, 64, 1, 0),
+    (32, 8, 2, 512, 17, 0),
+    (32, 8, 2, 512, 512, 3),
+    (64, 8, 8, 200, 199, 7),
+    (128, 32, 8, 4096, 93, 0),
+    (128, 32, 8, 4096, 3201, 0),
+    (128, 32, 8, 4096, 4096, 64),
+    (128, 32, 8, 16448, 16417, 0),
+    (128, 8, 1, 1024, 700, 1),
+]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,msl,kv_len,nsplit", ATTN_CASES)
+def test_attention_parity(hd, nh, nkv, msl, kv_len, nsplit):
+    rng = np.random.default_rng(hd * nh + kv_len)
+    kb = f16(rng.standard_normal(nkv * hd * msl))
+    vb = f16(rng.standard_normal(nkv * hd * msl))
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    got, k_after = hip().attention(q, kb, vb, hd, kv_len - 1, msl, nh, nkv, nsplit=nsplit)
+    want, _ = O.mha(q, kb, vb, hd, kv_len, msl, nh, nkv)
+    assert npref.rel_l2(got, want) < RTOL
+    assert np.array_equal(k_after, kb)  # no sink rotation below max_seq_len
+
+
+def test_attention_kv_len_one_returns_v0_exactly():
+    rng = np.random.default_rng(5)
+    hd, nh, nkv, msl = 128, 32, 8, 256
+    kb = f16(rng.standard_normal(nkv * hd * msl))
+    vb = f16(rng.standard_normal(nkv * hd * msl))
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    got, _ = hip().attention(q, kb, vb, hd, 0, msl, nh, nkv)
+    V = h2f(vb).reshape(nkv, hd, msl)
+    want = np.concatenate([V[h // (nh // nkv), :, 0] for h in range(nh)])
+    assert np.array_equal(got, want)
+
+
+def test_attention_known_answer_one_hot_softmax():
+    # The reference's known-answer construction (src/test.cpp:67-125) at head_dim 16: huge query
+    # entries make each head's softmax one-hot on a chosen position.
+    hd, msl, nh, nkv = 16, 4, 2, 1
+    kb = np.zeros(16 * msl, np.uint16)
+    kb[0 * 16 + 0] = f16([1.0])[0]    # t=0, dim 0
+    kb[1 * 16 + 1] = f16([1.0])[0]    # t=1, dim 1
+    kb[2 * 16 + 2] = f16([1.0])[0]    # t=2, dim 2
+    kb[3 * 16 + 0] = f16([-1.0])[0]   # t=3, dim 0
+    V = np.zeros((hd, msl), np.float32)
+    V[0] = [1, 0, 0, -1]
+    V[1] = [0, 1, 0, 0]
+    V[2] = [0, 0, 1, 0]
+    vb = f16(V.reshape(-1))
+    q = np.zeros(nh * hd, np.float32)
+    q[1] = 1e4
+    q[hd + 2] = 1e4
+    got, _ = hip().attention(q, kb, vb, hd, msl - 1, msl, nh, nkv)
+    want = np.zeros(nh * hd, np.float32)
+    want[1] = 1.0
+    want[hd + 2] = 1.0
+    assert np.allclose(got, want, atol=1e-4)
+
+
+def _oracle_qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc, theta=1e6, clip=3.4028234663852886e38):
+    xb = O.rmsnorm(x, g, 1e-5) if g is not None else x.astype(np.float32)
+    q = np.clip(O.matmul_f16(xb, wq), -clip, clip)
+    k = np.clip(O.matmul_f16(xb, wk), -clip, clip)
+    v = np.clip(O.matmul_f16(xb, wv), -clip, clip)
+    q = O.rope(q, hd, pos, theta, hd)
+    k = O.rope(k, hd, pos, theta, hd)
+    kc = kc.copy()
+    vc = vc.copy()
+    for i in range(k.size):
+        gi, j = divmod(i, hd)
+        kc[gi * hd * msl + O.k_cache_idx(j, pos, msl)] = O.f2h([k[i]])[0]
+        vc[gi * hd * msl + j * msl + pos] = O.f2h([v[i]])[0]
+    return q, kc, vc
+
+
+def test_qkv_kv_write_bit_exact_at_pos0():
+    # One-hot input, no norm, pos 0 (RoPE = identity): every K/V entry is an exact fp16 weight and
+    # must land at the reference index.
+    rng = np.random.default_rng(6)
+    dim, nh, nkv, hd, msl = 4096, 32, 8, 128, 64
+    wq = f16(rng.standard_normal((nh * hd, dim)))
+    wk = f16(rng.standard_normal((nkv * hd, dim)))
+    wv = f16(rng.standard_normal((nkv * hd, dim)))
+    x = np.zeros(dim, np.float32)
+    x[123] = 1.0
+    kc = np.zeros(nkv * hd * msl, np.uint16)
+    vc = np.zeros(nkv * hd * msl, np.uint16)
+    q, k2, v2 = hip().qkv(x, None, wq, wk, wv, nh, nkv, hd, msl, 0, kc, vc)
+    qo, ko, vo = _oracle_qkv(x, None, wq, wk, wv, nh, nkv, hd, msl, 0, kc, vc)
+    assert np.array_equal(q, h2f(wq[:, 123]))
+    assert np.array_equal(k2, ko)
+    assert np.array_equal(v2, vo)
+
+
+@pytest.mark.parametrize("pos", [0, 5, 4095])
+@pytest.mark.parametrize("shape", [(256, 8, 2, 32, 512), (4096, 32, 8, 128, 4096)])
+def test_qkv_rope_parity(pos, shape):
+    dim, nh, nkv, hd, msl = shape
+    rng = np.random.default_rng(pos + dim)
+    wq = f16(rng.standard_normal((nh * hd, dim)) * 0.02)
+    wk = f16(rng.standard_normal((nkv * hd, dim)) * 0.02)
+    wv = f16(rng.standard_normal((nkv * hd, dim)) * 0.02)
+    x = rng.standard_normal(dim).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    kc = f16(rng.standard_normal(nkv * hd * msl))
+    vc = f16(rng.standard_normal(nkv * hd * msl))
+    q, k2, v2 = hip().qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc)
+    qo, ko, vo = _oracle_qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc)
+    # the RoPE angle error grows with pos (fp32 frequencies can differ by an ulp between libms)
+    assert npref.rel_l2(q, qo) < 1e-5 + 3e-7 * pos
+    changed = (k2 != kc) | (ko != kc)
+    # only the entries of position `pos` may change, and they are all at reference indices
+    idx = np.array([gi * hd * msl + O.k_cache_idx(j, pos, msl) for gi in range(nkv) for j in range(hd)])
+    mask = np.zeros_like(changed)
+    mask[idx] = True
+    assert not np.any(changed & ~mask)
+    assert npref.rel_l2(h2f(k2[idx]), h2f(ko[idx])) < 2e-3
+    vidx = np.array([gi * hd * msl + j * msl + pos for gi in range(nkv) for j in range(hd)])
+    vmask = np.zeros(vc.size, bool)
+    vmask[vidx] = True
+    assert np.array_equal(v2[~vmask], vc[~vmask])
+    assert npref.rel_l2(h2f(v2[vidx]), h2f(vo[vidx])) < 2e-3
+
+
+def test_argmax_tie_rule():
+    lg = np.zeros(32000, np.float32)
+    assert hip().argmax(lg) == 0
+    lg[[7, 300, 31999]] = 5.0
+    assert hip().argmax(lg) == 7
+    rng = np.random.default_rng(8)
+    lg = rng.standard_normal(32000).astype(np.float32)
+    assert hip().argmax(lg) == O.argmax(lg)
+    lg[-1] = np.inf
+    assert hip().argmax(lg) == 31999

@@ -1,0 +1,615 @@
+// CDNA4 (gfx950) device code for the fp16 batch-1 decode step.
+//
+// Data layout in HBM (all row-major, as in the .yalm file):
+//   weights fp16 [rows][K]; activations fp32; KV caches fp16 per layer
+//   K[g][(j/16)*16*msl + t*16 + j%16], V[g][j*msl + t]   (reference src/model.h:14-17, 266-268)
+//
+// Every kernel runs 256-thread workgroups (four 64-lane wavefronts). Matvecs stream weight rows
+// with 16-byte loads: lane l of a wave reads bytes [16*(l + 64u), +16) of each row it owns, so a
+// wave-wide load instruction covers 1 KiB of one row and every HBM line is read exactly once.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yk {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kKvSinks = 2;  // reference src/model.h:12
+constexpr float kNegBig = -3.402823466e38f;
+
+// Per-token parameters, resident on the device so that a captured graph stays static.
+struct StepParams {
+  int token;
+  int pos;
+  int pad[2];
+};
+
+// Position arithmetic of reference src/infer.cpp:489-494.
+struct Positions {
+  int kv_sink, kv_pos, kv_len;
+};
+__device__ __forceinline__ Positions positions(int pos, int msl) {
+  Positions p;
+  p.kv_sink = pos >= msl ? kKvSinks : 0;
+  p.kv_pos = p.kv_sink + (pos - p.kv_sink) % (msl - p.kv_sink);
+  p.kv_len = pos >= msl ? msl : pos + 1;
+  return p;
+}
+
+__device__ __forceinline__ int k_cache_idx(int j, int t, int msl) {
+  return (j >> 4) * (16 * msl) + t * 16 + (j & 15);
+}
+
+// Wavefront reductions on DPP: an inclusive row scan (row_shr 1,2,4,8) leaves each 16-lane row's
+// total in its lane 15; row_bcast:15 and row_bcast:31 fold the rows so that lane 63 holds the
+// wave total, which readlane returns uniformly to every lane. No LDS traffic.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_src(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float lane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_src<0x111, 0xf>(0.f, v);  // row_shr:1
+  v += dpp_src<0x112, 0xf>(0.f, v);  // row_shr:2
+  v += dpp_src<0x114, 0xf>(0.f, v);  // row_shr:4
+  v += dpp_src<0x118, 0xf>(0.f, v);  // row_shr:8
+  v += dpp_src<0x142, 0xa>(0.f, v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_src<0x143, 0xc>(0.f, v);  // row_bcast:31 into rows 2 and 3
+  return lane63(v);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_src<0x111, 0xf>(v, v));
+  v = fmaxf(v, dpp_src<0x112, 0xf>(v, v));
+  v = fmaxf(v, dpp_src<0x114, 0xf>(v, v));
+  v = fmaxf(v, dpp_src<0x118, 0xf>(v, v));
+  v = fmaxf(v, dpp_src<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp_src<0x143, 0xc>(v, v));
+  return lane63(v);
+}
+
+// Block-wide sum; `red` is kWavesPerBlock floats of LDS. All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) s += red[w];
+  return s;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gelu(float x) {
+  return 0.5f * x * (1.0f + tanhf(0.797885f * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float clipf(float x, float v) { return x < -v ? -v : (x > v ? v : x); }
+
+// 8 fp16 weights (one 16-byte load) dotted with 8 fp32 activations from LDS.
+__device__ __forceinline__ float dot8(u32x4 wbits, const float* xs, float acc) {
+  f16x8 w = __builtin_bit_cast(f16x8, wbits);
+  f32x4 a = *reinterpret_cast<const f32x4*>(xs);
+  f32x4 b = *reinterpret_cast<const f32x4*>(xs + 4);
+  acc = fmaf((float)w[0], a[0], acc);
+  acc = fmaf((float)w[1], a[1], acc);
+  acc = fmaf((float)w[2], a[2], acc);
+  acc = fmaf((float)w[3], a[3], acc);
+  acc = fmaf((float)w[4], b[0], acc);
+  acc = fmaf((float)w[5], b[1], acc);
+  acc = fmaf((float)w[6], b[2], acc);
+  acc = fmaf((float)w[7], b[3], acc);
+  return acc;
+}
+
+// ------------------------------------------------------------------------------------------
+// Fused matvec family.
+//
+// A "group" is R weight rows that one wavefront streams together. Groups are dealt to waves
+// round-robin over the grid. The input vector (K fp32) is staged once per workgroup into LDS,
+// optionally RMS-normalised on the way (reference src/infer.cpp:136-146). The first group's
+// weight loads are issued before the staging so that HBM latency overlaps the staging.
+// ------------------------------------------------------------------------------------------
+enum EpiKind : int {
+  kEpiStore = 0,    // out[row] = acc
+  kEpiResidual = 1, // out[row] += acc            (x += W v)
+  kEpiSwiGLU = 2,   // out[p] = act(acc0) * acc1   (rows p of W1 and W3)
+  kEpiQkvRope = 3,  // q / K-cache / V-cache with clip and RoPE on row pairs
+};
+
+struct MatvecArgs {
+  const uint16_t* w0;  // group p, row r: w0 + p*row_step + r*r_step   (or w1 for r==1 in SwiGLU)
+  const uint16_t* w1;
+  long row_step, r_step;
+  int groups;  // number of groups
+  int K;       // row length (elements), multiple of 8
+  const float* x;      // input vector [K]
+  const float* gain;   // rmsnorm gain [K] or nullptr (no norm)
+  float eps;
+  float* out;
+  int act;  // 1 silu, 0 gelu (SwiGLU epilogue)
+  // QKV epilogue
+  int q_dim, kv_dim, head_dim, rotary_dim, msl;
+  float rope_theta, qkv_clip;
+  uint16_t* kcache;
+  uint16_t* vcache;
+  const StepParams* params;
+  // norm statistics written by the kernel for the host-side debug reader (unused otherwise)
+};
+
+// Loads of one row segment for this lane: chunk c = lane + 64*u, u < KC (KC = K/512 when > 0).
+template <int KC, int R>
+__device__ __forceinline__ void load_group(u32x4 (&wv)[R][KC > 0 ? KC : 1], const uint16_t* const (&rows)[R], int lane) {
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int u = 0; u < KC; ++u)
+      wv[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[r]) + lane + kWave * u);
+}
+
+template <int R>
+__device__ __forceinline__ void group_rows(const MatvecArgs& a, int p, const uint16_t* (&rows)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint16_t* base = (r == 1 && a.w1) ? a.w1 : a.w0;
+    long off = (long)p * a.row_step + ((r == 1 && a.w1) ? 0 : (long)r * a.r_step);
+    rows[r] = base + off;
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void epilogue(const MatvecArgs& a, int kind, int p, const float (&acc)[R]) {
+  if (kind == kEpiStore) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
+  } else if (kind == kEpiResidual) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) a.out[(long)p * R + r] += acc[r];
+  } else if (kind == kEpiSwiGLU) {
+    float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
+    a.out[p] = h * acc[R - 1];
+  } else {  // kEpiQkvRope: rows i = 2p, 2p+1 of [Wq; Wk; Wv]  (reference src/infer.cpp:279-305)
+    const int i = 2 * p;
+    float v0 = clipf(acc[0], a.qkv_clip);
+    float v1 = clipf(acc[R - 1], a.qkv_clip);
+    const int pos = a.params->pos;
+    if (i < a.q_dim + a.kv_dim) {  // RoPE on q and k (reference src/infer.cpp:202-215)
+      const int j = i % a.head_dim;
+      const float freq = j >= a.rotary_dim ? 0.f : 1.0f / powf(a.rope_theta, (float)j / (float)a.rotary_dim);
+      const float ang = (float)pos * freq;
+      const float c = cosf(ang), s = sinf(ang);
+      const float r0 = v0 * c - v1 * s;
+      const float r1 = v0 * s + v1 * c;
+      v0 = r0;
+      v1 = r1;
+    }
+    if (i < a.q_dim) {
+      a.out[i] = v0;
+      a.out[i + 1] = v1;
+    } else {
+      const Positions ps = positions(pos, a.msl);
+      const bool is_k = i < a.q_dim + a.kv_dim;
+      const int ik = i - a.q_dim - (is_k ? 0 : a.kv_dim);
+      const int g = ik / a.head_dim, j = ik % a.head_dim;
+      const long head = (long)g * a.head_dim * a.msl;
+      const f16 h0 = (f16)v0, h1 = (f16)v1;  // RNE, as _cvtss_sh(x, 0)
+      if (is_k) {
+        a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = __builtin_bit_cast(uint16_t, h0);
+        a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = __builtin_bit_cast(uint16_t, h1);
+      } else {
+        a.vcache[head + (long)j * a.msl + ps.kv_pos] = __builtin_bit_cast(uint16_t, h0);
+        a.vcache[head + (long)(j + 1) * a.msl + ps.kv_pos] = __builtin_bit_cast(uint16_t, h1);
+      }
+    }
+  }
+}
+
+// Stage the (optionally RMS-normalised) input vector into LDS: xs[i] = x[i] * inv * g[i] with
+// inv = 1/sqrt(mean(x^2) + eps) (reference src/infer.cpp:136-146). NPT > 0: K == 1024*NPT/... i.e.
+// exactly NPT float4 per thread, all loads issued before the first use; NPT == 0: any K % 4 == 0.
+template <int NPT>
+__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red) {
+  const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
+  const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
+  f32x4* o4 = reinterpret_cast<f32x4*>(xs);
+  if constexpr (NPT > 0) {
+    f32x4 xv[NPT], gv[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
+    if (a.gain) {
+#pragma unroll
+      for (int k = 0; k < NPT; ++k) gv[k] = g4[threadIdx.x + kBlock * k];
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < NPT; ++k)
+        ss += xv[k][0] * xv[k][0] + xv[k][1] * xv[k][1] + xv[k][2] * xv[k][2] + xv[k][3] * xv[k][3];
+      ss = block_sum(ss, red);
+      const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+#pragma unroll
+      for (int k = 0; k < NPT; ++k) {
+        f32x4 o;
+        o[0] = xv[k][0] * inv * gv[k][0];
+        o[1] = xv[k][1] * inv * gv[k][1];
+        o[2] = xv[k][2] * inv * gv[k][2];
+        o[3] = xv[k][3] * inv * gv[k][3];
+        o4[threadIdx.x + kBlock * k] = o;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NPT; ++k) o4[threadIdx.x + kBlock * k] = xv[k];
+    }
+  } else {
+    const int n4 = a.K >> 2;
+    if (a.gain) {
+      float ss = 0.f;
+      for (int i = threadIdx.x; i < n4; i += kBlock) {
+        f32x4 v = x4[i];
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      }
+      ss = block_sum(ss, red);
+      const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      for (int i = threadIdx.x; i < n4; i += kBlock) {
+        f32x4 v = x4[i], g = g4[i];
+        f32x4 o;
+        o[0] = v[0] * inv * g[0];
+        o[1] = v[1] * inv * g[1];
+        o[2] = v[2] * inv * g[2];
+        o[3] = v[3] * inv * g[3];
+        o4[i] = o;
+      }
+    } else {
+      for (int i = threadIdx.x; i < n4; i += kBlock) o4[i] = x4[i];
+    }
+  }
+  __syncthreads();
+}
+
+// KC > 0: K == 512*KC, fully unrolled row streaming. KC == 0: any K % 8 == 0.
+// One register buffer of weights per wave; latency is hidden by the other resident waves and by
+// issuing the next group's loads ahead of the current group's reductions and epilogue.
+template <int KC, int R>
+__global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a, int kind) {
+  extern __shared__ float lds[];
+  float* red = lds;      // kWavesPerBlock floats (padded to 16)
+  float* xs = lds + 16;  // K floats
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wave_stride = gridDim.x * kWavesPerBlock;
+  int p = blockIdx.x * kWavesPerBlock + wave;
+
+  if constexpr (KC > 0) {
+    // Single load site (one register buffer). The first iteration's loads are in flight while the
+    // workgroup stages x; waves without work still take part in the staging barrier.
+    u32x4 wv[R][KC];
+    bool staged = false;
+    for (;;) {
+      if (p < a.groups) {
+        const uint16_t* rows[R];
+        group_rows<R>(a, p, rows);
+        load_group<KC, R>(wv, rows, lane);
+      }
+      if (!staged) {
+        stage_input<KC / 2>(a, xs, red);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+        staged = true;
+      }
+      if (p >= a.groups) break;
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int u = 0; u < KC; ++u) {
+        // one 8-float slice of x serves all R rows; a scheduling fence every 4 slices bounds how
+        // many LDS reads the compiler hoists (each hoisted slice costs 8 VGPRs)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8(wv[r][u], xs + 8 * (lane + kWave * u), acc[r]);
+        if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+      if (lane == 0) epilogue<R>(a, kind, p, acc);
+      p += wave_stride;
+    }
+  } else {
+    stage_input<0>(a, xs, red);
+    const int nch = a.K >> 3;
+    for (; p < a.groups; p += wave_stride) {
+      const uint16_t* rows[R];
+      group_rows<R>(a, p, rows);
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+      for (int c = lane; c < nch; c += kWave) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[r]) + c);
+          acc[r] = dot8(w, xs + 8 * c, acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+      if (lane == 0) epilogue<R>(a, kind, p, acc);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Embedding gather (reference src/infer.cpp:460-481): x[i] = f32(E[token*dim + i]), exact.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* emb, float* x, int dim, const StepParams* params) {
+  const long base = (long)params->token * dim;
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < dim; i += gridDim.x * kBlock)
+    x[i] = (float)__builtin_bit_cast(f16, emb[base + i]);
+}
+
+// ------------------------------------------------------------------------------------------
+// Split-KV GQA decode attention (reference src/infer.cpp:218-250, 327-336).
+//
+// Workgroup (g, s) handles kv head g and the s-th slice of [0, kv_len) for all G query heads
+// that share g, so each K/V byte is read once per token. Scores for a 256-token tile go to LDS;
+// an online softmax keeps (max, sum, acc) per head. The last workgroup to finish for head g
+// (atomic ticket) merges the slices and writes out[h][0..hd).
+// Work split: chunk = roundup(ceil(kv_len / nsplit), 64) tokens per slice.
+// In sink mode (pos >= msl) slice 0 first re-rotates the two sink keys by one position
+// (reference src/infer.cpp:307-325).
+// ------------------------------------------------------------------------------------------
+struct AttnArgs {
+  const float* q;        // [nh][hd]
+  uint16_t* kcache;      // layer base
+  const uint16_t* vcache;
+  float* partial;        // [nh][nsplit][hd + 2]
+  unsigned* tickets;     // [nkv]
+  float* out;            // [nh][hd]
+  int head_dim, n_heads, n_kv_heads, msl, nsplit, rotary_dim;
+  float rope_theta;
+  const StepParams* params;
+};
+
+constexpr int kAttnTile = 256;
+constexpr int kMaxGroup = 8;
+
+__global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
+  __shared__ float qs[kMaxGroup * 128];
+  __shared__ float sc[kMaxGroup][kAttnTile];
+  __shared__ float red[kMaxGroup][kWavesPerBlock];
+  __shared__ float accs[kMaxGroup * 256];
+  __shared__ unsigned last_flag;
+
+  const int g = blockIdx.x, split = blockIdx.y;
+  const int hd = a.head_dim;
+  const int G = a.n_heads / a.n_kv_heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const Positions ps = positions(a.params->pos, a.msl);
+  const int kv_len = ps.kv_len;
+  int chunk = (kv_len + a.nsplit - 1) / a.nsplit;
+  chunk = (chunk + 63) & ~63;
+  const int t_begin = split * chunk;
+  const int t_end = min(kv_len, t_begin + chunk);
+  const long head_off = (long)g * hd * a.msl;
+  uint16_t* kh = a.kcache + head_off;
+  const uint16_t* vh = a.vcache + head_off;
+
+  if (ps.kv_sink > 0 && split == 0) {
+    // Re-rotate sink keys r < kv_sink by angle freq*1 in place (fp16 round trip as reference).
+    for (int e = tid; e < ps.kv_sink * (hd / 2); e += kBlock) {
+      const int r = e / (hd / 2);
+      const int j = 2 * (e % (hd / 2));
+      const float freq = j >= a.rotary_dim ? 0.f : 1.0f / powf(a.rope_theta, (float)j / (float)a.rotary_dim);
+      const float c = cosf(freq), s = sinf(freq);
+      uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
+      uint16_t* p1 = kh + k_cache_idx(j + 1, r, a.msl);
+      const float v0 = (float)__builtin_bit_cast(f16, *p0), v1 = (float)__builtin_bit_cast(f16, *p1);
+      *p0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
+      *p1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
+    }
+    __threadfence_block();
+    __syncthreads();
+  }
+
+  for (int e = tid; e < G * hd; e += kBlock) qs[e] = a.q[(long)g * G * hd + e];
+  float m_run[kMaxGroup], l_run[kMaxGroup];
+#pragma unroll
+  for (int h = 0; h < kMaxGroup; ++h) {
+    m_run[h] = kNegBig;
+    l_run[h] = 0.f;
+  }
+  // V phase mapping: thread owns dim i = tid % hd, token part tid / hd.
+  const int parts = kBlock / hd;
+  const int i_dim = tid % hd;
+  const int part = tid / hd;
+  const int tpp = kAttnTile / parts;  // tokens per part per tile
+  float acc[kMaxGroup];
+#pragma unroll
+  for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.f;
+  const float inv_sqrt = 1.0f / sqrtf((float)hd);
+  const bool vec_ok = (a.msl & 7) == 0;
+  __syncthreads();
+
+  for (int t0 = t_begin; t0 < t_end; t0 += kAttnTile) {
+    // scores
+    const int tok = t0 + tid;
+    float s[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) s[h] = 0.f;
+    if (tok < t_end) {
+      for (int c = 0; c < hd / 16; ++c) {
+        const u32x4* kp = reinterpret_cast<const u32x4*>(kh + (long)c * 16 * a.msl + (long)tok * 16);
+        const f16x8 k0 = __builtin_bit_cast(f16x8, kp[0]);
+        const f16x8 k1 = __builtin_bit_cast(f16x8, kp[1]);
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; ++h) {
+          if (h < G) {
+            const float* qh = qs + h * hd + c * 16;
+            float d = s[h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d = fmaf(qh[e], (float)k0[e], d);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d = fmaf(qh[8 + e], (float)k1[e], d);
+            s[h] = d;
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; ++h) s[h] = s[h] / sqrtf((float)hd);
+    } else {
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; ++h) s[h] = kNegBig;
+    }
+    (void)inv_sqrt;
+    // tile max per head
+    float corr[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (h < G) {
+        float m = wave_max(s[h]);
+        if (lane == 0) red[h][wave] = m;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (h < G) {
+        float m = red[h][0];
+#pragma unroll
+        for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, red[h][w]);
+        const float m_new = fmaxf(m_run[h], m);
+        corr[h] = expf(m_run[h] - m_new);
+        m_run[h] = m_new;
+        const float p = tok < t_end ? expf(s[h] - m_new) : 0.f;
+        sc[h][tid] = p;
+        s[h] = p;
+      }
+    }
+    __syncthreads();  // red reused below; sc complete
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (h < G) {
+        float ps_ = wave_sum(s[h]);
+        if (lane == 0) red[h][wave] = ps_;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (h < G) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) t += red[h][w];
+        l_run[h] = l_run[h] * corr[h] + t;
+        acc[h] *= corr[h];
+      }
+    }
+    // V accumulation over this part's tokens
+    const int tb = t0 + part * tpp;
+    const int te = min(t_end, tb + tpp);
+    const uint16_t* vrow = vh + (long)i_dim * a.msl;
+    int t = tb;
+    if (vec_ok) {
+      for (; t + 8 <= te; t += 8) {
+        const f16x8 v8 = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(vrow + t));
+        const int k = t - t0;
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; ++h) {
+          if (h < G) {
+            float d = acc[h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d = fmaf(sc[h][k + e], (float)v8[e], d);
+            acc[h] = d;
+          }
+        }
+      }
+    }
+    for (; t < te; ++t) {
+      const float v = (float)__builtin_bit_cast(f16, vrow[t]);
+      const int k = t - t0;
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; ++h)
+        if (h < G) acc[h] = fmaf(sc[h][k], v, acc[h]);
+    }
+    __syncthreads();  // sc / red reused by the next tile
+  }
+
+  // Merge the token parts of this workgroup, then publish the slice partial.
+  for (int h = 0; h < G; ++h) accs[h * 256 + tid] = acc[h];
+  __syncthreads();
+  const int stride = hd + 2;
+  for (int e = tid; e < G * hd; e += kBlock) {
+    const int h = e / hd, i = e % hd;
+    float o = 0.f;
+    for (int pt = 0; pt < parts; ++pt) o += accs[h * 256 + pt * hd + i];
+    float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
+    dst[i] = o;
+    if (i == 0) {
+      dst[hd] = m_run[h];
+      dst[hd + 1] = l_run[h];
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned t = atomicAdd(&a.tickets[g], 1u);
+    last_flag = (t == (unsigned)(gridDim.y - 1)) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  for (int e = tid; e < G * hd; e += kBlock) {
+    const int h = e / hd, i = e % hd;
+    const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride;
+    float M = kNegBig;
+    for (int sp = 0; sp < a.nsplit; ++sp) M = fmaxf(M, __builtin_nontemporal_load(src + sp * stride + hd));
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+      const float* ps_ = src + sp * stride;
+      const float w = expf(__builtin_nontemporal_load(ps_ + hd) - M);
+      L = fmaf(__builtin_nontemporal_load(ps_ + hd + 1), w, L);
+      O = fmaf(__builtin_nontemporal_load(ps_ + i), w, O);
+    }
+    a.out[(long)(g * G + h) * hd + i] = O / L;
+  }
+  if (tid == 0) atomicExch(&a.tickets[g], 0u);
+}
+
+// ------------------------------------------------------------------------------------------
+// Greedy argmax over logits with the reference tie rule (first index of the strict maximum,
+// src/sampler.cpp:27-38). One workgroup.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(kBlock) argmax_kernel(const float* logits, int n, int* out) {
+  __shared__ float bv[kBlock];
+  __shared__ int bi[kBlock];
+  float best = kNegBig;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += kBlock) {
+    const float v = logits[i];
+    if (v > best) {  // increasing i per thread: keeps the first index of this thread's maximum
+      best = v;
+      idx = i;
+    }
+  }
+  bv[threadIdx.x] = best;
+  bi[threadIdx.x] = idx;
+  __syncthreads();
+  for (int s = kBlock / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      const float ov = bv[threadIdx.x + s];
+      const int oi = bi[threadIdx.x + s];
+      if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
+        bv[threadIdx.x] = ov;
+        bi[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = bi[0] == 0x7fffffff ? 0 : bi[0];
+}
+
+}  // namespace yk

@@ -1,0 +1,872 @@
+// libyalm_hip.so: the C-ABI in include/yalm_hip.h over the gfx950 kernels in kernels.h.
+//
+// One decode step (reference src/infer.cu:1274-1378 in structure, src/infer.cpp:483-527 in
+// semantics) is enqueued as:
+//   embed -> 32 x [ rmsnorm+QKV+RoPE+KV-write | split-KV attention (+merge) | O-proj+residual |
+//                   rmsnorm+W1/W3+SwiGLU | W2+residual ] -> rmsnorm+lm_head [-> argmax]
+// Token and position live in a device-side parameter block written by a one-thread kernel
+// before each step, so the whole step is captured once per mode into a hipGraph and replayed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/yalm_hip.h"
+#include "kernels.h"
+
+using namespace yk;
+
+namespace {
+
+thread_local std::string g_thread_err;
+
+struct LayerW {
+  uint16_t* wqkv = nullptr;  // [q_dim + 2*kv_dim][dim]
+  uint16_t* wo = nullptr;    // [dim][q_dim]
+  uint16_t* w1 = nullptr;    // [hidden][dim]
+  uint16_t* w3 = nullptr;    // [hidden][dim]
+  uint16_t* w2 = nullptr;    // [dim][hidden]
+  float* rms_att = nullptr;
+  float* rms_ffn = nullptr;
+  bool loaded = false;
+};
+
+__global__ void set_params_kernel(StepParams* p, int token, int pos) {
+  p->token = token;
+  p->pos = pos;
+}
+
+}  // namespace
+
+struct yhip_ctx {
+  yhip_config c{};
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t stream = nullptr;
+  std::string err;
+
+  char* wbase = nullptr;
+  size_t wbytes = 0;
+  std::vector<LayerW> layers;
+  uint16_t* embed = nullptr;
+  float* rms_final = nullptr;
+  uint16_t* wcls = nullptr;
+  bool globals_loaded = false;
+
+  uint16_t* kv = nullptr;  // layer l: K at kv + 2*l*kv_elems, V at kv + (2*l+1)*kv_elems
+  size_t kv_elems = 0;
+
+  char* abase = nullptr;  // activations
+  float* x = nullptr;
+  float* q = nullptr;
+  float* att = nullptr;
+  float* hb = nullptr;
+  float* logits = nullptr;
+  float* partial = nullptr;
+  unsigned* tickets = nullptr;
+  int* argmax_dev = nullptr;
+  StepParams* params = nullptr;
+
+  float* logits_host = nullptr;  // pinned
+  int* argmax_host = nullptr;    // pinned
+
+  bool use_graph = true;
+  int attn_splits = 32;
+  hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // hydrate, logits, argmax
+
+  int q_dim() const { return c.n_heads * c.head_dim; }
+  int kv_dim() const { return c.n_kv_heads * c.head_dim; }
+  uint16_t* kcache(int l) const { return kv + (size_t)2 * l * kv_elems; }
+  uint16_t* vcache(int l) const { return kv + (size_t)(2 * l + 1) * kv_elems; }
+};
+
+namespace {
+
+int fail(yhip_ctx* ctx, int code, const std::string& msg) {
+  if (ctx)
+    ctx->err = msg;
+  else
+    g_thread_err = msg;
+  return code;
+}
+
+#define HIP_TRY(ctx, expr)                                                                           \
+  do {                                                                                               \
+    hipError_t e_ = (expr);                                                                          \
+    if (e_ != hipSuccess)                                                                            \
+      return fail(ctx, YHIP_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));             \
+  } while (0)
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- matvec launch -------------------------------------------------------------------------
+int max_blocks_for(int num_cus) { return num_cus * 4; }
+
+template <int KC, int R>
+void launch_mv(const MatvecArgs& a, int kind, int blocks, hipStream_t s) {
+  const size_t lds = (16 + (size_t)a.K) * sizeof(float);
+  hipLaunchKernelGGL((matvec_kernel<KC, R>), dim3(blocks), dim3(kBlock), lds, s, a, kind);
+}
+
+// Chooses the instantiation for row length K and rows-per-group R.
+int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s) {
+  if (a.K % 8 != 0 || (16 + (size_t)a.K) * sizeof(float) > 65536)
+    return fail(ctx, YHIP_EINVAL, "matvec: row length must be a multiple of 8 and at most 16368");
+  int waves_needed = a.groups;
+  int blocks = (waves_needed + kWavesPerBlock - 1) / kWavesPerBlock;
+  blocks = std::max(1, std::min(blocks, max_blocks_for(num_cus)));
+  if (R == 1) {
+    if (a.K == 4096) launch_mv<8, 1>(a, kind, blocks, s);
+    else if (a.K == 14336) launch_mv<28, 1>(a, kind, blocks, s);
+    else launch_mv<0, 1>(a, kind, blocks, s);
+  } else if (R == 2) {
+    if (a.K == 4096) launch_mv<8, 2>(a, kind, blocks, s);
+    else launch_mv<0, 2>(a, kind, blocks, s);
+  } else {
+    return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("matvec launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
+MatvecArgs mv_base() {
+  MatvecArgs a;
+  memset(&a, 0, sizeof(a));
+  a.qkv_clip = 3.402823466e38f;
+  return a;
+}
+
+int launch_attention(yhip_ctx* ctx, const AttnArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(attention_kernel, dim3(a.n_kv_heads, a.nsplit), dim3(kBlock), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
+int check_attn_shape(yhip_ctx* ctx, int hd, int nh, int nkv) {
+  if (!(hd == 16 || hd == 32 || hd == 64 || hd == 128))
+    return fail(ctx, YHIP_EINVAL, "head_dim must be 16, 32, 64 or 128");
+  if (nkv <= 0 || nkv > 64 || nh % nkv != 0 || nh / nkv > kMaxGroup)
+    return fail(ctx, YHIP_EINVAL, "n_heads must be a multiple of n_kv_heads (at most 64) with at most 8 query heads per kv head");
+  return YHIP_OK;
+}
+
+// ---- one decode step ------------------------------------------------------------------------
+// mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
+int enqueue_step(yhip_ctx* ctx, int mode) {
+  const yhip_config& c = ctx->c;
+  hipStream_t s = ctx->stream;
+  const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
+  hipLaunchKernelGGL(embed_kernel, dim3((c.dim + kBlock - 1) / kBlock), dim3(kBlock), 0, s, ctx->embed, ctx->x,
+                     c.dim, (const StepParams*)ctx->params);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& L = ctx->layers[l];
+    int rc;
+    // 1. rmsnorm + QKV + clip + RoPE + KV write
+    MatvecArgs a = mv_base();
+    a.w0 = L.wqkv;
+    a.row_step = 2L * c.dim;
+    a.r_step = c.dim;
+    a.groups = (qd + 2 * kvd) / 2;
+    a.K = c.dim;
+    a.x = ctx->x;
+    a.gain = L.rms_att;
+    a.eps = c.norm_eps;
+    a.out = ctx->q;
+    a.q_dim = qd;
+    a.kv_dim = kvd;
+    a.head_dim = c.head_dim;
+    a.rotary_dim = c.rotary_dim;
+    a.msl = c.max_seq_len;
+    a.rope_theta = c.rope_theta;
+    a.qkv_clip = c.qkv_clip;
+    a.kcache = ctx->kcache(l);
+    a.vcache = ctx->vcache(l);
+    a.params = ctx->params;
+    if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s))) return rc;
+    // 2. attention
+    AttnArgs t;
+    t.q = ctx->q;
+    t.kcache = ctx->kcache(l);
+    t.vcache = ctx->vcache(l);
+    t.partial = ctx->partial;
+    t.tickets = ctx->tickets;
+    t.out = ctx->att;
+    t.head_dim = c.head_dim;
+    t.n_heads = c.n_heads;
+    t.n_kv_heads = c.n_kv_heads;
+    t.msl = c.max_seq_len;
+    t.nsplit = ctx->attn_splits;
+    t.rotary_dim = c.rotary_dim;
+    t.rope_theta = c.rope_theta;
+    t.params = ctx->params;
+    if ((rc = launch_attention(ctx, t, s))) return rc;
+    // 3. O-proj + residual
+    a = mv_base();
+    a.w0 = L.wo;
+    a.row_step = 2L * qd;
+    a.r_step = qd;
+    a.groups = c.dim / 2;
+    a.K = qd;
+    a.x = ctx->att;
+    a.out = ctx->x;
+    if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s))) return rc;
+    // 4. rmsnorm + W1/W3 + SwiGLU
+    a = mv_base();
+    a.w0 = L.w1;
+    a.w1 = L.w3;
+    a.row_step = c.dim;
+    a.groups = c.hidden_dim;
+    a.K = c.dim;
+    a.x = ctx->x;
+    a.gain = L.rms_ffn;
+    a.eps = c.norm_eps;
+    a.out = ctx->hb;
+    a.act = c.act;
+    if ((rc = launch_matvec(ctx, a, kEpiSwiGLU, 2, ctx->num_cus, s))) return rc;
+    // 5. W2 + residual
+    a = mv_base();
+    a.w0 = L.w2;
+    a.row_step = c.hidden_dim;
+    a.r_step = c.hidden_dim;
+    a.groups = c.dim;
+    a.K = c.hidden_dim;
+    a.x = ctx->hb;
+    a.out = ctx->x;
+    if ((rc = launch_matvec(ctx, a, kEpiResidual, 1, ctx->num_cus, s))) return rc;
+  }
+  if (mode == 0) return YHIP_OK;
+  const int Rc = (c.vocab_size % 2 == 0) ? 2 : 1;
+  MatvecArgs a = mv_base();
+  a.w0 = ctx->wcls;
+  a.row_step = (long)Rc * c.dim;
+  a.r_step = c.dim;
+  a.groups = c.vocab_size / Rc;
+  a.K = c.dim;
+  a.x = ctx->x;
+  a.gain = ctx->rms_final;
+  a.eps = c.norm_eps;
+  a.out = ctx->logits;
+  if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s)) return rc;
+  if (mode == 1) {
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
+                                hipMemcpyDeviceToHost, s));
+  } else {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kBlock), 0, s, (const float*)ctx->logits, c.vocab_size,
+                       ctx->argmax_dev);
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, s));
+  }
+  return YHIP_OK;
+}
+
+void drop_graphs(yhip_ctx* ctx) {
+  for (auto& g : ctx->graph) {
+    if (g) hipGraphExecDestroy(g);
+    g = nullptr;
+  }
+}
+
+int run_step(yhip_ctx* ctx, int token, int pos, int mode) {
+  const yhip_config& c = ctx->c;
+  if (token < 0 || token >= c.vocab_size) return fail(ctx, YHIP_EINVAL, "token id out of range");
+  if (pos < 0) return fail(ctx, YHIP_EINVAL, "negative position");
+  if (!ctx->globals_loaded) return fail(ctx, YHIP_ESTATE, "globals not uploaded");
+  for (int l = 0; l < c.n_layers; ++l)
+    if (!ctx->layers[l].loaded) return fail(ctx, YHIP_ESTATE, "layer " + std::to_string(l) + " not uploaded");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(1), 0, ctx->stream, ctx->params, token, pos);
+  HIP_TRY(ctx, hipGetLastError());
+  if (!ctx->use_graph) return enqueue_step(ctx, mode);
+  if (!ctx->graph[mode]) {
+    hipGraph_t g = nullptr;
+    HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(ctx, mode);
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (rc) {
+      if (g) hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&ctx->graph[mode], g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      ctx->graph[mode] = nullptr;
+      return fail(ctx, YHIP_EDEVICE, std::string("graph instantiate: ") + hipGetErrorString(e));
+    }
+  }
+  HIP_TRY(ctx, hipGraphLaunch(ctx->graph[mode], ctx->stream));
+  return YHIP_OK;
+}
+
+}  // namespace
+
+// ============================================================================================
+// C-ABI
+// ============================================================================================
+extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx** out) {
+  if (!cfg || !out) return fail(nullptr, YHIP_EINVAL, "null argument");
+  *out = nullptr;
+  const yhip_config& c = *cfg;
+  if (c.dim <= 0 || c.hidden_dim <= 0 || c.n_layers < 0 || c.vocab_size <= 0 || c.max_seq_len <= kKvSinks ||
+      c.rotary_dim < 0 || c.rotary_dim > c.head_dim)
+    return fail(nullptr, YHIP_EINVAL, "invalid config dimensions");
+  if (c.dim % 8 || c.hidden_dim % 8 || (c.n_heads * c.head_dim) % 8)
+    return fail(nullptr, YHIP_EINVAL, "dim, hidden_dim and n_heads*head_dim must be multiples of 8");
+  if (c.dim > 16368 || c.hidden_dim > 16368 || c.n_heads * c.head_dim > 16368)
+    return fail(nullptr, YHIP_EINVAL, "row lengths above 16368 are not supported");
+  if (c.act != YHIP_ACT_GELU && c.act != YHIP_ACT_SILU) return fail(nullptr, YHIP_EINVAL, "unknown activation");
+  if (int rc = check_attn_shape(nullptr, c.head_dim, c.n_heads, c.n_kv_heads)) return rc;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device_ordinal < 0 || device_ordinal >= ndev)
+    return fail(nullptr, YHIP_EDEVICE, "no such HIP device");
+  yhip_ctx* ctx = new yhip_ctx();
+  ctx->c = c;
+  ctx->device = device_ordinal;
+  ctx->attn_splits = std::max(1, std::min(64, 256 / std::max(1, c.n_kv_heads)));
+  auto bail = [&](int rc) {
+    yhip_destroy(ctx);
+    return rc;
+  };
+  if (hipSetDevice(device_ordinal) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "hipSetDevice failed"));
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device_ordinal) == hipSuccess && prop.multiProcessorCount > 0)
+    ctx->num_cus = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(nullptr, YHIP_EDEVICE, "stream create failed"));
+
+  // Weights: one allocation, 256-byte aligned sub-buffers.
+  const size_t dim = c.dim, hid = c.hidden_dim, qd = ctx->q_dim(), kvd = ctx->kv_dim(), V = c.vocab_size;
+  size_t per_layer = 0;
+  auto take = [&](size_t bytes) {
+    size_t off = per_layer;
+    per_layer = align_up(per_layer + bytes, 256);
+    return off;
+  };
+  const size_t o_qkv = take((qd + 2 * kvd) * dim * 2), o_wo = take(dim * qd * 2), o_w1 = take(hid * dim * 2),
+               o_w3 = take(hid * dim * 2), o_w2 = take(dim * hid * 2), o_ra = take(dim * 4), o_rf = take(dim * 4);
+  const size_t g_emb = align_up(V * dim * 2, 256), g_cls = align_up(V * dim * 2, 256), g_rf = align_up(dim * 4, 256);
+  ctx->wbytes = per_layer * c.n_layers + g_emb + g_cls + g_rf;
+  if (hipMalloc(&ctx->wbase, ctx->wbytes) != hipSuccess)
+    return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory for weights"));
+  ctx->layers.resize(c.n_layers);
+  for (int l = 0; l < c.n_layers; ++l) {
+    char* b = ctx->wbase + per_layer * l;
+    LayerW& L = ctx->layers[l];
+    L.wqkv = (uint16_t*)(b + o_qkv);
+    L.wo = (uint16_t*)(b + o_wo);
+    L.w1 = (uint16_t*)(b + o_w1);
+    L.w3 = (uint16_t*)(b + o_w3);
+    L.w2 = (uint16_t*)(b + o_w2);
+    L.rms_att = (float*)(b + o_ra);
+    L.rms_ffn = (float*)(b + o_rf);
+  }
+  char* gb = ctx->wbase + per_layer * c.n_layers;
+  ctx->embed = (uint16_t*)gb;
+  ctx->wcls = (uint16_t*)(gb + g_emb);
+  ctx->rms_final = (float*)(gb + g_emb + g_cls);
+
+  // KV caches, zeroed (reference src/model.cpp:203-204).
+  ctx->kv_elems = (size_t)c.n_kv_heads * c.head_dim * c.max_seq_len;
+  const size_t kv_bytes = ctx->kv_elems * 2 * 2 * std::max(1, c.n_layers);
+  if (hipMalloc(&ctx->kv, kv_bytes) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory for KV"));
+  if (hipMemset(ctx->kv, 0, kv_bytes) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "KV memset failed"));
+
+  // Activations.
+  size_t ab = 0;
+  auto atake = [&](size_t bytes) {
+    size_t off = ab;
+    ab = align_up(ab + bytes, 256);
+    return off;
+  };
+  const size_t a_x = atake(dim * 4), a_q = atake(qd * 4), a_att = atake(qd * 4), a_hb = atake(hid * 4),
+               a_lg = atake(V * 4), a_part = atake((size_t)c.n_heads * 64 * (c.head_dim + 2) * 4),
+               a_tk = atake(64 * 4), a_am = atake(64), a_par = atake(sizeof(StepParams));
+  if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
+  if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
+  ctx->x = (float*)(ctx->abase + a_x);
+  ctx->q = (float*)(ctx->abase + a_q);
+  ctx->att = (float*)(ctx->abase + a_att);
+  ctx->hb = (float*)(ctx->abase + a_hb);
+  ctx->logits = (float*)(ctx->abase + a_lg);
+  ctx->partial = (float*)(ctx->abase + a_part);
+  ctx->tickets = (unsigned*)(ctx->abase + a_tk);
+  ctx->argmax_dev = (int*)(ctx->abase + a_am);
+  ctx->params = (StepParams*)(ctx->abase + a_par);
+  if (hipHostMalloc((void**)&ctx->logits_host, V * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&ctx->argmax_host, 64, hipHostMallocDefault) != hipSuccess)
+    return bail(fail(nullptr, YHIP_EDEVICE, "pinned host allocation failed"));
+  *out = ctx;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_destroy(yhip_ctx* ctx) {
+  if (!ctx) return YHIP_OK;
+  hipSetDevice(ctx->device);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  drop_graphs(ctx);
+  if (ctx->wbase) hipFree(ctx->wbase);
+  if (ctx->kv) hipFree(ctx->kv);
+  if (ctx->abase) hipFree(ctx->abase);
+  if (ctx->logits_host) hipHostFree(ctx->logits_host);
+  if (ctx->argmax_host) hipHostFree(ctx->argmax_host);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_upload_layer(yhip_ctx* ctx, int layer, const float* rms_att, const float* rms_ffn,
+                                 const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, const uint16_t* wo,
+                                 const uint16_t* w1, const uint16_t* w2, const uint16_t* w3) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (layer < 0 || layer >= ctx->c.n_layers) return fail(ctx, YHIP_EINVAL, "layer index out of range");
+  if (!rms_att || !rms_ffn || !wq || !wk || !wv || !wo || !w1 || !w2 || !w3)
+    return fail(ctx, YHIP_EINVAL, "null weight pointer");
+  const yhip_config& c = ctx->c;
+  const size_t dim = c.dim, hid = c.hidden_dim, qd = ctx->q_dim(), kvd = ctx->kv_dim();
+  LayerW& L = ctx->layers[layer];
+  hipStream_t s = ctx->stream;
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv, wq, qd * dim * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv + qd * dim, wk, kvd * dim * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv + (qd + kvd) * dim, wv, kvd * dim * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.wo, wo, dim * qd * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.w1, w1, hid * dim * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.w3, w3, hid * dim * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.w2, w2, dim * hid * 2, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.rms_att, rms_att, dim * 4, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipMemcpyAsync(L.rms_ffn, rms_ffn, dim * 4, hipMemcpyHostToDevice, s));
+  HIP_TRY(ctx, hipStreamSynchronize(s));  // host buffers may be released after return
+  L.loaded = true;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_upload_globals(yhip_ctx* ctx, const uint16_t* embed, const float* rms_final, const uint16_t* wcls) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (!embed || !rms_final) return fail(ctx, YHIP_EINVAL, "null weight pointer");
+  const yhip_config& c = ctx->c;
+  const size_t n = (size_t)c.vocab_size * c.dim;
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->embed, embed, n * 2, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->wcls, wcls ? wcls : embed, n * 2, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->rms_final, rms_final, (size_t)c.dim * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->globals_loaded = true;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_forward(yhip_ctx* ctx, int token, int pos, int mode, float* logits_host) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (mode != YHIP_MODE_HYDRATE && mode != YHIP_MODE_LOGITS) return fail(ctx, YHIP_EINVAL, "unknown mode");
+  if (mode == YHIP_MODE_LOGITS && !logits_host) return fail(ctx, YHIP_EINVAL, "null logits buffer");
+  if (int rc = run_step(ctx, token, pos, mode)) return rc;
+  if (mode == YHIP_MODE_HYDRATE) return YHIP_OK;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  if (logits_host != ctx->logits_host) memcpy(logits_host, ctx->logits_host, (size_t)ctx->c.vocab_size * 4);
+  return YHIP_OK;
+}
+
+extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_token) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (!next_token) return fail(ctx, YHIP_EINVAL, "null output");
+  if (int rc = run_step(ctx, token, pos, 2)) return rc;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  *next_token = *ctx->argmax_host;
+  return YHIP_OK;
+}
+
+extern "C" float* yhip_logits_host(yhip_ctx* ctx) { return ctx ? ctx->logits_host : nullptr; }
+
+extern "C" int yhip_kv_read(yhip_ctx* ctx, int layer, uint16_t* k_host, uint16_t* v_host) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (layer < 0 || layer >= ctx->c.n_layers) return fail(ctx, YHIP_EINVAL, "layer index out of range");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  const size_t bytes = ctx->kv_elems * 2;
+  if (k_host) HIP_TRY(ctx, hipMemcpyAsync(k_host, ctx->kcache(layer), bytes, hipMemcpyDeviceToHost, ctx->stream));
+  if (v_host) HIP_TRY(ctx, hipMemcpyAsync(v_host, ctx->vcache(layer), bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16_t* v_host) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (layer < 0 || layer >= ctx->c.n_layers) return fail(ctx, YHIP_EINVAL, "layer index out of range");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  const size_t bytes = ctx->kv_elems * 2;
+  if (k_host) HIP_TRY(ctx, hipMemcpyAsync(ctx->kcache(layer), k_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+  if (v_host) HIP_TRY(ctx, hipMemcpyAsync(ctx->vcache(layer), v_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
+  if (!ctx || !key) return fail(ctx, YHIP_EINVAL, "null argument");
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  if (!strcmp(key, "graph")) {
+    ctx->use_graph = value != 0;
+  } else if (!strcmp(key, "attn_splits")) {
+    if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "attn_splits must be in [1, 64]");
+    ctx->attn_splits = value;
+  } else {
+    return fail(ctx, YHIP_EINVAL, std::string("unknown option ") + key);
+  }
+  drop_graphs(ctx);
+  return YHIP_OK;
+}
+
+extern "C" int yhip_debug_read(yhip_ctx* ctx, int which, float* host, size_t n) {
+  if (!ctx || !host) return fail(ctx, YHIP_EINVAL, "null argument");
+  const yhip_config& c = ctx->c;
+  const float* src = nullptr;
+  size_t cap = 0;
+  switch (which) {
+    case 0: src = ctx->x; cap = c.dim; break;
+    case 1: src = ctx->q; cap = ctx->q_dim(); break;
+    case 2: src = ctx->att; cap = ctx->q_dim(); break;
+    case 3: src = ctx->hb; cap = c.hidden_dim; break;
+    case 4: src = ctx->logits; cap = c.vocab_size; break;
+    default: return fail(ctx, YHIP_EINVAL, "unknown buffer");
+  }
+  if (n > cap) return fail(ctx, YHIP_EINVAL, "read larger than buffer");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  HIP_TRY(ctx, hipMemcpyAsync(host, src, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
+extern "C" const char* yhip_last_error(const yhip_ctx* ctx) { return ctx ? ctx->err.c_str() : g_thread_err.c_str(); }
+
+// ============================================================================================
+// Kernel-level hooks (test only; allocate per call).
+// ============================================================================================
+namespace {
+
+struct DevBufs {
+  std::vector<void*> ptrs;
+  ~DevBufs() {
+    for (void* p : ptrs) hipFree(p);
+  }
+  template <class T>
+  T* alloc(size_t n, const void* init = nullptr) {
+    void* p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    if (init) {
+      if (hipMemcpy(p, init, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    } else {
+      hipMemset(p, 0, std::max<size_t>(n, 1) * sizeof(T));
+    }
+    return (T*)p;
+  }
+};
+
+int device_cus() {
+  int dev = 0;
+  hipGetDevice(&dev);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0) return prop.multiProcessorCount;
+  return 256;
+}
+
+#define TRY_ALLOC(p) \
+  if (!(p)) return fail(nullptr, YHIP_EDEVICE, "device allocation failed")
+
+}  // namespace
+
+extern "C" int yhip_test_matvec(const float* x, const float* gain, float eps, const uint16_t* w, int n, int d,
+                                const float* resid, float* out) {
+  if (!x || !w || !out || n <= 0 || d <= 0) return fail(nullptr, YHIP_EINVAL, "bad argument");
+  DevBufs b;
+  float* dx = b.alloc<float>(n, x);
+  TRY_ALLOC(dx);
+  float* dg = gain ? b.alloc<float>(n, gain) : nullptr;
+  if (gain) TRY_ALLOC(dg);
+  uint16_t* dw = b.alloc<uint16_t>((size_t)n * d, w);
+  TRY_ALLOC(dw);
+  float* dout = b.alloc<float>(d, resid);
+  TRY_ALLOC(dout);
+  MatvecArgs a = mv_base();
+  a.w0 = dw;
+  a.K = n;
+  a.x = dx;
+  a.gain = dg;
+  a.eps = eps;
+  a.out = dout;
+  const int R = (d % 2 == 0) ? 2 : 1;
+  a.row_step = (long)R * n;
+  a.r_step = n;
+  a.groups = d / R;
+  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, R, device_cus(), nullptr)) return rc;
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  HIP_TRY(nullptr, hipMemcpy(out, dout, (size_t)d * 4, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* w1, const uint16_t* w2,
+                             const uint16_t* w3, int hidden_dim, int dim, int act, const float* resid, float* out) {
+  if (!x || !w1 || !w2 || !w3 || !out || hidden_dim <= 0 || dim <= 0) return fail(nullptr, YHIP_EINVAL, "bad argument");
+  DevBufs b;
+  float* dx = b.alloc<float>(dim, x);
+  TRY_ALLOC(dx);
+  float* dg = gain ? b.alloc<float>(dim, gain) : nullptr;
+  if (gain) TRY_ALLOC(dg);
+  uint16_t* d1 = b.alloc<uint16_t>((size_t)hidden_dim * dim, w1);
+  uint16_t* d2 = b.alloc<uint16_t>((size_t)hidden_dim * dim, w2);
+  uint16_t* d3 = b.alloc<uint16_t>((size_t)hidden_dim * dim, w3);
+  float* dh = b.alloc<float>(hidden_dim);
+  float* dout = b.alloc<float>(dim, resid);
+  TRY_ALLOC(d1);
+  TRY_ALLOC(d2);
+  TRY_ALLOC(d3);
+  TRY_ALLOC(dh);
+  TRY_ALLOC(dout);
+  const int cus = device_cus();
+  MatvecArgs a = mv_base();
+  a.w0 = d1;
+  a.w1 = d3;
+  a.row_step = dim;
+  a.groups = hidden_dim;
+  a.K = dim;
+  a.x = dx;
+  a.gain = dg;
+  a.eps = eps;
+  a.out = dh;
+  a.act = act;
+  if (int rc = launch_matvec(nullptr, a, kEpiSwiGLU, 2, cus, nullptr)) return rc;
+  a = mv_base();
+  a.w0 = d2;
+  a.row_step = hidden_dim;
+  a.r_step = hidden_dim;
+  a.groups = dim;
+  a.K = hidden_dim;
+  a.x = dh;
+  a.out = dout;
+  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, 1, cus, nullptr)) return rc;
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  HIP_TRY(nullptr, hipMemcpy(out, dout, (size_t)dim * 4, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
+                                   int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
+                                   int rotary_dim, float* att_out) {
+  if (!q || !kcache || !vcache || !att_out || pos < 0 || max_seq_len <= kKvSinks)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
+  if (nsplit <= 0) nsplit = std::max(1, std::min(64, 256 / n_kv_heads));
+  if (nsplit > 64) return fail(nullptr, YHIP_EINVAL, "nsplit must be at most 64");
+  const size_t kv = (size_t)n_kv_heads * head_dim * max_seq_len;
+  DevBufs b;
+  float* dq = b.alloc<float>((size_t)n_heads * head_dim, q);
+  uint16_t* dk = b.alloc<uint16_t>(kv, kcache);
+  uint16_t* dv = b.alloc<uint16_t>(kv, vcache);
+  float* dpart = b.alloc<float>((size_t)n_heads * nsplit * (head_dim + 2));
+  unsigned* dt = b.alloc<unsigned>(64);
+  float* dout = b.alloc<float>((size_t)n_heads * head_dim);
+  StepParams hp{0, pos, {0, 0}};
+  StepParams* dp = b.alloc<StepParams>(1, &hp);
+  TRY_ALLOC(dq);
+  TRY_ALLOC(dk);
+  TRY_ALLOC(dv);
+  TRY_ALLOC(dpart);
+  TRY_ALLOC(dt);
+  TRY_ALLOC(dout);
+  TRY_ALLOC(dp);
+  AttnArgs t;
+  t.q = dq;
+  t.kcache = dk;
+  t.vcache = dv;
+  t.partial = dpart;
+  t.tickets = dt;
+  t.out = dout;
+  t.head_dim = head_dim;
+  t.n_heads = n_heads;
+  t.n_kv_heads = n_kv_heads;
+  t.msl = max_seq_len;
+  t.nsplit = nsplit;
+  t.rotary_dim = rotary_dim;
+  t.rope_theta = rope_theta;
+  t.params = dp;
+  if (int rc = launch_attention(nullptr, t, nullptr)) return rc;
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  HIP_TRY(nullptr, hipMemcpy(att_out, dout, (size_t)n_heads * head_dim * 4, hipMemcpyDeviceToHost));
+  HIP_TRY(nullptr, hipMemcpy(kcache, dk, kv * 2, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* wq, const uint16_t* wk,
+                             const uint16_t* wv, int dim, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                             int rotary_dim, float rope_theta, float qkv_clip, int pos, float* q_out,
+                             uint16_t* kcache, uint16_t* vcache) {
+  if (!x || !wq || !wk || !wv || !q_out || !kcache || !vcache || dim <= 0 || head_dim <= 0 || head_dim % 2 ||
+      n_heads <= 0 || n_kv_heads <= 0 || max_seq_len <= kKvSinks || pos < 0)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  const size_t qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
+  const size_t kv = kvd * max_seq_len;
+  DevBufs b;
+  float* dx = b.alloc<float>(dim, x);
+  float* dg = gain ? b.alloc<float>(dim, gain) : nullptr;
+  uint16_t* dw = b.alloc<uint16_t>((qd + 2 * kvd) * dim);
+  TRY_ALLOC(dx);
+  if (gain) TRY_ALLOC(dg);
+  TRY_ALLOC(dw);
+  HIP_TRY(nullptr, hipMemcpy(dw, wq, qd * dim * 2, hipMemcpyHostToDevice));
+  HIP_TRY(nullptr, hipMemcpy(dw + qd * dim, wk, kvd * dim * 2, hipMemcpyHostToDevice));
+  HIP_TRY(nullptr, hipMemcpy(dw + (qd + kvd) * dim, wv, kvd * dim * 2, hipMemcpyHostToDevice));
+  float* dq = b.alloc<float>(qd);
+  uint16_t* dk = b.alloc<uint16_t>(kv, kcache);
+  uint16_t* dv = b.alloc<uint16_t>(kv, vcache);
+  StepParams hp{0, pos, {0, 0}};
+  StepParams* dp = b.alloc<StepParams>(1, &hp);
+  TRY_ALLOC(dq);
+  TRY_ALLOC(dk);
+  TRY_ALLOC(dv);
+  TRY_ALLOC(dp);
+  MatvecArgs a = mv_base();
+  a.w0 = dw;
+  a.row_step = 2L * dim;
+  a.r_step = dim;
+  a.groups = (int)((qd + 2 * kvd) / 2);
+  a.K = dim;
+  a.x = dx;
+  a.gain = dg;
+  a.eps = eps;
+  a.out = dq;
+  a.q_dim = (int)qd;
+  a.kv_dim = (int)kvd;
+  a.head_dim = head_dim;
+  a.rotary_dim = rotary_dim;
+  a.msl = max_seq_len;
+  a.rope_theta = rope_theta;
+  a.qkv_clip = qkv_clip;
+  a.kcache = dk;
+  a.vcache = dv;
+  a.params = dp;
+  if (int rc = launch_matvec(nullptr, a, kEpiQkvRope, 2, device_cus(), nullptr)) return rc;
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  HIP_TRY(nullptr, hipMemcpy(q_out, dq, qd * 4, hipMemcpyDeviceToHost));
+  HIP_TRY(nullptr, hipMemcpy(kcache, dk, kv * 2, hipMemcpyDeviceToHost));
+  HIP_TRY(nullptr, hipMemcpy(vcache, dv, kv * 2, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_test_argmax(const float* logits, int n, int* out) {
+  if (!logits || !out || n <= 0) return fail(nullptr, YHIP_EINVAL, "bad argument");
+  DevBufs b;
+  float* dl = b.alloc<float>(n, logits);
+  int* dout = b.alloc<int>(1);
+  TRY_ALLOC(dl);
+  TRY_ALLOC(dout);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kBlock), 0, nullptr, (const float*)dl, n, dout);
+  HIP_TRY(nullptr, hipGetLastError());
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  HIP_TRY(nullptr, hipMemcpy(out, dout, sizeof(int), hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+// ============================================================================================
+// Microbenchmark of one fused kernel with rotating weight copies.
+// ============================================================================================
+namespace {
+__global__ void fill_weights_kernel(uint16_t* w, size_t n, uint32_t seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    uint32_t h = (uint32_t)i * 2654435761u ^ seed;
+    h ^= h >> 15;
+    h *= 2246822519u;
+    h ^= h >> 13;
+    // uniform in [-0.03, 0.03): small, finite fp16
+    const float u = ((h >> 8) * (1.0f / 16777216.0f) - 0.5f) * 0.06f;
+    w[i] = __builtin_bit_cast(uint16_t, (f16)u);
+  }
+}
+__global__ void fill_float_kernel(float* p, size_t n, float base, float step) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = base + step * (float)((i * 7919u) % 1000u);
+}
+}  // namespace
+
+extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, float* us_per_launch) {
+  if (!us_per_launch || rows <= 0 || cols <= 0 || copies <= 0 || reps <= 0 || warmup < 0 || kind < 0 || kind > 4)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  if ((kind == 0 || kind == 1 || kind == 4) && rows % 2) return fail(nullptr, YHIP_EINVAL, "rows must be even");
+  const int R = (kind == 3) ? 1 : 2;
+  const int nmat = (kind == 2) ? 2 : 1;
+  const size_t per = (size_t)rows * cols * nmat;
+  DevBufs b;
+  uint16_t* w = b.alloc<uint16_t>(per * copies);
+  float* x = b.alloc<float>(cols);
+  float* g = b.alloc<float>(cols);
+  float* out = b.alloc<float>(std::max(rows, 1 << 16));
+  // attention-shaped KV for the QKV epilogue: 8 kv heads of 128 at msl 4096 when rows == 6144
+  const int hd = 128, nkv = 8, msl = 4096;
+  uint16_t* kc = b.alloc<uint16_t>((size_t)nkv * hd * msl);
+  uint16_t* vc = b.alloc<uint16_t>((size_t)nkv * hd * msl);
+  StepParams hp{0, 7, {0, 0}};
+  StepParams* dp = b.alloc<StepParams>(1, &hp);
+  TRY_ALLOC(w);
+  TRY_ALLOC(x);
+  TRY_ALLOC(g);
+  TRY_ALLOC(out);
+  TRY_ALLOC(kc);
+  TRY_ALLOC(vc);
+  TRY_ALLOC(dp);
+  hipLaunchKernelGGL(fill_weights_kernel, dim3(4096), dim3(256), 0, nullptr, w, per * copies, 12345u);
+  hipLaunchKernelGGL(fill_float_kernel, dim3(64), dim3(256), 0, nullptr, x, (size_t)cols, -1.0f, 0.002f);
+  hipLaunchKernelGGL(fill_float_kernel, dim3(64), dim3(256), 0, nullptr, g, (size_t)cols, 0.9f, 0.0002f);
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  hipStream_t s;
+  HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  const int cus = device_cus();
+  auto launch = [&](int it) -> int {
+    const uint16_t* base = w + per * (it % copies);
+    MatvecArgs a = mv_base();
+    a.K = cols;
+    a.x = x;
+    a.out = out;
+    int ek = kEpiStore;
+    switch (kind) {
+      case 0:
+        a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
+        a.q_dim = rows - 2 * nkv * hd; a.kv_dim = nkv * hd; a.head_dim = hd; a.rotary_dim = hd; a.msl = msl;
+        a.rope_theta = 1e6f; a.kcache = kc; a.vcache = vc; a.params = dp; ek = kEpiQkvRope;
+        if (a.q_dim < 0) return fail(nullptr, YHIP_EINVAL, "QKV bench needs rows >= 2048");
+        break;
+      case 1:
+        a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; ek = kEpiResidual;
+        break;
+      case 2:
+        a.w0 = base; a.w1 = base + (size_t)rows * cols; a.row_step = cols; a.groups = rows; a.gain = g;
+        a.eps = 1e-5f; a.act = 1; ek = kEpiSwiGLU;
+        break;
+      case 3:
+        a.w0 = base; a.row_step = cols; a.r_step = cols; a.groups = rows; ek = kEpiResidual;
+        break;
+      default:
+        a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
+        break;
+    }
+    return launch_matvec(nullptr, a, ek, R, cus, s);
+  };
+  int rc = 0;
+  for (int i = 0; i < warmup && !rc; ++i) rc = launch(i);
+  hipEvent_t e0, e1;
+  hipEventCreate(&e0);
+  hipEventCreate(&e1);
+  hipEventRecord(e0, s);
+  for (int i = 0; i < reps && !rc; ++i) rc = launch(warmup + i);
+  hipEventRecord(e1, s);
+  hipError_t e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  hipStreamDestroy(s);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, hipGetErrorString(e));
+  *us_per_launch = ms * 1000.0f / reps;
+  return YHIP_OK;
+}

@@ -1,0 +1,271 @@
+"""ctypes binding of libyalm_hip.so (the C-ABI declared in include/yalm_hip.h).
+
+This is what a Python caller (the tests, bench.py) uses to reach the HIP decode path. It loads the
+in-tree library and fails loudly if it has not been built: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libyalm_hip.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_ip = ctypes.POINTER(ctypes.c_int)
+
+MODE_HYDRATE = 0
+MODE_LOGITS = 1
+
+# Every symbol include/yalm_hip.h declares.
+EXPORTS = (
+    "yhip_create", "yhip_destroy", "yhip_upload_layer", "yhip_upload_globals", "yhip_forward",
+    "yhip_forward_argmax", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
+    "yhip_debug_read", "yhip_last_error", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
+    "yhip_test_qkv", "yhip_test_argmax", "yhip_bench_kernel",
+)
+
+
+class HipConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "dim", "hidden_dim", "head_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size",
+        "max_seq_len", "rotary_dim")] + [
+        ("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float), ("qkv_clip", ctypes.c_float),
+        ("act", ctypes.c_int)]
+
+
+class HipError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """Load libyalm_hip.so; raises if it is missing (build with __graft_entry__.build())."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipError(f"HIP library not built: {LIB_PATH}")
+    L = ctypes.CDLL(LIB_PATH)
+    vp = ctypes.c_void_p
+    sig = {
+        "yhip_create": (ctypes.c_int, [ctypes.POINTER(HipConfig), ctypes.c_int, ctypes.POINTER(vp)]),
+        "yhip_destroy": (ctypes.c_int, [vp]),
+        "yhip_upload_layer": (ctypes.c_int, [vp, ctypes.c_int, _f32p, _f32p] + [_u16p] * 7),
+        "yhip_upload_globals": (ctypes.c_int, [vp, _u16p, _f32p, _u16p]),
+        "yhip_forward": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
+        "yhip_forward_argmax": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int, _ip]),
+        "yhip_logits_host": (_f32p, [vp]),
+        "yhip_kv_read": (ctypes.c_int, [vp, ctypes.c_int, _u16p, _u16p]),
+        "yhip_kv_write": (ctypes.c_int, [vp, ctypes.c_int, _u16p, _u16p]),
+        "yhip_set_option": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.c_int]),
+        "yhip_debug_read": (ctypes.c_int, [vp, ctypes.c_int, _f32p, ctypes.c_size_t]),
+        "yhip_last_error": (ctypes.c_char_p, [vp]),
+        "yhip_test_matvec": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, ctypes.c_int, ctypes.c_int,
+                                            _f32p, _f32p]),
+        "yhip_test_ffn": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, _f32p, _f32p]),
+        "yhip_test_attention": (ctypes.c_int, [_f32p, _u16p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                               ctypes.c_int, _f32p]),
+        "yhip_test_qkv": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p] + [ctypes.c_int] * 7
+                          + [ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p, _u16p, _u16p]),
+        "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
+        "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc, ctx=None):
+    if rc != 0:
+        msg = lib().yhip_last_error(ctx)
+        raise HipError(f"yalm_hip error {rc}: {msg.decode() if msg else ''}")
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_f32p)
+
+
+def _u16(a):
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    return a, a.ctypes.data_as(_u16p)
+
+
+def make_config(cfg) -> HipConfig:
+    get = (lambda k: cfg[k]) if isinstance(cfg, dict) else (lambda k: getattr(cfg, k))
+    act = get("act")
+    if isinstance(act, str):
+        act = 1 if act == "silu" else 0
+    return HipConfig(get("dim"), get("hidden_dim"), get("head_dim"), get("n_layers"), get("n_heads"),
+                     get("n_kv_heads"), get("vocab_size"), get("max_seq_len"), get("rotary_dim"),
+                     float(get("rope_theta")), float(get("norm_eps")), float(get("qkv_clip")), int(act))
+
+
+class HipModel:
+    """A device context holding one model's weights and KV caches (one decode stream)."""
+
+    def __init__(self, cfg, tensors=None, device=0):
+        self.cfg = make_config(cfg)
+        h = ctypes.c_void_p()
+        _check(lib().yhip_create(ctypes.byref(self.cfg), device, ctypes.byref(h)))
+        self.h = h
+        if tensors is not None:
+            self.upload(tensors)
+
+    def upload(self, tensors):
+        c = self.cfg
+        for i in range(c.n_layers):
+            p = f"model.layers.{i}."
+            keep = [_u16(tensors[p + n]) for n in ("attn.wq.weight", "attn.wk.weight", "attn.wv.weight",
+                                                   "attn.wo.weight", "mlp.w1.weight", "mlp.w2.weight",
+                                                   "mlp.w3.weight")]
+            ra_arr = np.ascontiguousarray(tensors[p + "attn.norm.weight"], np.float32)
+            rf_arr = np.ascontiguousarray(tensors[p + "mlp.norm.weight"], np.float32)
+            _check(lib().yhip_upload_layer(self.h, i, ra_arr.ctypes.data_as(_f32p), rf_arr.ctypes.data_as(_f32p),
+                                           *[ptr for _, ptr in keep]), self.h)
+        e, ep = _u16(tensors["model.embed.weight"])
+        g, gp = _f32(tensors["model.norm.weight"])
+        if "model.output.weight" in tensors:
+            o, op = _u16(tensors["model.output.weight"])
+        else:
+            op = None
+        _check(lib().yhip_upload_globals(self.h, ep, gp, op), self.h)
+
+    def forward(self, token, pos, mode=MODE_LOGITS):
+        if mode == MODE_HYDRATE:
+            _check(lib().yhip_forward(self.h, token, pos, mode, None), self.h)
+            return None
+        out = np.zeros(self.cfg.vocab_size, np.float32)
+        _check(lib().yhip_forward(self.h, token, pos, mode, out.ctypes.data_as(_f32p)), self.h)
+        return out
+
+    def forward_argmax(self, token, pos):
+        nxt = ctypes.c_int()
+        _check(lib().yhip_forward_argmax(self.h, token, pos, ctypes.byref(nxt)), self.h)
+        return nxt.value
+
+    def kv(self, layer):
+        c = self.cfg
+        n = c.n_kv_heads * c.head_dim * c.max_seq_len
+        k = np.zeros(n, np.uint16)
+        v = np.zeros(n, np.uint16)
+        _check(lib().yhip_kv_read(self.h, layer, k.ctypes.data_as(_u16p), v.ctypes.data_as(_u16p)), self.h)
+        return k, v
+
+    def set_kv(self, layer, k, v):
+        k, kp = _u16(k)
+        v, vp = _u16(v)
+        _check(lib().yhip_kv_write(self.h, layer, kp, vp), self.h)
+
+    def set_option(self, key, value):
+        _check(lib().yhip_set_option(self.h, key.encode(), int(value)), self.h)
+
+    def debug_read(self, which, n):
+        out = np.zeros(n, np.float32)
+        _check(lib().yhip_debug_read(self.h, which, out.ctypes.data_as(_f32p), n), self.h)
+        return out
+
+    def close(self):
+        if self.h:
+            lib().yhip_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- kernel-level hooks --------------------------------------------------------------------
+def matvec(x, w, gain=None, eps=1e-5, resid=None):
+    d, n = w.shape
+    x, xp = _f32(x)
+    w, wp = _u16(w)
+    g_keep = np.ascontiguousarray(gain, np.float32) if gain is not None else None
+    gp = g_keep.ctypes.data_as(_f32p) if g_keep is not None else None
+    r_keep = np.ascontiguousarray(resid, np.float32) if resid is not None else None
+    rp = r_keep.ctypes.data_as(_f32p) if r_keep is not None else None
+    out = np.zeros(d, np.float32)
+    _check(lib().yhip_test_matvec(xp, gp, eps, wp, n, d, rp, out.ctypes.data_as(_f32p)))
+    return out
+
+
+def ffn(x, w1, w2, w3, gain=None, eps=1e-5, act=1, resid=None):
+    hidden, dim = w1.shape
+    x, xp = _f32(x)
+    a1, p1 = _u16(w1)
+    a2, p2 = _u16(w2)
+    a3, p3 = _u16(w3)
+    g_keep = np.ascontiguousarray(gain, np.float32) if gain is not None else None
+    r_keep = np.ascontiguousarray(resid, np.float32) if resid is not None else None
+    out = np.zeros(dim, np.float32)
+    _check(lib().yhip_test_ffn(xp, g_keep.ctypes.data_as(_f32p) if g_keep is not None else None, eps, p1, p2, p3,
+                               hidden, dim, act, r_keep.ctypes.data_as(_f32p) if r_keep is not None else None,
+                               out.ctypes.data_as(_f32p)))
+    return out
+
+
+def attention(q, kcache, vcache, head_dim, pos, max_seq_len, n_heads, n_kv_heads, nsplit=0, rope_theta=1e6,
+              rotary_dim=None):
+    """Returns (att_out, kcache_after) -- the K cache changes only in sink mode (pos >= msl)."""
+    q, qp = _f32(q)
+    k = np.array(np.asarray(kcache).view(np.uint16) if np.asarray(kcache).dtype == np.float16 else kcache,
+                 dtype=np.uint16, copy=True)
+    v, vp = _u16(vcache)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    _check(lib().yhip_test_attention(qp, k.ctypes.data_as(_u16p), vp, head_dim, pos, max_seq_len, n_heads,
+                                     n_kv_heads, nsplit, rope_theta, rotary_dim or head_dim,
+                                     out.ctypes.data_as(_f32p)))
+    return out, k
+
+
+def qkv(x, gain, wq, wk, wv, n_heads, n_kv_heads, head_dim, max_seq_len, pos, kcache, vcache, eps=1e-5,
+        rope_theta=1e6, rotary_dim=None, qkv_clip=3.4028234663852886e38):
+    dim = wq.shape[1]
+    x, xp = _f32(x)
+    g_keep = np.ascontiguousarray(gain, np.float32) if gain is not None else None
+    aq, pq = _u16(wq)
+    ak, pk = _u16(wk)
+    av, pv = _u16(wv)
+    k = np.array(kcache, dtype=np.uint16, copy=True)
+    v = np.array(vcache, dtype=np.uint16, copy=True)
+    q = np.zeros(n_heads * head_dim, np.float32)
+    _check(lib().yhip_test_qkv(xp, g_keep.ctypes.data_as(_f32p) if g_keep is not None else None, eps, pq, pk, pv,
+                               dim, n_heads, n_kv_heads, head_dim, max_seq_len, rotary_dim or head_dim, rope_theta,
+                               qkv_clip, pos, q.ctypes.data_as(_f32p), k.ctypes.data_as(_u16p),
+                               v.ctypes.data_as(_u16p)))
+    return q, k, v
+
+
+def argmax(logits):
+    lg, p = _f32(logits)
+    out = ctypes.c_int()
+    _check(lib().yhip_test_argmax(p, lg.size, ctypes.byref(out)))
+    return out.value
+
+
+def bench_kernel(kind, rows, cols, copies=4, warmup=20, reps=200):
+    us = ctypes.c_float()
+    _check(lib().yhip_bench_kernel(kind, rows, cols, copies, warmup, reps, ctypes.byref(us)))
+    return us.value
