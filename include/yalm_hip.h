@@ -120,9 +120,12 @@ int yhip_test_argmax(const float* logits, int n, int* out);
 /* ---- microbenchmark: one fused decode kernel at a given shape, weights rotated over `copies`
  * device-resident copies (to keep the 256 MB last-level cache from serving them), timed with HIP
  * events on the launching stream. kind: 0 = rmsnorm+QKV+RoPE (rows = q+k+v dims), 1 = O-proj +
- * residual, 2 = rmsnorm + W1/W3 + SwiGLU, 3 = W2 + residual, 4 = rmsnorm + lm_head.
+ * residual, 2 = rmsnorm + W1/W3 + SwiGLU, 3 = W2 + residual, 4 = rmsnorm + lm_head, 5 = plain
+ * device copy of rows*cols fp16 (the reference point for hardware byte counters).
+ * blocks_per_cu caps the grid at blocks_per_cu x CUs workgroups (0 = the decode path's default).
  * Writes the mean kernel time in microseconds. ---- */
-int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, float* us_per_launch);
+int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, int blocks_per_cu,
+                      float* us_per_launch);
 
 #ifdef __cplusplus
 }

@@ -39,3 +39,34 @@ def test_create_without_device_fails_cleanly():
     from tests.util import MICRO
     with pytest.raises(H.HipError):
         H.HipModel(dict(MICRO))
+
+
+def header_arities(name):
+    text = open(os.path.join(ROOT, "include", name)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(yhip_[a-z_0-9]+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_argument_counts_match_header():
+    from yalm_amd import hip as H
+    L = H.lib()
+    for name, n in header_arities("yalm_hip.h").items():
+        assert len(getattr(L, name).argtypes) == n, name
+
+
+def test_host_library_exports_and_binding_arities():
+    from yalm_amd import host as HO
+    lib = ctypes.CDLL(HO.LIB_PATH)
+    text = open(os.path.join(ROOT, "include", "yalm_host.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decl = {m.group(1): (0 if m.group(2).strip() in ("", "void") else m.group(2).count(",") + 1)
+            for m in re.finditer(r"\b(yalm_[a-z_0-9]+)\s*\(([^)]*)\)\s*;", text)}
+    assert sorted(decl) == sorted(HO.EXPORTS)
+    L = HO.lib()
+    for name, n in decl.items():
+        assert hasattr(lib, name), name
+        assert len(getattr(L, name).argtypes) == n, name

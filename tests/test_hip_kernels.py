@@ -139,10 +139,11 @@ def _oracle_qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc, theta=1e6, clip
     k = O.rope(k, hd, pos, theta, hd)
     kc = kc.copy()
     vc = vc.copy()
+    kv_pos = O.positions(pos, msl)[1]  # the ring slot once pos >= max_seq_len
     for i in range(k.size):
         gi, j = divmod(i, hd)
-        kc[gi * hd * msl + O.k_cache_idx(j, pos, msl)] = O.f2h([k[i]])[0]
-        vc[gi * hd * msl + j * msl + pos] = O.f2h([v[i]])[0]
+        kc[gi * hd * msl + O.k_cache_idx(j, kv_pos, msl)] = O.f2h([k[i]])[0]
+        vc[gi * hd * msl + j * msl + kv_pos] = O.f2h([v[i]])[0]
     return q, kc, vc
 
 
@@ -182,13 +183,14 @@ def test_qkv_rope_parity(pos, shape):
     # the RoPE angle error grows with pos (fp32 frequencies can differ by an ulp between libms)
     assert npref.rel_l2(q, qo) < 1e-5 + 3e-7 * pos
     changed = (k2 != kc) | (ko != kc)
-    # only the entries of position `pos` may change, and they are all at reference indices
-    idx = np.array([gi * hd * msl + O.k_cache_idx(j, pos, msl) for gi in range(nkv) for j in range(hd)])
+    # only the entries of slot kv_pos may change, and they are all at reference indices
+    kv_pos = O.positions(pos, msl)[1]
+    idx = np.array([gi * hd * msl + O.k_cache_idx(j, kv_pos, msl) for gi in range(nkv) for j in range(hd)])
     mask = np.zeros_like(changed)
     mask[idx] = True
     assert not np.any(changed & ~mask)
     assert npref.rel_l2(h2f(k2[idx]), h2f(ko[idx])) < 2e-3
-    vidx = np.array([gi * hd * msl + j * msl + pos for gi in range(nkv) for j in range(hd)])
+    vidx = np.array([gi * hd * msl + j * msl + kv_pos for gi in range(nkv) for j in range(hd)])
     vmask = np.zeros(vc.size, bool)
     vmask[vidx] = True
     assert np.array_equal(v2[~vmask], vc[~vmask])

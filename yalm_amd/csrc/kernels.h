@@ -143,7 +143,7 @@ struct MatvecArgs {
   uint16_t* kcache;
   uint16_t* vcache;
   const StepParams* params;
-  // norm statistics written by the kernel for the host-side debug reader (unused otherwise)
+  const float* rope_cs;  // [head_dim]: (cos, sin) per rotary pair at this step's position
 };
 
 // Loads of one row segment for this lane: chunk c = lane + 64*u, u < KC (KC = K/512 when > 0).
@@ -166,15 +166,15 @@ __device__ __forceinline__ void group_rows(const MatvecArgs& a, int p, const uin
   }
 }
 
-template <int R>
-__device__ __forceinline__ void epilogue(const MatvecArgs& a, int kind, int p, const float (&acc)[R]) {
-  if (kind == kEpiStore) {
+template <int R, EpiKind EPI>
+__device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float (&acc)[R]) {
+  if constexpr (EPI == kEpiStore) {
 #pragma unroll
     for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
-  } else if (kind == kEpiResidual) {
+  } else if constexpr (EPI == kEpiResidual) {
 #pragma unroll
     for (int r = 0; r < R; ++r) a.out[(long)p * R + r] += acc[r];
-  } else if (kind == kEpiSwiGLU) {
+  } else if constexpr (EPI == kEpiSwiGLU) {
     float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
     a.out[p] = h * acc[R - 1];
   } else {  // kEpiQkvRope: rows i = 2p, 2p+1 of [Wq; Wk; Wv]  (reference src/infer.cpp:279-305)
@@ -183,10 +183,9 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int kind, int p, c
     float v1 = clipf(acc[R - 1], a.qkv_clip);
     const int pos = a.params->pos;
     if (i < a.q_dim + a.kv_dim) {  // RoPE on q and k (reference src/infer.cpp:202-215)
+      // (cos, sin) of pos * freq_j for this step, computed once per token by embed_kernel
       const int j = i % a.head_dim;
-      const float freq = j >= a.rotary_dim ? 0.f : 1.0f / powf(a.rope_theta, (float)j / (float)a.rotary_dim);
-      const float ang = (float)pos * freq;
-      const float c = cosf(ang), s = sinf(ang);
+      const float c = a.rope_cs[j], s = a.rope_cs[j + 1];
       const float r0 = v0 * c - v1 * s;
       const float r1 = v0 * s + v1 * c;
       v0 = r0;
@@ -276,8 +275,8 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
 // KC > 0: K == 512*KC, fully unrolled row streaming. KC == 0: any K % 8 == 0.
 // One register buffer of weights per wave; latency is hidden by the other resident waves and by
 // issuing the next group's loads ahead of the current group's reductions and epilogue.
-template <int KC, int R>
-__global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a, int kind) {
+template <int KC, int R, EpiKind EPI>
+__global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
   extern __shared__ float lds[];
   float* red = lds;      // kWavesPerBlock floats (padded to 16)
   float* xs = lds + 16;  // K floats
@@ -315,7 +314,7 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a, int kind) 
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane == 0) epilogue<R>(a, kind, p, acc);
+      if (lane == 0) epilogue<R, EPI>(a, p, acc);
       p += wave_stride;
     }
   } else {
@@ -336,28 +335,66 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a, int kind) 
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane == 0) epilogue<R>(a, kind, p, acc);
+      if (lane == 0) epilogue<R, EPI>(a, p, acc);
     }
   }
 }
 
 // ------------------------------------------------------------------------------------------
-// Embedding gather (reference src/infer.cpp:460-481): x[i] = f32(E[token*dim + i]), exact.
+// Per-step RoPE table: rope_cs[2k], rope_cs[2k+1] = cos, sin of (float)pos * inv_freq[k], the angle
+// of rotary pair k (reference src/infer.cpp:205-208: fp32 angle pos * freq, then cosf / sinf).
+// inv_freq[k] = 1 / powf(theta, 2k / rotary_dim), or 0 past rotary_dim, is computed on the host.
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* emb, float* x, int dim, const StepParams* params) {
+__device__ __forceinline__ void fill_rope_table(const float* inv_freq, float* rope_cs, int half, int pos) {
+  for (int k = threadIdx.x; k < half; k += blockDim.x) {
+    const float ang = (float)pos * inv_freq[k];
+    rope_cs[2 * k] = cosf(ang);
+    rope_cs[2 * k + 1] = sinf(ang);
+  }
+}
+
+__global__ void rope_table_kernel(const float* inv_freq, float* rope_cs, int half, const StepParams* params) {
+  fill_rope_table(inv_freq, rope_cs, half, params->pos);
+}
+
+// ------------------------------------------------------------------------------------------
+// Embedding gather (reference src/infer.cpp:460-481): x[i] = f32(E[token*dim + i]), exact.
+// Workgroup 0 also fills the step's RoPE table.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* emb, float* x, int dim, const StepParams* params,
+                                                       const float* inv_freq, float* rope_cs, int half) {
   const long base = (long)params->token * dim;
   for (int i = blockIdx.x * kBlock + threadIdx.x; i < dim; i += gridDim.x * kBlock)
     x[i] = (float)__builtin_bit_cast(f16, emb[base + i]);
+  if (blockIdx.x == 0) fill_rope_table(inv_freq, rope_cs, half, params->pos);
 }
+
+// ------------------------------------------------------------------------------------------
+// Cross-workgroup hand-off without cache-wide fences.
+//
+// On a multi-XCD part each XCD has its own L2; an agent-scope fence would write back and
+// invalidate the whole L2 of every workgroup that executes it. Data that one workgroup hands to
+// another is instead written and read with agent-scope relaxed atomics (coherent, written through
+// past the XCD's L2), and `publish()` waits until this thread's stores have completed before the
+// workgroup signals.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void store_shared(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_shared(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------------------------------
 // Split-KV GQA decode attention (reference src/infer.cpp:218-250, 327-336).
 //
 // Workgroup (g, s) handles kv head g and the s-th slice of [0, kv_len) for all G query heads
-// that share g, so each K/V byte is read once per token. Scores for a 256-token tile go to LDS;
-// an online softmax keeps (max, sum, acc) per head. The last workgroup to finish for head g
-// (atomic ticket) merges the slices and writes out[h][0..hd).
-// Work split: chunk = roundup(ceil(kv_len / nsplit), 64) tokens per slice.
+// that share g, so each K/V byte is read once per token. Slices are at least kMinSlice tokens:
+//   chunk = max(kMinSlice, roundup(ceil(kv_len / nsplit), 64)),  active = ceil(kv_len / chunk)
+// Workgroups past `active` exit at once. With one active slice the workgroup writes the output
+// directly; otherwise each writes (max, sum, acc) per head and the last to finish (atomic ticket)
+// merges them. Scores for a 256-token tile go to LDS; an online softmax keeps (max, sum, acc).
 // In sink mode (pos >= msl) slice 0 first re-rotates the two sink keys by one position
 // (reference src/infer.cpp:307-325).
 // ------------------------------------------------------------------------------------------
@@ -368,13 +405,20 @@ struct AttnArgs {
   float* partial;        // [nh][nsplit][hd + 2]
   unsigned* tickets;     // [nkv]
   float* out;            // [nh][hd]
-  int head_dim, n_heads, n_kv_heads, msl, nsplit, rotary_dim;
-  float rope_theta;
+  int head_dim, n_heads, n_kv_heads, msl, nsplit;
+  const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
 };
 
 constexpr int kAttnTile = 256;
 constexpr int kMaxGroup = 8;
+constexpr int kMinSlice = 256;
+
+__device__ __forceinline__ int attn_chunk(int kv_len, int nsplit) {
+  int chunk = (kv_len + nsplit - 1) / nsplit;
+  chunk = (chunk + 63) & ~63;
+  return chunk < kMinSlice ? kMinSlice : chunk;
+}
 
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   __shared__ float qs[kMaxGroup * 128];
@@ -390,8 +434,9 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   const int lane = tid & (kWave - 1), wave = tid / kWave;
   const Positions ps = positions(a.params->pos, a.msl);
   const int kv_len = ps.kv_len;
-  int chunk = (kv_len + a.nsplit - 1) / a.nsplit;
-  chunk = (chunk + 63) & ~63;
+  const int chunk = attn_chunk(kv_len, a.nsplit);
+  const int active = (kv_len + chunk - 1) / chunk;
+  if (split >= active) return;
   const int t_begin = split * chunk;
   const int t_end = min(kv_len, t_begin + chunk);
   const long head_off = (long)g * hd * a.msl;
@@ -403,7 +448,7 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
     for (int e = tid; e < ps.kv_sink * (hd / 2); e += kBlock) {
       const int r = e / (hd / 2);
       const int j = 2 * (e % (hd / 2));
-      const float freq = j >= a.rotary_dim ? 0.f : 1.0f / powf(a.rope_theta, (float)j / (float)a.rotary_dim);
+      const float freq = a.inv_freq[j / 2];
       const float c = cosf(freq), s = sinf(freq);
       uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
       uint16_t* p1 = kh + k_cache_idx(j + 1, r, a.msl);
@@ -411,7 +456,6 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
       *p0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
       *p1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
     }
-    __threadfence_block();
     __syncthreads();
   }
 
@@ -430,7 +474,6 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   float acc[kMaxGroup];
 #pragma unroll
   for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.f;
-  const float inv_sqrt = 1.0f / sqrtf((float)hd);
   const bool vec_ok = (a.msl & 7) == 0;
   __syncthreads();
 
@@ -464,7 +507,6 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int h = 0; h < kMaxGroup; ++h) s[h] = kNegBig;
     }
-    (void)inv_sqrt;
     // tile max per head
     float corr[kMaxGroup];
 #pragma unroll
@@ -538,78 +580,114 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
     __syncthreads();  // sc / red reused by the next tile
   }
 
-  // Merge the token parts of this workgroup, then publish the slice partial.
+  // Merge the token parts of this workgroup.
   for (int h = 0; h < G; ++h) accs[h * 256 + tid] = acc[h];
   __syncthreads();
+  if (active == 1) {  // the only slice: final normalisation here
+    for (int e = tid; e < G * hd; e += kBlock) {
+      const int h = e / hd, i = e % hd;
+      float o = 0.f;
+      for (int pt = 0; pt < parts; ++pt) o += accs[h * 256 + pt * hd + i];
+      a.out[(long)(g * G + h) * hd + i] = o / l_run[h];
+    }
+    return;
+  }
   const int stride = hd + 2;
   for (int e = tid; e < G * hd; e += kBlock) {
     const int h = e / hd, i = e % hd;
     float o = 0.f;
     for (int pt = 0; pt < parts; ++pt) o += accs[h * 256 + pt * hd + i];
     float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
-    dst[i] = o;
+    store_shared(dst + i, o);
     if (i == 0) {
-      dst[hd] = m_run[h];
-      dst[hd + 1] = l_run[h];
+      store_shared(dst + hd, m_run[h]);
+      store_shared(dst + hd + 1, l_run[h]);
     }
   }
-  __threadfence();
+  publish();
   __syncthreads();
   if (tid == 0) {
-    const unsigned t = atomicAdd(&a.tickets[g], 1u);
-    last_flag = (t == (unsigned)(gridDim.y - 1)) ? 1u : 0u;
+    const unsigned t = __hip_atomic_fetch_add(&a.tickets[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = (t == (unsigned)(active - 1)) ? 1u : 0u;
   }
   __syncthreads();
   if (!last_flag) return;
-  __threadfence();
   for (int e = tid; e < G * hd; e += kBlock) {
     const int h = e / hd, i = e % hd;
     const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride;
     float M = kNegBig;
-    for (int sp = 0; sp < a.nsplit; ++sp) M = fmaxf(M, __builtin_nontemporal_load(src + sp * stride + hd));
+    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, load_shared(src + sp * stride + hd));
     float L = 0.f, O = 0.f;
-    for (int sp = 0; sp < a.nsplit; ++sp) {
+    for (int sp = 0; sp < active; ++sp) {
       const float* ps_ = src + sp * stride;
-      const float w = expf(__builtin_nontemporal_load(ps_ + hd) - M);
-      L = fmaf(__builtin_nontemporal_load(ps_ + hd + 1), w, L);
-      O = fmaf(__builtin_nontemporal_load(ps_ + i), w, O);
+      const float w = expf(load_shared(ps_ + hd) - M);
+      L = fmaf(load_shared(ps_ + hd + 1), w, L);
+      O = fmaf(load_shared(ps_ + i), w, O);
     }
     a.out[(long)(g * G + h) * hd + i] = O / L;
   }
-  if (tid == 0) atomicExch(&a.tickets[g], 0u);
+  if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------------------
 // Greedy argmax over logits with the reference tie rule (first index of the strict maximum,
-// src/sampler.cpp:27-38). One workgroup.
+// src/sampler.cpp:27-38). One workgroup of kArgmaxThreads; every thread issues its float4 loads
+// up front (n = 32000 -> 8 per thread).
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(kBlock) argmax_kernel(const float* logits, int n, int* out) {
-  __shared__ float bv[kBlock];
-  __shared__ int bi[kBlock];
-  float best = kNegBig;
-  int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += kBlock) {
-    const float v = logits[i];
-    if (v > best) {  // increasing i per thread: keeps the first index of this thread's maximum
-      best = v;
-      idx = i;
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const float* logits, int n, int* out) {
+  __shared__ float sv[kArgmaxThreads / kWave];
+  __shared__ int si[kArgmaxThreads / kWave];
+  float bv = kNegBig;
+  int bi = 0x7fffffff;
+  const int n4 = n >> 2;
+  const f32x4* l4 = reinterpret_cast<const f32x4*>(logits);
+  constexpr int kBatch = 8;
+  for (int base = 0; base < n4; base += kArgmaxThreads * kBatch) {
+    f32x4 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = base + k * kArgmaxThreads + threadIdx.x;
+      v[k] = idx < n4 ? l4[idx] : f32x4{kNegBig, kNegBig, kNegBig, kNegBig};
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = base + k * kArgmaxThreads + threadIdx.x;
+      if (idx < n4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (v[k][e] > kNegBig) better(bv, bi, v[k][e], 4 * idx + e);
     }
   }
-  bv[threadIdx.x] = best;
-  bi[threadIdx.x] = idx;
+  for (int i = 4 * n4 + threadIdx.x; i < n; i += kArgmaxThreads)
+    if (logits[i] > kNegBig) better(bv, bi, logits[i], i);
+  // wave reduce (value, index) with the tie rule
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    better(bv, bi, ov, oi);
+  }
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
   __syncthreads();
-  for (int s = kBlock / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      const float ov = bv[threadIdx.x + s];
-      const int oi = bi[threadIdx.x + s];
-      if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
-        bv[threadIdx.x] = ov;
-        bi[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = sv[0];
+    int i = si[0];
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) better(v, i, sv[w], si[w]);
+    out[0] = i == 0x7fffffff ? 0 : i;
   }
-  if (threadIdx.x == 0) out[0] = bi[0] == 0x7fffffff ? 0 : bi[0];
 }
 
 }  // namespace yk

@@ -69,6 +69,8 @@ struct yhip_ctx {
   unsigned* tickets = nullptr;
   int* argmax_dev = nullptr;
   StepParams* params = nullptr;
+  float* inv_freq = nullptr;  // [head_dim / 2]
+  float* rope_cs = nullptr;   // [head_dim], refreshed every step
 
   float* logits_host = nullptr;  // pinned
   int* argmax_host = nullptr;    // pinned
@@ -102,31 +104,54 @@ int fail(yhip_ctx* ctx, int code, const std::string& msg) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// ---- matvec launch -------------------------------------------------------------------------
-int max_blocks_for(int num_cus) { return num_cus * 4; }
-
-template <int KC, int R>
-void launch_mv(const MatvecArgs& a, int kind, int blocks, hipStream_t s) {
-  const size_t lds = (16 + (size_t)a.K) * sizeof(float);
-  hipLaunchKernelGGL((matvec_kernel<KC, R>), dim3(blocks), dim3(kBlock), lds, s, a, kind);
+// Rotary inverse frequencies, one per pair: 1 / powf(theta, j / rotary_dim) for even j < rotary_dim,
+// 0 beyond it (reference src/infer.cpp:205), computed once on the host in fp32.
+std::vector<float> make_inv_freq(int head_dim, int rotary_dim, float theta) {
+  std::vector<float> f(head_dim / 2);
+  for (int k = 0; k < head_dim / 2; ++k) {
+    const int j = 2 * k;
+    f[k] = j >= rotary_dim ? 0.f : 1.0f / powf(theta, (float)j / (float)rotary_dim);
+  }
+  return f;
 }
 
-// Chooses the instantiation for row length K and rows-per-group R.
-int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s) {
+// ---- matvec launch -------------------------------------------------------------------------
+// Workgroups per CU: measured best on MI355X is 2 for 4096-long rows (QKV, O, W1/W3, lm_head) and 1
+// for 14336-long rows (W2, whose 57 KB LDS input already limits residency).
+int default_bpc(int K) { return K >= 8192 ? 1 : 2; }
+
+template <int KC, int R, EpiKind EPI>
+void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
+  const size_t lds = (16 + (size_t)a.K) * sizeof(float);
+  hipLaunchKernelGGL((matvec_kernel<KC, R, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
+}
+
+template <EpiKind EPI>
+void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
+  if (R == 1) {
+    if (a.K == 4096) launch_mv<8, 1, EPI>(a, blocks, s);
+    else if (a.K == 14336) launch_mv<28, 1, EPI>(a, blocks, s);
+    else launch_mv<0, 1, EPI>(a, blocks, s);
+  } else {
+    if (a.K == 4096) launch_mv<8, 2, EPI>(a, blocks, s);
+    else launch_mv<0, 2, EPI>(a, blocks, s);
+  }
+}
+
+// Chooses the instantiation for row length K, rows-per-group R and epilogue kind.
+int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s, int bpc = 0) {
   if (a.K % 8 != 0 || (16 + (size_t)a.K) * sizeof(float) > 65536)
     return fail(ctx, YHIP_EINVAL, "matvec: row length must be a multiple of 8 and at most 16368");
-  int waves_needed = a.groups;
-  int blocks = (waves_needed + kWavesPerBlock - 1) / kWavesPerBlock;
-  blocks = std::max(1, std::min(blocks, max_blocks_for(num_cus)));
-  if (R == 1) {
-    if (a.K == 4096) launch_mv<8, 1>(a, kind, blocks, s);
-    else if (a.K == 14336) launch_mv<28, 1>(a, kind, blocks, s);
-    else launch_mv<0, 1>(a, kind, blocks, s);
-  } else if (R == 2) {
-    if (a.K == 4096) launch_mv<8, 2>(a, kind, blocks, s);
-    else launch_mv<0, 2>(a, kind, blocks, s);
-  } else {
-    return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
+  if (R != 1 && R != 2) return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
+  if (bpc <= 0) bpc = default_bpc(a.K);
+  int blocks = (a.groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  blocks = std::max(1, std::min(blocks, num_cus * bpc));
+  switch (kind) {
+    case kEpiStore: launch_by_shape<kEpiStore>(a, R, blocks, s); break;
+    case kEpiResidual: launch_by_shape<kEpiResidual>(a, R, blocks, s); break;
+    case kEpiSwiGLU: launch_by_shape<kEpiSwiGLU>(a, R, blocks, s); break;
+    case kEpiQkvRope: launch_by_shape<kEpiQkvRope>(a, R, blocks, s); break;
+    default: return fail(ctx, YHIP_EINVAL, "matvec: unknown epilogue");
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("matvec launch: ") + hipGetErrorString(e));
@@ -162,7 +187,8 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
   hipStream_t s = ctx->stream;
   const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
   hipLaunchKernelGGL(embed_kernel, dim3((c.dim + kBlock - 1) / kBlock), dim3(kBlock), 0, s, ctx->embed, ctx->x,
-                     c.dim, (const StepParams*)ctx->params);
+                     c.dim, (const StepParams*)ctx->params, (const float*)ctx->inv_freq, ctx->rope_cs,
+                     c.head_dim / 2);
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& L = ctx->layers[l];
     int rc;
@@ -187,6 +213,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.kcache = ctx->kcache(l);
     a.vcache = ctx->vcache(l);
     a.params = ctx->params;
+    a.rope_cs = ctx->rope_cs;
     if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s))) return rc;
     // 2. attention
     AttnArgs t;
@@ -201,8 +228,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     t.n_kv_heads = c.n_kv_heads;
     t.msl = c.max_seq_len;
     t.nsplit = ctx->attn_splits;
-    t.rotary_dim = c.rotary_dim;
-    t.rope_theta = c.rope_theta;
+    t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
     if ((rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
@@ -256,7 +282,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
   } else {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kBlock), 0, s, (const float*)ctx->logits, c.vocab_size,
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, (const float*)ctx->logits, c.vocab_size,
                        ctx->argmax_dev);
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, s));
   }
@@ -384,7 +410,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   };
   const size_t a_x = atake(dim * 4), a_q = atake(qd * 4), a_att = atake(qd * 4), a_hb = atake(hid * 4),
                a_lg = atake(V * 4), a_part = atake((size_t)c.n_heads * 64 * (c.head_dim + 2) * 4),
-               a_tk = atake(64 * 4), a_am = atake(64), a_par = atake(sizeof(StepParams));
+               a_tk = atake(64 * 4), a_am = atake(64), a_par = atake(sizeof(StepParams)),
+               a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4);
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -396,6 +423,13 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->tickets = (unsigned*)(ctx->abase + a_tk);
   ctx->argmax_dev = (int*)(ctx->abase + a_am);
   ctx->params = (StepParams*)(ctx->abase + a_par);
+  ctx->inv_freq = (float*)(ctx->abase + a_if);
+  ctx->rope_cs = (float*)(ctx->abase + a_cs);
+  {
+    const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
+    if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bail(fail(nullptr, YHIP_EDEVICE, "upload of rotary frequencies failed"));
+  }
   if (hipHostMalloc((void**)&ctx->logits_host, V * 4, hipHostMallocDefault) != hipSuccess ||
       hipHostMalloc((void**)&ctx->argmax_host, 64, hipHostMallocDefault) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "pinned host allocation failed"));
@@ -669,6 +703,8 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   float* dout = b.alloc<float>((size_t)n_heads * head_dim);
   StepParams hp{0, pos, {0, 0}};
   StepParams* dp = b.alloc<StepParams>(1, &hp);
+  const std::vector<float> freqs = make_inv_freq(head_dim, rotary_dim, rope_theta);
+  float* dfreq = b.alloc<float>(freqs.size(), freqs.data());
   TRY_ALLOC(dq);
   TRY_ALLOC(dk);
   TRY_ALLOC(dv);
@@ -676,6 +712,7 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   TRY_ALLOC(dt);
   TRY_ALLOC(dout);
   TRY_ALLOC(dp);
+  TRY_ALLOC(dfreq);
   AttnArgs t;
   t.q = dq;
   t.kcache = dk;
@@ -688,8 +725,7 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   t.n_kv_heads = n_kv_heads;
   t.msl = max_seq_len;
   t.nsplit = nsplit;
-  t.rotary_dim = rotary_dim;
-  t.rope_theta = rope_theta;
+  t.inv_freq = dfreq;
   t.params = dp;
   if (int rc = launch_attention(nullptr, t, nullptr)) return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
@@ -722,10 +758,18 @@ extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const
   uint16_t* dv = b.alloc<uint16_t>(kv, vcache);
   StepParams hp{0, pos, {0, 0}};
   StepParams* dp = b.alloc<StepParams>(1, &hp);
+  const std::vector<float> freqs = make_inv_freq(head_dim, rotary_dim, rope_theta);
+  float* dfreq = b.alloc<float>(freqs.size(), freqs.data());
+  float* dcs = b.alloc<float>(head_dim);
   TRY_ALLOC(dq);
   TRY_ALLOC(dk);
   TRY_ALLOC(dv);
   TRY_ALLOC(dp);
+  TRY_ALLOC(dfreq);
+  TRY_ALLOC(dcs);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(1), dim3(kBlock), 0, nullptr, (const float*)dfreq, dcs, head_dim / 2,
+                     (const StepParams*)dp);
+  HIP_TRY(nullptr, hipGetLastError());
   MatvecArgs a = mv_base();
   a.w0 = dw;
   a.row_step = 2L * dim;
@@ -746,6 +790,7 @@ extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const
   a.kcache = dk;
   a.vcache = dv;
   a.params = dp;
+  a.rope_cs = dcs;
   if (int rc = launch_matvec(nullptr, a, kEpiQkvRope, 2, device_cus(), nullptr)) return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
   HIP_TRY(nullptr, hipMemcpy(q_out, dq, qd * 4, hipMemcpyDeviceToHost));
@@ -761,7 +806,7 @@ extern "C" int yhip_test_argmax(const float* logits, int n, int* out) {
   int* dout = b.alloc<int>(1);
   TRY_ALLOC(dl);
   TRY_ALLOC(dout);
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kBlock), 0, nullptr, (const float*)dl, n, dout);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, nullptr, (const float*)dl, n, dout);
   HIP_TRY(nullptr, hipGetLastError());
   HIP_TRY(nullptr, hipDeviceSynchronize());
   HIP_TRY(nullptr, hipMemcpy(out, dout, sizeof(int), hipMemcpyDeviceToHost));
@@ -783,14 +828,20 @@ __global__ void fill_weights_kernel(uint16_t* w, size_t n, uint32_t seed) {
     w[i] = __builtin_bit_cast(uint16_t, (f16)u);
   }
 }
+// Plain streaming copy: the counter calibration reference (reads and writes exactly n16*16 bytes).
+__global__ void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
 __global__ void fill_float_kernel(float* p, size_t n, float base, float step) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     p[i] = base + step * (float)((i * 7919u) % 1000u);
 }
 }  // namespace
 
-extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, float* us_per_launch) {
-  if (!us_per_launch || rows <= 0 || cols <= 0 || copies <= 0 || reps <= 0 || warmup < 0 || kind < 0 || kind > 4)
+extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, int blocks_per_cu,
+                                 float* us_per_launch) {
+  if (!us_per_launch || rows <= 0 || cols <= 0 || copies <= 0 || reps <= 0 || warmup < 0 || kind < 0 || kind > 5)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   if ((kind == 0 || kind == 1 || kind == 4) && rows % 2) return fail(nullptr, YHIP_EINVAL, "rows must be even");
   const int R = (kind == 3) ? 1 : 2;
@@ -807,6 +858,11 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
   uint16_t* vc = b.alloc<uint16_t>((size_t)nkv * hd * msl);
   StepParams hp{0, 7, {0, 0}};
   StepParams* dp = b.alloc<StepParams>(1, &hp);
+  const std::vector<float> freqs = make_inv_freq(hd, hd, 1e6f);
+  float* dfreq = b.alloc<float>(freqs.size(), freqs.data());
+  float* dcs = b.alloc<float>(hd);
+  TRY_ALLOC(dfreq);
+  TRY_ALLOC(dcs);
   TRY_ALLOC(w);
   TRY_ALLOC(x);
   TRY_ALLOC(g);
@@ -817,12 +873,25 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
   hipLaunchKernelGGL(fill_weights_kernel, dim3(4096), dim3(256), 0, nullptr, w, per * copies, 12345u);
   hipLaunchKernelGGL(fill_float_kernel, dim3(64), dim3(256), 0, nullptr, x, (size_t)cols, -1.0f, 0.002f);
   hipLaunchKernelGGL(fill_float_kernel, dim3(64), dim3(256), 0, nullptr, g, (size_t)cols, 0.9f, 0.0002f);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(1), dim3(kBlock), 0, nullptr, (const float*)dfreq, dcs, hd / 2,
+                     (const StepParams*)dp);
+  uint16_t* copy_dst = nullptr;
+  if (kind == 5) {
+    if (per % 8) return fail(nullptr, YHIP_EINVAL, "copy size must be a multiple of 16 bytes");
+    copy_dst = b.alloc<uint16_t>(per);
+    TRY_ALLOC(copy_dst);
+  }
   HIP_TRY(nullptr, hipDeviceSynchronize());
   hipStream_t s;
   HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   const int cus = device_cus();
   auto launch = [&](int it) -> int {
     const uint16_t* base = w + per * (it % copies);
+    if (kind == 5) {
+      hipLaunchKernelGGL(copy_kernel, dim3(cus * 8), dim3(256), 0, s, (const u32x4*)base, (u32x4*)copy_dst,
+                         per * 2 / 16);
+      return hipGetLastError() == hipSuccess ? YHIP_OK : fail(nullptr, YHIP_EDEVICE, "copy launch failed");
+    }
     MatvecArgs a = mv_base();
     a.K = cols;
     a.x = x;
@@ -832,7 +901,7 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
       case 0:
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
         a.q_dim = rows - 2 * nkv * hd; a.kv_dim = nkv * hd; a.head_dim = hd; a.rotary_dim = hd; a.msl = msl;
-        a.rope_theta = 1e6f; a.kcache = kc; a.vcache = vc; a.params = dp; ek = kEpiQkvRope;
+        a.rope_theta = 1e6f; a.kcache = kc; a.vcache = vc; a.params = dp; a.rope_cs = dcs; ek = kEpiQkvRope;
         if (a.q_dim < 0) return fail(nullptr, YHIP_EINVAL, "QKV bench needs rows >= 2048");
         break;
       case 1:
@@ -849,7 +918,7 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
         break;
     }
-    return launch_matvec(nullptr, a, ek, R, cus, s);
+    return launch_matvec(nullptr, a, ek, R, cus, s, blocks_per_cu);
   };
   int rc = 0;
   for (int i = 0; i < warmup && !rc; ++i) rc = launch(i);

@@ -73,10 +73,10 @@ def lib():
         "yhip_test_attention": (ctypes.c_int, [_f32p, _u16p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                                ctypes.c_int, _f32p]),
-        "yhip_test_qkv": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p] + [ctypes.c_int] * 7
+        "yhip_test_qkv": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p] + [ctypes.c_int] * 6
                           + [ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p, _u16p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
-        "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
+        "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -123,8 +123,18 @@ class HipModel:
         h = ctypes.c_void_p()
         _check(lib().yhip_create(ctypes.byref(self.cfg), device, ctypes.byref(h)))
         self.h = h
+        self.owned = True
         if tensors is not None:
             self.upload(tensors)
+
+    @classmethod
+    def attach(cls, ctx_ptr, cfg):
+        """Non-owning view of a context created elsewhere (e.g. by a host-library session)."""
+        self = cls.__new__(cls)
+        self.cfg = make_config(cfg)
+        self.h = ctypes.c_void_p(ctx_ptr)
+        self.owned = False
+        return self
 
     def upload(self, tensors):
         c = self.cfg
@@ -180,9 +190,9 @@ class HipModel:
         return out
 
     def close(self):
-        if self.h:
+        if self.h and getattr(self, "owned", True):
             lib().yhip_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __enter__(self):
         return self
@@ -265,7 +275,7 @@ def argmax(logits):
     return out.value
 
 
-def bench_kernel(kind, rows, cols, copies=4, warmup=20, reps=200):
+def bench_kernel(kind, rows, cols, copies=4, warmup=20, reps=200, blocks_per_cu=0):
     us = ctypes.c_float()
-    _check(lib().yhip_bench_kernel(kind, rows, cols, copies, warmup, reps, ctypes.byref(us)))
+    _check(lib().yhip_bench_kernel(kind, rows, cols, copies, warmup, reps, blocks_per_cu, ctypes.byref(us)))
     return us.value
