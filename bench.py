@@ -99,6 +99,7 @@ def main():
     ap.add_argument("--graph", type=int, default=1, help="1: replay a captured hipGraph per step")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode budget (0 = skip)")
     ap.add_argument("--kernel-reps", type=int, default=200)
+    ap.add_argument("--attn-min-slice", type=int, default=0, help="override the attention slice floor")
     ap.add_argument("--profile-kernel", choices=["w13", "copy"], default=None,
                     help="run only that kernel (for hardware-counter passes) and exit")
     args = ap.parse_args()
@@ -133,9 +134,12 @@ def main():
     sess.hip(0)
     log(f"[bench] weights uploaded in {time.perf_counter() - t0:.1f} s")
     ctxp = sess.hip_ctx()
-    rc = hip.lib().yhip_set_option(ctxp, b"graph", int(args.graph))
-    if rc != 0:
-        raise RuntimeError(hip.lib().yhip_last_error(ctxp).decode())
+    opts = [(b"graph", int(args.graph))]
+    if args.attn_min_slice:
+        opts.append((b"attn_min_slice", args.attn_min_slice))
+    for key, val in opts:
+        if hip.lib().yhip_set_option(ctxp, key, val) != 0:
+            raise RuntimeError(hip.lib().yhip_last_error(ctxp).decode())
 
     prompt = host.uniform_ids(n_prompt, prompt_seed, cfg["vocab_size"])
     start_pos = 0

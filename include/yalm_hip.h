@@ -81,7 +81,10 @@ int yhip_kv_read(yhip_ctx* ctx, int layer, uint16_t* k_host, uint16_t* v_host);
 int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16_t* v_host);
 
 /* Options: "graph" (1 = replay a captured hipGraph per step, default; 0 = direct launches),
- * "attn_splits" (KV slices per kv head, default 256/n_kv_heads clamped to [1,64]). */
+ * "attn_splits" (most KV slices per kv head, default 512/n_kv_heads clamped to [1,64]),
+ * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64).
+ * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
+ * yhip_test_* hooks; 0 = the decode path's default). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 
 /* Debug read of a device activation after the last forward: which = 0 x [dim], 1 q [nh*hd],
@@ -126,6 +129,11 @@ int yhip_test_argmax(const float* logits, int n, int* out);
  * Writes the mean kernel time in microseconds. ---- */
 int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, int blocks_per_cu,
                       float* us_per_launch);
+
+/* ---- microbenchmark of the split-KV attention kernel over `copies` rotating KV caches (random
+ * fp16), at position kv_len - 1, `nsplit` slices of at least `min_slice` tokens. Mean microseconds. */
+int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, int max_seq_len, int kv_len, int nsplit,
+                         int min_slice, int copies, int warmup, int reps, float* us_per_launch);
 
 #ifdef __cplusplus
 }

@@ -27,9 +27,18 @@ def hip():
 RTOL = 1e-5
 
 
+@pytest.fixture(params=[0, 1], ids=["bpc_default", "bpc_1"])
+def bpc(request):
+    """Runs a test with the decode path's grid and with one workgroup per CU (many row groups per
+    wave, exercising the row loop of every fused matvec)."""
+    hip().set_test_bpc(request.param)
+    yield request.param
+    hip().set_test_bpc(0)
+
+
 @pytest.mark.parametrize("d,n", [(32, 64), (100, 256), (384, 768), (6144, 4096), (4096, 14336), (1000, 4096)])
 @pytest.mark.parametrize("norm", [False, True])
-def test_matvec_parity(d, n, norm):
+def test_matvec_parity(d, n, norm, bpc):
     rng = np.random.default_rng(d * 7 + n)
     w = f16(rng.standard_normal((d, n)) * 0.02)
     x = rng.standard_normal(n).astype(np.float32)
@@ -55,7 +64,7 @@ def test_matvec_one_hot_is_exact(n):
 
 @pytest.mark.parametrize("dim,hidden", [(64, 128), (256, 768), (4096, 14336)])
 @pytest.mark.parametrize("act", [1, 0])
-def test_ffn_parity(dim, hidden, act):
+def test_ffn_parity(dim, hidden, act, bpc):
     rng = np.random.default_rng(dim + hidden + act)
     w1 = f16(rng.standard_normal((hidden, dim)) * 0.02)
     w2 = f16(rng.standard_normal((dim, hidden)) * 0.02)
@@ -66,6 +75,25 @@ def test_ffn_parity(dim, hidden, act):
     got = hip().ffn(x, w1, w2, w3, gain=g, eps=1e-5, act=act, resid=resid)
     want = O.ffn(O.rmsnorm(x, g, 1e-5), w1, w2, w3, act) + resid
     assert npref.rel_l2(got, want) < RTOL
+
+
+@pytest.mark.parametrize("hidden", [1024, 4096, 8192])
+def test_swiglu_rows_exact_over_row_loop(hidden, bpc):
+    # Square down-projection with identity rows makes the FFN output equal hb itself, so every
+    # SwiGLU row (rows past the first pass of the row loop included) is checked on its own.
+    rng = np.random.default_rng(hidden)
+    dim = 4096
+    x = rng.standard_normal(dim).astype(np.float32)
+    w1 = f16(rng.standard_normal((hidden, dim)) * 0.02)
+    w3 = f16(rng.standard_normal((hidden, dim)) * 0.02)
+    w2 = np.zeros((dim, hidden), np.float16)
+    k = min(dim, hidden)
+    w2[np.arange(k), np.arange(k)] = 1.0
+    got = hip().ffn(x, w1, w2.view(np.uint16), w3, gain=None, act=1)[:k]
+    a = O.matmul_f16(x, w1)[:k]
+    b = O.matmul_f16(x, w3)[:k]
+    want = a / (1 + np.exp(-a)) * b
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
 
 
 ATTN_CASES = [
@@ -79,6 +107,11 @@ ATTN_CASES = [
     (128, 32, 8, 4096, 4096, 64),
     (128, 32, 8, 16448, 16417, 0),
     (128, 8, 1, 1024, 700, 1),
+    (64, 8, 8, 100, 99, 0),       # max_seq_len not a multiple of 8: scalar V path
+    (128, 32, 8, 4096, 64, 0),    # exactly one 64-token slice
+    (128, 32, 8, 4096, 65, 0),    # a second slice holding one token
+    (32, 8, 2, 520, 300, 5),
+    (16, 8, 1, 333, 333, 0),
 ]
 
 
@@ -168,7 +201,7 @@ def test_qkv_kv_write_bit_exact_at_pos0():
 
 @pytest.mark.parametrize("pos", [0, 5, 4095])
 @pytest.mark.parametrize("shape", [(256, 8, 2, 32, 512), (4096, 32, 8, 128, 4096)])
-def test_qkv_rope_parity(pos, shape):
+def test_qkv_rope_parity(pos, shape, bpc):
     dim, nh, nkv, hd, msl = shape
     rng = np.random.default_rng(pos + dim)
     wq = f16(rng.standard_normal((nh * hd, dim)) * 0.02)

@@ -166,31 +166,49 @@ __device__ __forceinline__ void group_rows(const MatvecArgs& a, int p, const uin
   }
 }
 
+// Epilogues run on every lane of the wave (all operands are wave-uniform after the reductions);
+// only lane 0 stores. Keeping the computation outside a lane-0 branch keeps the row loop's control
+// flow simple.
+// Operands an epilogue needs from memory, loaded together with the group's weights so that their
+// latency is not paid at the end of the group.
 template <int R, EpiKind EPI>
-__device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float (&acc)[R]) {
+__device__ __forceinline__ void epilogue_prefetch(const MatvecArgs& a, int p, float (&pre)[R]) {
+  if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) pre[r] = a.out[(long)p * R + r];
+  }
+}
+
+template <int R, EpiKind EPI>
+__device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float (&acc)[R], const float (&pre)[R],
+                                         int pos, const float* rope_cs, bool store) {
   if constexpr (EPI == kEpiStore) {
+    if (store)
 #pragma unroll
-    for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
+      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
   } else if constexpr (EPI == kEpiResidual) {
+    if (store)
 #pragma unroll
-    for (int r = 0; r < R; ++r) a.out[(long)p * R + r] += acc[r];
+      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = pre[r] + acc[r];
   } else if constexpr (EPI == kEpiSwiGLU) {
-    float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
-    a.out[p] = h * acc[R - 1];
+    const float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
+    const float v = h * acc[R - 1];
+    if (store) a.out[p] = v;
   } else {  // kEpiQkvRope: rows i = 2p, 2p+1 of [Wq; Wk; Wv]  (reference src/infer.cpp:279-305)
     const int i = 2 * p;
     float v0 = clipf(acc[0], a.qkv_clip);
     float v1 = clipf(acc[R - 1], a.qkv_clip);
-    const int pos = a.params->pos;
     if (i < a.q_dim + a.kv_dim) {  // RoPE on q and k (reference src/infer.cpp:202-215)
-      // (cos, sin) of pos * freq_j for this step, computed once per token by embed_kernel
+      // (cos, sin) of pos * freq_j for this step (computed once per token by embed_kernel, staged
+      // into LDS with the input vector)
       const int j = i % a.head_dim;
-      const float c = a.rope_cs[j], s = a.rope_cs[j + 1];
+      const float c = rope_cs[j], s = rope_cs[j + 1];
       const float r0 = v0 * c - v1 * s;
       const float r1 = v0 * s + v1 * c;
       v0 = r0;
       v1 = r1;
     }
+    if (!store) return;
     if (i < a.q_dim) {
       a.out[i] = v0;
       a.out[i + 1] = v1;
@@ -217,6 +235,8 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
 // exactly NPT float4 per thread, all loads issued before the first use; NPT == 0: any K % 4 == 0.
 template <int NPT>
 __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red) {
+  if (a.rope_cs)  // the step's RoPE table goes to LDS right after the input vector
+    for (int i = threadIdx.x; i < a.head_dim; i += kBlock) xs[a.K + i] = a.rope_cs[i];
   const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
   const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
   f32x4* o4 = reinterpret_cast<f32x4*>(xs);
@@ -286,21 +306,20 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
   int p = blockIdx.x * kWavesPerBlock + wave;
 
   if constexpr (KC > 0) {
-    // Single load site (one register buffer). The first iteration's loads are in flight while the
-    // workgroup stages x; waves without work still take part in the staging barrier.
+    // One register buffer: the first group's loads are in flight while the workgroup stages x
+    // (every wave takes part in the staging barrier); each later group is loaded at the end of
+    // the previous iteration, after its registers are dead.
     u32x4 wv[R][KC];
-    bool staged = false;
-    for (;;) {
-      if (p < a.groups) {
-        const uint16_t* rows[R];
-        group_rows<R>(a, p, rows);
-        load_group<KC, R>(wv, rows, lane);
-      }
-      if (!staged) {
-        stage_input<KC / 2>(a, xs, red);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
-        staged = true;
-      }
-      if (p >= a.groups) break;
+    float pre[R];
+    const int pos = EPI == kEpiQkvRope ? a.params->pos : 0;
+    if (p < a.groups) {
+      const uint16_t* rows[R];
+      group_rows<R>(a, p, rows);
+      load_group<KC, R>(wv, rows, lane);
+      epilogue_prefetch<R, EPI>(a, p, pre);
+    }
+    stage_input<KC / 2>(a, xs, red);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+    while (p < a.groups) {
       float acc[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -314,15 +333,24 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane == 0) epilogue<R, EPI>(a, p, acc);
+      epilogue<R, EPI>(a, p, acc, pre, pos, xs + a.K, lane == 0);
       p += wave_stride;
+      if (p < a.groups) {
+        const uint16_t* rows[R];
+        group_rows<R>(a, p, rows);
+        load_group<KC, R>(wv, rows, lane);
+        epilogue_prefetch<R, EPI>(a, p, pre);
+      }
     }
   } else {
     stage_input<0>(a, xs, red);
     const int nch = a.K >> 3;
+    const int pos = EPI == kEpiQkvRope ? a.params->pos : 0;
     for (; p < a.groups; p += wave_stride) {
       const uint16_t* rows[R];
       group_rows<R>(a, p, rows);
+      float pre[R];
+      epilogue_prefetch<R, EPI>(a, p, pre);
       float acc[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -335,7 +363,7 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane == 0) epilogue<R, EPI>(a, p, acc);
+      epilogue<R, EPI>(a, p, acc, pre, pos, xs + a.K, lane == 0);
     }
   }
 }
@@ -390,8 +418,8 @@ __device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)
 // Split-KV GQA decode attention (reference src/infer.cpp:218-250, 327-336).
 //
 // Workgroup (g, s) handles kv head g and the s-th slice of [0, kv_len) for all G query heads
-// that share g, so each K/V byte is read once per token. Slices are at least kMinSlice tokens:
-//   chunk = max(kMinSlice, roundup(ceil(kv_len / nsplit), 64)),  active = ceil(kv_len / chunk)
+// that share g, so each K/V byte is read once per token. Slices are at least min_slice tokens:
+//   chunk = max(min_slice, roundup(ceil(kv_len / nsplit), 64)),  active = ceil(kv_len / chunk)
 // Workgroups past `active` exit at once. With one active slice the workgroup writes the output
 // directly; otherwise each writes (max, sum, acc) per head and the last to finish (atomic ticket)
 // merges them. Scores for a 256-token tile go to LDS; an online softmax keeps (max, sum, acc).
@@ -406,48 +434,82 @@ struct AttnArgs {
   unsigned* tickets;     // [nkv]
   float* out;            // [nh][hd]
   int head_dim, n_heads, n_kv_heads, msl, nsplit;
+  int min_slice;          // smallest KV slice per workgroup (multiple of 64)
   const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
 };
 
-constexpr int kAttnTile = 256;
 constexpr int kMaxGroup = 8;
-constexpr int kMinSlice = 256;
 
-__device__ __forceinline__ int attn_chunk(int kv_len, int nsplit) {
+__device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice) {
   int chunk = (kv_len + nsplit - 1) / nsplit;
   chunk = (chunk + 63) & ~63;
-  return chunk < kMinSlice ? kMinSlice : chunk;
+  return chunk < min_slice ? min_slice : chunk;
 }
 
+// Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32); every lane of a group gets the
+// group total. DPP quad permutes and row mirrors, plus one cross-row swap for N = 32.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if constexpr (N >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+  if constexpr (N >= 16) v += dpp_mov<0x140>(v); // row_mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+  return v;
+}
+
+// K and V registers for one tile of one thread (loaded one tile ahead of use).
+template <int CPL, int DPT>
+struct AttnTileRegs {
+  u32x4 k[CPL][2];  // this thread's 16-dim K chunks of its token
+  u32x4 v[DPT];     // 8 consecutive tokens of each of this thread's V rows
+};
+
+// HD: head_dim; G: query heads per kv head.
+template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
-  __shared__ float qs[kMaxGroup * 128];
-  __shared__ float sc[kMaxGroup][kAttnTile];
-  __shared__ float red[kMaxGroup][kWavesPerBlock];
-  __shared__ float accs[kMaxGroup * 256];
+  // Score phase: LPT lanes per token, each owning CPL 16-dim chunks of K; TT tokens per tile.
+  // Value phase: LPD adjacent lanes cover one V row's TT tokens (8 tokens = 16 bytes each, so a
+  // wave instruction reads whole 128-byte lines); thread owns DPT rows d = dgrp + NDG*m and
+  // tokens 8*oct .. 8*oct+7 of the tile. Partial sums stay per lane and are reduced over the LPD
+  // lanes once, after the last tile. Every tile issues the same loads (addresses clamped into the
+  // cache, results masked), so the compiler waits only for the tile it is about to use.
+  constexpr int LPT = HD >= 64 ? 4 : HD / 16;
+  constexpr int CPL = HD / 16 / LPT;
+  constexpr int TT = kBlock / LPT;
+  constexpr int LPD = TT / 8;
+  constexpr int NDG = kBlock / LPD;
+  constexpr int DPT = HD / NDG;
+  static_assert(DPT >= 1 && NDG * DPT == HD && LPD <= kWave && G >= 1 && G <= kMaxGroup, "tile layout");
+  __shared__ float qs[G * HD];
+  __shared__ __attribute__((aligned(16))) float ps[G][TT];
+  __shared__ float red[2][G][kWavesPerBlock];
   __shared__ unsigned last_flag;
 
   const int g = blockIdx.x, split = blockIdx.y;
-  const int hd = a.head_dim;
-  const int G = a.n_heads / a.n_kv_heads;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const Positions ps = positions(a.params->pos, a.msl);
-  const int kv_len = ps.kv_len;
-  const int chunk = attn_chunk(kv_len, a.nsplit);
+  const Positions pss = positions(a.params->pos, a.msl);
+  const int kv_len = pss.kv_len;
+  const int chunk = attn_chunk(kv_len, a.nsplit, a.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
   if (split >= active) return;
   const int t_begin = split * chunk;
   const int t_end = min(kv_len, t_begin + chunk);
-  const long head_off = (long)g * hd * a.msl;
+  const long head_off = (long)g * HD * a.msl;
   uint16_t* kh = a.kcache + head_off;
   const uint16_t* vh = a.vcache + head_off;
 
-  if (ps.kv_sink > 0 && split == 0) {
+  if (pss.kv_sink > 0 && split == 0) {
     // Re-rotate sink keys r < kv_sink by angle freq*1 in place (fp16 round trip as reference).
-    for (int e = tid; e < ps.kv_sink * (hd / 2); e += kBlock) {
-      const int r = e / (hd / 2);
-      const int j = 2 * (e % (hd / 2));
+    for (int e = tid; e < pss.kv_sink * (HD / 2); e += kBlock) {
+      const int r = e / (HD / 2);
+      const int j = 2 * (e % (HD / 2));
       const float freq = a.inv_freq[j / 2];
       const float c = cosf(freq), s = sinf(freq);
       uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
@@ -459,150 +521,167 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  for (int e = tid; e < G * hd; e += kBlock) qs[e] = a.q[(long)g * G * hd + e];
-  float m_run[kMaxGroup], l_run[kMaxGroup];
+  const int tok_l = tid / LPT, sub = tid % LPT;
+  const int oct = tid % LPD, dgrp = tid / LPD;
+  const bool vec_ok = (a.msl & 7) == 0;
+  const int vmax = vec_ok ? a.msl - 8 : 0;
+
+  auto load_tile = [&](int t0, AttnTileRegs<CPL, DPT>& r) {
+    const int tok = min(t0 + tok_l, a.msl - 1);
 #pragma unroll
-  for (int h = 0; h < kMaxGroup; ++h) {
+    for (int cc = 0; cc < CPL; ++cc) {
+      const u32x4* kp = reinterpret_cast<const u32x4*>(kh + (long)(sub * CPL + cc) * 16 * a.msl + (long)tok * 16);
+      r.k[cc][0] = kp[0];
+      r.k[cc][1] = kp[1];
+    }
+    if (vec_ok) {
+      const int tv = min(t0 + 8 * oct, vmax);
+#pragma unroll
+      for (int m = 0; m < DPT; ++m)
+        r.v[m] = *reinterpret_cast<const u32x4*>(vh + (long)(dgrp + NDG * m) * a.msl + tv);
+    }
+  };
+
+  for (int e = tid; e < G * HD; e += kBlock) qs[e] = a.q[(long)g * G * HD + e];
+  AttnTileRegs<CPL, DPT> cur, nxt;
+  load_tile(t_begin, cur);
+  float m_run[G], l_run[G], acc[DPT][G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
     m_run[h] = kNegBig;
     l_run[h] = 0.f;
-  }
-  // V phase mapping: thread owns dim i = tid % hd, token part tid / hd.
-  const int parts = kBlock / hd;
-  const int i_dim = tid % hd;
-  const int part = tid / hd;
-  const int tpp = kAttnTile / parts;  // tokens per part per tile
-  float acc[kMaxGroup];
 #pragma unroll
-  for (int h = 0; h < kMaxGroup; ++h) acc[h] = 0.f;
-  const bool vec_ok = (a.msl & 7) == 0;
+    for (int m = 0; m < DPT; ++m) acc[m][h] = 0.f;
+  }
+  const float inv_sqrt_hd = 1.0f / sqrtf((float)HD);
   __syncthreads();
 
-  for (int t0 = t_begin; t0 < t_end; t0 += kAttnTile) {
-    // scores
-    const int tok = t0 + tid;
-    float s[kMaxGroup];
+  for (int t0 = t_begin; t0 < t_end; t0 += TT) {
+    load_tile(t0 + TT < t_end ? t0 + TT : t0, nxt);  // next tile (or this one again) in flight
+    const int tok = t0 + tok_l;
+    const bool valid = tok < t_end;
+    // scores: partial dots over this lane's chunks, then summed over the LPT lanes of the token
+    float s[G];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) s[h] = 0.f;
-    if (tok < t_end) {
-      for (int c = 0; c < hd / 16; ++c) {
-        const u32x4* kp = reinterpret_cast<const u32x4*>(kh + (long)c * 16 * a.msl + (long)tok * 16);
-        const f16x8 k0 = __builtin_bit_cast(f16x8, kp[0]);
-        const f16x8 k1 = __builtin_bit_cast(f16x8, kp[1]);
+    for (int h = 0; h < G; ++h) s[h] = 0.f;
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-          if (h < G) {
-            const float* qh = qs + h * hd + c * 16;
-            float d = s[h];
+    for (int cc = 0; cc < CPL; ++cc) {
+      const f16x8 k0 = __builtin_bit_cast(f16x8, cur.k[cc][0]);
+      const f16x8 k1 = __builtin_bit_cast(f16x8, cur.k[cc][1]);
+      const int c = sub * CPL + cc;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qh[e], (float)k0[e], d);
+      for (int h = 0; h < G; ++h) {
+        const float* qh = qs + h * HD + c * 16;
+        float d = s[h];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qh[8 + e], (float)k1[e], d);
-            s[h] = d;
-          }
+        for (int e = 0; e < 8; ++e) d = fmaf(qh[e], (float)k0[e], d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qh[8 + e], (float)k1[e], d);
+        s[h] = d;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      s[h] = lane_group_sum<LPT>(s[h]);
+      s[h] = valid ? s[h] * inv_sqrt_hd : kNegBig;
+      const float m = wave_max(s[h]);
+      if (lane == 0) red[0][h][wave] = m;
+    }
+    __syncthreads();
+    float corr[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float m = red[0][h][0];
+#pragma unroll
+      for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, red[0][h][w]);
+      const float m_new = fmaxf(m_run[h], m);
+      corr[h] = expf(m_run[h] - m_new);
+      m_run[h] = m_new;
+      const float p = valid ? expf(s[h] - m_new) : 0.f;
+      const bool mine = sub == (h % LPT);  // each (token, head) probability stored and summed once
+      if (mine) ps[h][tok_l] = p;
+      const float t = wave_sum(mine ? p : 0.f);
+      if (lane == 0) red[1][h][wave] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWavesPerBlock; ++w) t += red[1][h][w];
+      l_run[h] = l_run[h] * corr[h] + t;
+#pragma unroll
+      for (int m = 0; m < DPT; ++m) acc[m][h] *= corr[h];
+    }
+    // values: acc[m][h] += sum over this lane's 8 tokens of p[h][t] * V[d_m][t]
+    const int tv = t0 + 8 * oct;
+    if (vec_ok && tv + 8 <= t_end) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&ps[h][8 * oct]);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&ps[h][8 * oct + 4]);
+#pragma unroll
+        for (int m = 0; m < DPT; ++m) {
+          const f16x8 v8 = __builtin_bit_cast(f16x8, cur.v[m]);
+          float d = acc[m][h];
+          d = fmaf(p0[0], (float)v8[0], d);
+          d = fmaf(p0[1], (float)v8[1], d);
+          d = fmaf(p0[2], (float)v8[2], d);
+          d = fmaf(p0[3], (float)v8[3], d);
+          d = fmaf(p1[0], (float)v8[4], d);
+          d = fmaf(p1[1], (float)v8[5], d);
+          d = fmaf(p1[2], (float)v8[6], d);
+          d = fmaf(p1[3], (float)v8[7], d);
+          acc[m][h] = d;
         }
       }
+    } else if (tv < t_end) {  // partial run at the end of the slice: element by element
+      for (int e = 0; e < 8; ++e) {
+        const int t = tv + e;
+        if (t < t_end) {
 #pragma unroll
-      for (int h = 0; h < kMaxGroup; ++h) s[h] = s[h] / sqrtf((float)hd);
-    } else {
+          for (int m = 0; m < DPT; ++m) {
+            const float v = (float)__builtin_bit_cast(f16, vh[(long)(dgrp + NDG * m) * a.msl + t]);
 #pragma unroll
-      for (int h = 0; h < kMaxGroup; ++h) s[h] = kNegBig;
-    }
-    // tile max per head
-    float corr[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (h < G) {
-        float m = wave_max(s[h]);
-        if (lane == 0) red[h][wave] = m;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (h < G) {
-        float m = red[h][0];
-#pragma unroll
-        for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, red[h][w]);
-        const float m_new = fmaxf(m_run[h], m);
-        corr[h] = expf(m_run[h] - m_new);
-        m_run[h] = m_new;
-        const float p = tok < t_end ? expf(s[h] - m_new) : 0.f;
-        sc[h][tid] = p;
-        s[h] = p;
-      }
-    }
-    __syncthreads();  // red reused below; sc complete
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (h < G) {
-        float ps_ = wave_sum(s[h]);
-        if (lane == 0) red[h][wave] = ps_;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (h < G) {
-        float t = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) t += red[h][w];
-        l_run[h] = l_run[h] * corr[h] + t;
-        acc[h] *= corr[h];
-      }
-    }
-    // V accumulation over this part's tokens
-    const int tb = t0 + part * tpp;
-    const int te = min(t_end, tb + tpp);
-    const uint16_t* vrow = vh + (long)i_dim * a.msl;
-    int t = tb;
-    if (vec_ok) {
-      for (; t + 8 <= te; t += 8) {
-        const f16x8 v8 = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(vrow + t));
-        const int k = t - t0;
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-          if (h < G) {
-            float d = acc[h];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(sc[h][k + e], (float)v8[e], d);
-            acc[h] = d;
+            for (int h = 0; h < G; ++h) acc[m][h] = fmaf(ps[h][8 * oct + e], v, acc[m][h]);
           }
         }
       }
     }
-    for (; t < te; ++t) {
-      const float v = (float)__builtin_bit_cast(f16, vrow[t]);
-      const int k = t - t0;
-#pragma unroll
-      for (int h = 0; h < kMaxGroup; ++h)
-        if (h < G) acc[h] = fmaf(sc[h][k], v, acc[h]);
-    }
-    __syncthreads();  // sc / red reused by the next tile
+    cur = nxt;
+    __syncthreads();  // ps / red are rewritten by the next tile
   }
 
-  // Merge the token parts of this workgroup.
-  for (int h = 0; h < G; ++h) accs[h * 256 + tid] = acc[h];
-  __syncthreads();
+  // Reduce the value sums over the LPD lanes of each row group (adjacent lanes).
+#pragma unroll
+  for (int m = 0; m < DPT; ++m)
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[m][h] = lane_group_sum<LPD>(acc[m][h]);
+  const bool writer = oct == 0;
   if (active == 1) {  // the only slice: final normalisation here
-    for (int e = tid; e < G * hd; e += kBlock) {
-      const int h = e / hd, i = e % hd;
-      float o = 0.f;
-      for (int pt = 0; pt < parts; ++pt) o += accs[h * 256 + pt * hd + i];
-      a.out[(long)(g * G + h) * hd + i] = o / l_run[h];
-    }
+    if (writer)
+#pragma unroll
+      for (int m = 0; m < DPT; ++m)
+#pragma unroll
+        for (int h = 0; h < G; ++h) a.out[(long)(g * G + h) * HD + dgrp + NDG * m] = acc[m][h] / l_run[h];
     return;
   }
-  const int stride = hd + 2;
-  for (int e = tid; e < G * hd; e += kBlock) {
-    const int h = e / hd, i = e % hd;
-    float o = 0.f;
-    for (int pt = 0; pt < parts; ++pt) o += accs[h * 256 + pt * hd + i];
-    float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
-    store_shared(dst + i, o);
-    if (i == 0) {
-      store_shared(dst + hd, m_run[h]);
-      store_shared(dst + hd + 1, l_run[h]);
-    }
+  const int stride = HD + 2;
+  if (writer) {
+#pragma unroll
+    for (int m = 0; m < DPT; ++m)
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+        store_shared(a.partial + ((long)(g * G + h) * a.nsplit + split) * stride + dgrp + NDG * m, acc[m][h]);
+  }
+  if (tid < G) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      if (h == tid) {
+        float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
+        store_shared(dst + HD, m_run[h]);
+        store_shared(dst + HD + 1, l_run[h]);
+      }
   }
   publish();
   __syncthreads();
@@ -612,19 +691,19 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   }
   __syncthreads();
   if (!last_flag) return;
-  for (int e = tid; e < G * hd; e += kBlock) {
-    const int h = e / hd, i = e % hd;
+  for (int e = tid; e < G * HD; e += kBlock) {
+    const int h = e / HD, i = e % HD;
     const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride;
     float M = kNegBig;
-    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, load_shared(src + sp * stride + hd));
+    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, load_shared(src + sp * stride + HD));
     float L = 0.f, O = 0.f;
     for (int sp = 0; sp < active; ++sp) {
-      const float* ps_ = src + sp * stride;
-      const float w = expf(load_shared(ps_ + hd) - M);
-      L = fmaf(load_shared(ps_ + hd + 1), w, L);
-      O = fmaf(load_shared(ps_ + i), w, O);
+      const float* pp = src + sp * stride;
+      const float w = expf(load_shared(pp + HD) - M);
+      L = fmaf(load_shared(pp + HD + 1), w, L);
+      O = fmaf(load_shared(pp + i), w, O);
     }
-    a.out[(long)(g * G + h) * hd + i] = O / L;
+    a.out[(long)(g * G + h) * HD + i] = O / L;
   }
   if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

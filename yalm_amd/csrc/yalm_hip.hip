@@ -22,6 +22,9 @@ using namespace yk;
 namespace {
 
 thread_local std::string g_thread_err;
+// Workgroups per CU for the kernel-level test hooks (0 = the decode path's default); set with
+// yhip_set_option(NULL, "test_bpc", n) so tests can force many row groups per wave.
+int g_test_bpc = 0;
 
 struct LayerW {
   uint16_t* wqkv = nullptr;  // [q_dim + 2*kv_dim][dim]
@@ -77,6 +80,7 @@ struct yhip_ctx {
 
   bool use_graph = true;
   int attn_splits = 32;
+  int attn_min_slice = 64;
   hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // hydrate, logits, argmax
 
   int q_dim() const { return c.n_heads * c.head_dim; }
@@ -122,7 +126,8 @@ int default_bpc(int K) { return K >= 8192 ? 1 : 2; }
 
 template <int KC, int R, EpiKind EPI>
 void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
-  const size_t lds = (16 + (size_t)a.K) * sizeof(float);
+  // reduction scratch + input vector (+ the RoPE table for the QKV epilogue)
+  const size_t lds = (16 + (size_t)a.K + (a.rope_cs ? (size_t)a.head_dim : 0)) * sizeof(float);
   hipLaunchKernelGGL((matvec_kernel<KC, R, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
 }
 
@@ -140,8 +145,8 @@ void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
 
 // Chooses the instantiation for row length K, rows-per-group R and epilogue kind.
 int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s, int bpc = 0) {
-  if (a.K % 8 != 0 || (16 + (size_t)a.K) * sizeof(float) > 65536)
-    return fail(ctx, YHIP_EINVAL, "matvec: row length must be a multiple of 8 and at most 16368");
+  if (a.K % 8 != 0 || (16 + (size_t)a.K + 128) * sizeof(float) > 65536)
+    return fail(ctx, YHIP_EINVAL, "matvec: row length must be a multiple of 8 and at most 16240");
   if (R != 1 && R != 2) return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
   if (bpc <= 0) bpc = default_bpc(a.K);
   int blocks = (a.groups + kWavesPerBlock - 1) / kWavesPerBlock;
@@ -165,8 +170,28 @@ MatvecArgs mv_base() {
   return a;
 }
 
+template <int HD>
+bool launch_attention_hd(const AttnArgs& a, hipStream_t s) {
+  const dim3 grid(a.n_kv_heads, a.nsplit);
+  switch (a.n_heads / a.n_kv_heads) {
+    case 1: hipLaunchKernelGGL((attention_kernel<HD, 1>), grid, dim3(kBlock), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((attention_kernel<HD, 2>), grid, dim3(kBlock), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((attention_kernel<HD, 4>), grid, dim3(kBlock), 0, s, a); return true;
+    case 8: hipLaunchKernelGGL((attention_kernel<HD, 8>), grid, dim3(kBlock), 0, s, a); return true;
+    default: return false;
+  }
+}
+
 int launch_attention(yhip_ctx* ctx, const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(attention_kernel, dim3(a.n_kv_heads, a.nsplit), dim3(kBlock), 0, s, a);
+  bool ok = false;
+  switch (a.head_dim) {
+    case 16: ok = launch_attention_hd<16>(a, s); break;
+    case 32: ok = launch_attention_hd<32>(a, s); break;
+    case 64: ok = launch_attention_hd<64>(a, s); break;
+    case 128: ok = launch_attention_hd<128>(a, s); break;
+    default: break;
+  }
+  if (!ok) return fail(ctx, YHIP_EINVAL, "unsupported attention shape (head_dim 16/32/64/128, 1/2/4/8 q heads per kv head)");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention launch: ") + hipGetErrorString(e));
   return YHIP_OK;
@@ -175,8 +200,11 @@ int launch_attention(yhip_ctx* ctx, const AttnArgs& a, hipStream_t s) {
 int check_attn_shape(yhip_ctx* ctx, int hd, int nh, int nkv) {
   if (!(hd == 16 || hd == 32 || hd == 64 || hd == 128))
     return fail(ctx, YHIP_EINVAL, "head_dim must be 16, 32, 64 or 128");
-  if (nkv <= 0 || nkv > 64 || nh % nkv != 0 || nh / nkv > kMaxGroup)
-    return fail(ctx, YHIP_EINVAL, "n_heads must be a multiple of n_kv_heads (at most 64) with at most 8 query heads per kv head");
+  if (nkv <= 0 || nkv > 64 || nh % nkv != 0)
+    return fail(ctx, YHIP_EINVAL, "n_heads must be a multiple of n_kv_heads (at most 64)");
+  const int G = nh / nkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(ctx, YHIP_EINVAL, "query heads per kv head must be 1, 2, 4 or 8");
   return YHIP_OK;
 }
 
@@ -228,6 +256,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     t.n_kv_heads = c.n_kv_heads;
     t.msl = c.max_seq_len;
     t.nsplit = ctx->attn_splits;
+    t.min_slice = ctx->attn_min_slice;
     t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
     if ((rc = launch_attention(ctx, t, s))) return rc;
@@ -342,8 +371,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
     return fail(nullptr, YHIP_EINVAL, "invalid config dimensions");
   if (c.dim % 8 || c.hidden_dim % 8 || (c.n_heads * c.head_dim) % 8)
     return fail(nullptr, YHIP_EINVAL, "dim, hidden_dim and n_heads*head_dim must be multiples of 8");
-  if (c.dim > 16368 || c.hidden_dim > 16368 || c.n_heads * c.head_dim > 16368)
-    return fail(nullptr, YHIP_EINVAL, "row lengths above 16368 are not supported");
+  if (c.dim > 16240 || c.hidden_dim > 16240 || c.n_heads * c.head_dim > 16240)
+    return fail(nullptr, YHIP_EINVAL, "row lengths above 16240 are not supported");
   if (c.act != YHIP_ACT_GELU && c.act != YHIP_ACT_SILU) return fail(nullptr, YHIP_EINVAL, "unknown activation");
   if (int rc = check_attn_shape(nullptr, c.head_dim, c.n_heads, c.n_kv_heads)) return rc;
   int ndev = 0;
@@ -352,7 +381,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   yhip_ctx* ctx = new yhip_ctx();
   ctx->c = c;
   ctx->device = device_ordinal;
-  ctx->attn_splits = std::max(1, std::min(64, 256 / std::max(1, c.n_kv_heads)));
+  ctx->attn_splits = std::max(1, std::min(64, 512 / std::max(1, c.n_kv_heads)));
   auto bail = [&](int rc) {
     yhip_destroy(ctx);
     return rc;
@@ -537,7 +566,15 @@ extern "C" int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, c
 }
 
 extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
-  if (!ctx || !key) return fail(ctx, YHIP_EINVAL, "null argument");
+  if (!key) return fail(ctx, YHIP_EINVAL, "null argument");
+  if (!ctx) {
+    if (!strcmp(key, "test_bpc")) {
+      if (value < 0 || value > 64) return fail(nullptr, YHIP_EINVAL, "test_bpc must be in [0, 64]");
+      g_test_bpc = value;
+      return YHIP_OK;
+    }
+    return fail(nullptr, YHIP_EINVAL, std::string("unknown process-wide option ") + key);
+  }
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
   if (!strcmp(key, "graph")) {
@@ -545,6 +582,9 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "attn_splits")) {
     if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "attn_splits must be in [1, 64]");
     ctx->attn_splits = value;
+  } else if (!strcmp(key, "attn_min_slice")) {
+    if (value < 64 || value % 64) return fail(ctx, YHIP_EINVAL, "attn_min_slice must be a positive multiple of 64");
+    ctx->attn_min_slice = value;
   } else {
     return fail(ctx, YHIP_EINVAL, std::string("unknown option ") + key);
   }
@@ -634,7 +674,8 @@ extern "C" int yhip_test_matvec(const float* x, const float* gain, float eps, co
   a.row_step = (long)R * n;
   a.r_step = n;
   a.groups = d / R;
-  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, R, device_cus(), nullptr)) return rc;
+  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, R, device_cus(), nullptr, g_test_bpc))
+    return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
   HIP_TRY(nullptr, hipMemcpy(out, dout, (size_t)d * 4, hipMemcpyDeviceToHost));
   return YHIP_OK;
@@ -670,7 +711,7 @@ extern "C" int yhip_test_ffn(const float* x, const float* gain, float eps, const
   a.eps = eps;
   a.out = dh;
   a.act = act;
-  if (int rc = launch_matvec(nullptr, a, kEpiSwiGLU, 2, cus, nullptr)) return rc;
+  if (int rc = launch_matvec(nullptr, a, kEpiSwiGLU, 2, cus, nullptr, g_test_bpc)) return rc;
   a = mv_base();
   a.w0 = d2;
   a.row_step = hidden_dim;
@@ -679,7 +720,8 @@ extern "C" int yhip_test_ffn(const float* x, const float* gain, float eps, const
   a.K = hidden_dim;
   a.x = dh;
   a.out = dout;
-  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, 1, cus, nullptr)) return rc;
+  if (int rc = launch_matvec(nullptr, a, resid ? kEpiResidual : kEpiStore, 1, cus, nullptr, g_test_bpc))
+    return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
   HIP_TRY(nullptr, hipMemcpy(out, dout, (size_t)dim * 4, hipMemcpyDeviceToHost));
   return YHIP_OK;
@@ -725,6 +767,7 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   t.n_kv_heads = n_kv_heads;
   t.msl = max_seq_len;
   t.nsplit = nsplit;
+  t.min_slice = 64;
   t.inv_freq = dfreq;
   t.params = dp;
   if (int rc = launch_attention(nullptr, t, nullptr)) return rc;
@@ -791,7 +834,7 @@ extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const
   a.vcache = dv;
   a.params = dp;
   a.rope_cs = dcs;
-  if (int rc = launch_matvec(nullptr, a, kEpiQkvRope, 2, device_cus(), nullptr)) return rc;
+  if (int rc = launch_matvec(nullptr, a, kEpiQkvRope, 2, device_cus(), nullptr, g_test_bpc)) return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
   HIP_TRY(nullptr, hipMemcpy(q_out, dq, qd * 4, hipMemcpyDeviceToHost));
   HIP_TRY(nullptr, hipMemcpy(kcache, dk, kv * 2, hipMemcpyDeviceToHost));
@@ -921,6 +964,73 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
     return launch_matvec(nullptr, a, ek, R, cus, s, blocks_per_cu);
   };
   int rc = 0;
+  for (int i = 0; i < warmup && !rc; ++i) rc = launch(i);
+  hipEvent_t e0, e1;
+  hipEventCreate(&e0);
+  hipEventCreate(&e1);
+  hipEventRecord(e0, s);
+  for (int i = 0; i < reps && !rc; ++i) rc = launch(warmup + i);
+  hipEventRecord(e1, s);
+  hipError_t e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  hipStreamDestroy(s);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, hipGetErrorString(e));
+  *us_per_launch = ms * 1000.0f / reps;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, int max_seq_len, int kv_len, int nsplit,
+                                    int min_slice, int copies, int warmup, int reps, float* us_per_launch) {
+  if (!us_per_launch || kv_len <= 0 || kv_len > max_seq_len || copies <= 0 || reps <= 0 || warmup < 0 || nsplit < 1 ||
+      nsplit > 64 || min_slice < 64 || min_slice % 64)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
+  const size_t kv = (size_t)n_kv_heads * head_dim * max_seq_len;
+  DevBufs b;
+  uint16_t* caches = b.alloc<uint16_t>(kv * 2 * copies);
+  float* dq = b.alloc<float>((size_t)n_heads * head_dim);
+  float* dpart = b.alloc<float>((size_t)n_heads * 64 * (head_dim + 2));
+  unsigned* dt = b.alloc<unsigned>(64);
+  float* dout = b.alloc<float>((size_t)n_heads * head_dim);
+  StepParams hp{0, kv_len - 1, {0, 0}};
+  StepParams* dp = b.alloc<StepParams>(1, &hp);
+  const std::vector<float> freqs = make_inv_freq(head_dim, head_dim, 1e6f);
+  float* dfreq = b.alloc<float>(freqs.size(), freqs.data());
+  TRY_ALLOC(caches);
+  TRY_ALLOC(dq);
+  TRY_ALLOC(dpart);
+  TRY_ALLOC(dt);
+  TRY_ALLOC(dout);
+  TRY_ALLOC(dp);
+  TRY_ALLOC(dfreq);
+  hipLaunchKernelGGL(fill_weights_kernel, dim3(4096), dim3(256), 0, nullptr, caches, kv * 2 * copies, 777u);
+  hipLaunchKernelGGL(fill_float_kernel, dim3(64), dim3(256), 0, nullptr, dq, (size_t)n_heads * head_dim, -1.0f, 0.002f);
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  hipStream_t s;
+  HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  int rc = 0;
+  auto launch = [&](int it) {
+    AttnArgs t;
+    t.q = dq;
+    t.kcache = caches + kv * 2 * (it % copies);
+    t.vcache = t.kcache + kv;
+    t.partial = dpart;
+    t.tickets = dt;
+    t.out = dout;
+    t.head_dim = head_dim;
+    t.n_heads = n_heads;
+    t.n_kv_heads = n_kv_heads;
+    t.msl = max_seq_len;
+    t.nsplit = nsplit;
+    t.min_slice = min_slice;
+    t.inv_freq = dfreq;
+    t.params = dp;
+    return launch_attention(nullptr, t, s);
+  };
   for (int i = 0; i < warmup && !rc; ++i) rc = launch(i);
   hipEvent_t e0, e1;
   hipEventCreate(&e0);

@@ -25,7 +25,7 @@ EXPORTS = (
     "yhip_create", "yhip_destroy", "yhip_upload_layer", "yhip_upload_globals", "yhip_forward",
     "yhip_forward_argmax", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
-    "yhip_test_qkv", "yhip_test_argmax", "yhip_bench_kernel",
+    "yhip_test_qkv", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
 )
 
 
@@ -77,6 +77,7 @@ def lib():
                           + [ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p, _u16p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
+        "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -208,6 +209,11 @@ class HipModel:
 
 
 # ---- kernel-level hooks --------------------------------------------------------------------
+def set_test_bpc(n):
+    """Workgroups per CU used by the kernel-level hooks (0 = the decode path's default)."""
+    _check(lib().yhip_set_option(None, b"test_bpc", int(n)))
+
+
 def matvec(x, w, gain=None, eps=1e-5, resid=None):
     d, n = w.shape
     x, xp = _f32(x)
@@ -278,4 +284,12 @@ def argmax(logits):
 def bench_kernel(kind, rows, cols, copies=4, warmup=20, reps=200, blocks_per_cu=0):
     us = ctypes.c_float()
     _check(lib().yhip_bench_kernel(kind, rows, cols, copies, warmup, reps, blocks_per_cu, ctypes.byref(us)))
+    return us.value
+
+
+def bench_attention(kv_len, max_seq_len=4096, nsplit=32, min_slice=64, head_dim=128, n_heads=32, n_kv_heads=8,
+                    copies=8, warmup=10, reps=100):
+    us = ctypes.c_float()
+    _check(lib().yhip_bench_attention(head_dim, n_heads, n_kv_heads, max_seq_len, kv_len, nsplit, min_slice, copies,
+                                      warmup, reps, ctypes.byref(us)))
     return us.value
