@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Batch-1 fp16 decode benchmark on one MI355X, Mistral-7B-shaped random-init weights.
 
-    python bench.py [--steps K] [--warmup W] [--workload decode|long|attn] [--graph 0|1]
+    python bench.py [--steps K] [--warmup W] [--workload decode|long|attn] [--path single|graph|direct]
 
 Workloads (synthetic, seeded; no checkpoint download):
   decode  dim 4096, hidden 14336, 32 layers, 32/8 heads, vocab 32000, ctx 4096: 32 prompt ids then
@@ -96,7 +96,9 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", choices=["decode", "long", "attn"], default="decode")
-    ap.add_argument("--graph", type=int, default=1, help="1: replay a captured hipGraph per step")
+    ap.add_argument("--path", choices=["graph", "single", "direct"], default="graph",
+                    help="graph: per-op kernels replayed from a captured hipGraph; single: one launch per token "
+                         "(dataflow of workgroups); direct: the per-op kernels launched one by one")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode budget (0 = skip)")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--attn-min-slice", type=int, default=0, help="override the attention slice floor")
@@ -134,7 +136,7 @@ def main():
     sess.hip(0)
     log(f"[bench] weights uploaded in {time.perf_counter() - t0:.1f} s")
     ctxp = sess.hip_ctx()
-    opts = [(b"graph", int(args.graph))]
+    opts = [(b"single_launch", int(args.path == "single")), (b"graph", int(args.path == "graph"))]
     if args.attn_min_slice:
         opts.append((b"attn_min_slice", args.attn_min_slice))
     for key, val in opts:
@@ -181,7 +183,11 @@ def main():
     log(f"[bench] warm-up: {args.warmup} steps")
     run(max(args.warmup, 1))
     log(f"[bench] timed: {steps} steps")
+    view = hip.HipModel.attach(ctxp, cfg)
+    view.set_option("stats", 1)  # HIP events around each step's kernels on the context's stream
     toks, secs, hydrate_s = run(steps)
+    dev_us, dev_steps = view.step_stats()
+    view.set_option("stats", 0)
     assert len(secs) == steps, "decode stopped early"
     total = float(np.sum(secs))
     tok_s = steps / total
@@ -191,11 +197,16 @@ def main():
     step_gbs = step_bytes * tok_s / 1e9
     log(f"[bench] {tok_s:.1f} tok/s ({1e3 * total / steps:.3f} ms/step), {step_gbs:.0f} GB/s algorithmic")
 
-    # dominant kernel, timed live on its own stream with HIP events (rotating weight copies)
-    copies = 7  # 7 x 235 MB > 1.6 GB, far beyond the 256 MB last-level cache
-    us = hip.bench_kernel(2, 14336, 4096, copies=copies, warmup=20, reps=args.kernel_reps)
-    achieved = W13_BYTES / (us * 1e-6) / 1e9
-    log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {achieved:.0f} GB/s")
+    # device time per timed step (HIP events on the decode stream)
+    step_us = dev_us / max(dev_steps, 1)
+    log(f"[bench] device time per step: {step_us:.1f} us over {dev_steps} steps "
+        f"({step_bytes / (step_us * 1e-6) / 1e9:.0f} GB/s algorithmic)")
+
+    # fused rmsnorm + W1/W3 + SwiGLU matvec, timed on its own stream with HIP events over rotating
+    # weight copies (7 x 235 MB, far beyond the 256 MB last-level cache)
+    us = hip.bench_kernel(2, 14336, 4096, copies=7, warmup=20, reps=args.kernel_reps)
+    w13_gbs = W13_BYTES / (us * 1e-6) / 1e9
+    log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {w13_gbs:.0f} GB/s")
 
     cpu = None
     if args.cpu_seconds > 0 and wl == "decode":
@@ -203,11 +214,26 @@ def main():
         cpu = cpu_baseline(sess, cfg, prompt, [int(t) for t in toks], args.cpu_seconds)
         log(f"[bench] CPU: {cpu['value']} tok/s on {cpu['cores']} cores; {cpu['sample']}")
 
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "w13_swiglu_traffic.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+    def traffic_of(name):
+        tf = os.path.join(ROOT, "profiles", name)
+        if os.path.exists(tf):
+            with open(tf) as f:
+                return json.load(f).get("bytes_per_launch")
+        return None
+
+    w13 = {"bound": "hbm", "achieved": round(w13_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+           "frac": round(w13_gbs / PEAK_GBS, 4), "traffic": traffic_of("w13_swiglu_traffic.json"),
+           "kernel": "matvec_kernel<8,2> as rmsnorm + W1/W3 + SwiGLU (14336 x 4096 x 2)",
+           "bytes_per_launch": W13_BYTES, "us_per_launch": round(us, 3)}
+    if args.path == "single":
+        # one launch per token: the dominant kernel is the whole step
+        achieved = step_bytes / (step_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_of("decode_step_traffic.json"),
+                    "kernel": "decode_flow_kernel<128,4> (the whole token, one launch)",
+                    "bytes_per_launch": int(step_bytes), "us_per_launch": round(step_us, 3)}
+    else:
+        roofline = w13
 
     out = {
         "metric": METRIC,
@@ -228,14 +254,13 @@ def main():
                          "attn": "Mistral-7B-shape fp16 decode over a KV cache pre-filled to 16384, ctx 16448"}[wl],
             "dim": 4096, "hidden_dim": 14336, "n_layers": 32, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128,
             "vocab": 32000, "context": ctx_len, "prompt_tokens": n_prompt, "global_batch": 1,
-            "accumulate": "fp32", "activations": "fp32", "graph": bool(args.graph), "parallelism": "none (1 GPU)",
+            "accumulate": "fp32", "activations": "fp32", "path": args.path, "parallelism": "none (1 GPU)",
         },
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved_GBps": round(step_gbs, 1),
                           "peak_GBps": PEAK_GBS, "frac": round(step_gbs / PEAK_GBS, 4), "kv_len_mean": kv_mean},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "matvec_kernel<8,2> as rmsnorm + W1/W3 + SwiGLU (14336 x 4096 x 2)",
-                     "bytes_per_launch": W13_BYTES, "us_per_launch": round(us, 3)},
+        "roofline": roofline,
+        "w13_kernel": w13,
+        "device_us_per_step": round(step_us, 2),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

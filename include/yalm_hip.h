@@ -80,12 +80,22 @@ float* yhip_logits_host(yhip_ctx* ctx);
 int yhip_kv_read(yhip_ctx* ctx, int layer, uint16_t* k_host, uint16_t* v_host);
 int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16_t* v_host);
 
-/* Options: "graph" (1 = replay a captured hipGraph per step, default; 0 = direct launches),
- * "attn_splits" (most KV slices per kv head, default 512/n_kv_heads clamped to [1,64]),
- * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64).
+/* Options: "single_launch" (1 = the whole step as one launch, a dataflow of workgroups, where the
+ * kernel has an instantiation: head_dim 128 with 4 q heads per kv head, and the test shapes;
+ * 0 = per-op kernels, the default), "flow_bpc" / "flow_bpc_w2" (workgroups per CU of the single
+ * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
+ * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
+ * kv head, default 512/n_kv_heads clamped to [1,64]),
+ * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64), "stats" (1 = time
+ * every synchronised step on the device with HIP events and reset the totals; 0 = off).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
+
+/* Device time of the steps timed since "stats" was set: total microseconds between HIP events
+ * recorded on the context's stream around each LOGITS/argmax step's kernels, and the step count.
+ * No reference counterpart (the reference times whole steps on the host, src/main.cpp:195-210). */
+int yhip_step_stats(const yhip_ctx* ctx, double* us_total, int* steps);
 
 /* Debug read of a device activation after the last forward: which = 0 x [dim], 1 q [nh*hd],
  * 2 attention output [nh*hd], 3 hb [hidden], 4 logits [vocab]. Mirrors the reference's

@@ -22,14 +22,50 @@ def hip():
     return H
 
 
-def _models(cfg, tensors):
-    return O.OracleModel(cfg, tensors), hip().HipModel(cfg, tensors)
+# The three ways a step can run: one launch per token (a dataflow of workgroups), the captured
+# hipGraph of per-op kernels (the default), and the same kernels launched directly.
+PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
+         "direct": dict(single_launch=0, graph=0)}
 
 
-def test_embedding_gather_bit_exact():
+def use_path(m, path):
+    for k, v in PATHS[path].items():
+        m.set_option(k, v)
+
+
+def _models(cfg, tensors, path="single"):
+    hm = hip().HipModel(cfg, tensors)
+    use_path(hm, path)
+    return O.OracleModel(cfg, tensors), hm
+
+
+def _check_kv(om, hm, n_layers):
+    for layer in range(n_layers):
+        ko, vo = om.kv(layer)
+        kh, vh = hm.kv(layer)
+        # indexing: exactly the same entries are written
+        assert np.array_equal(ko != 0, kh != 0)
+        assert np.array_equal(vo != 0, vh != 0)
+        # values: where fp32 summation order moves a value across an fp16 rounding boundary the two
+        # differ by an ulp, tiny against the tensor's scale. Layer 0 depends only on the (exact)
+        # embedding, so nearly all of its written entries are bit-identical; deeper layers see inputs
+        # that already went through fp16 caches, which turns summation-order noise into occasional
+        # ulp flips, so only the scale-relative bounds apply there.
+        for a, b in ((kh, ko), (vh, vo)):
+            fa, fb = h2f(a), h2f(b)
+            assert np.max(np.abs(fa - fb)) <= 2e-3 * np.max(np.abs(fb))
+            assert npref.rel_l2(fa, fb) < 1e-3
+            if layer == 0:
+                written = (a != 0) | (b != 0)
+                assert np.mean(a[written] == b[written]) > 0.99
+
+
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_embedding_gather_bit_exact(path):
     cfg = dict(MICRO, n_layers=0)
     t = np_tensors(cfg, seed=21)
     with hip().HipModel(cfg, t) as m:
+        use_path(m, path)
         for tok in (0, 1, 255, cfg["vocab_size"] - 1):
             m.forward(tok, 0)
             x = m.debug_read(0, cfg["dim"])
@@ -37,12 +73,11 @@ def test_embedding_gather_bit_exact():
 
 
 @pytest.mark.parametrize("cfg_name", ["micro", "tiny"])
-@pytest.mark.parametrize("graph", [1, 0])
-def test_teacher_forced_logits_and_kv(cfg_name, graph):
+@pytest.mark.parametrize("path", list(PATHS))
+def test_teacher_forced_logits_and_kv(cfg_name, path):
     cfg = dict(MICRO if cfg_name == "micro" else TINY)
     t = np_tensors(cfg, seed=22, std=0.02 if cfg_name == "tiny" else 0.1)
-    om, hm = _models(cfg, t)
-    hm.set_option("graph", graph)
+    om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(23)
     toks = rng.integers(0, cfg["vocab_size"], 12)
     worst = 0.0
@@ -54,26 +89,37 @@ def test_teacher_forced_logits_and_kv(cfg_name, graph):
             worst = max(worst, npref.rel_l2(lh, lo))
     assert worst < LOGIT_TOL, worst
     assert worst < 1e-4  # fp32 accumulation on both sides: far inside the contract
-    for layer in range(cfg["n_layers"]):
-        ko, vo = om.kv(layer)
-        kh, vh = hm.kv(layer)
-        # indexing: exactly the same entries are written
-        assert np.array_equal(ko != 0, kh != 0)
-        assert np.array_equal(vo != 0, vh != 0)
-        # values: the same fp16 almost everywhere; where fp32 summation order moves a value across an
-        # fp16 rounding boundary the two differ by an ulp, tiny against the tensor's scale
-        for a, b in ((kh, ko), (vh, vo)):
-            fa, fb = h2f(a), h2f(b)
-            assert np.max(np.abs(fa - fb)) <= 2e-3 * np.max(np.abs(fb))
-            assert npref.rel_l2(fa, fb) < 1e-3
-            assert np.mean(a == b) > 0.99
+    _check_kv(om, hm, cfg["n_layers"])
     hm.close()
 
 
-def test_greedy_sequence_matches_32_tokens():
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_mistral_shape_two_layers(path):
+    # The Mistral-7B layer shape (dim 4096, hidden 14336, 32/8 heads of 128) with two layers: the
+    # instantiations the full model runs, checked teacher-forced against the oracle.
+    cfg = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32, n_kv_heads=8,
+               max_seq_len=256, rotary_dim=128)
+    t = np_tensors(cfg, seed=31)
+    om, hm = _models(cfg, t, path)
+    rng = np.random.default_rng(32)
+    toks = rng.integers(0, cfg["vocab_size"], 70)
+    worst = 0.0
+    for pos, tok in enumerate(toks):
+        mode = 1 if pos % 10 in (0, 9) else 0
+        lo = om.forward(int(tok), pos, mode)
+        lh = hm.forward(int(tok), pos, mode)
+        if mode == 1:
+            worst = max(worst, npref.rel_l2(lh, lo))
+    assert worst < 1e-4, worst
+    _check_kv(om, hm, cfg["n_layers"])
+    hm.close()
+
+
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_greedy_sequence_matches_32_tokens(path):
     cfg = dict(TINY)
     t = np_tensors(cfg, seed=24)
-    om, hm = _models(cfg, t)
+    om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(16)
     prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 16)]
     seqs = []
@@ -96,10 +142,13 @@ def test_greedy_sequence_matches_32_tokens():
     hm.close()
 
 
-def test_forward_argmax_matches_host_argmax():
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_forward_argmax_matches_host_argmax(path):
     cfg = dict(TINY)
     t = np_tensors(cfg, seed=25)
     with hip().HipModel(cfg, t) as a, hip().HipModel(cfg, t) as b:
+        use_path(a, "graph")
+        use_path(b, path)
         tok = 5
         for pos in range(6):
             lg = a.forward(tok, pos)
@@ -108,12 +157,13 @@ def test_forward_argmax_matches_host_argmax():
             tok = nxt
 
 
-def test_sink_mode_beyond_context_matches_oracle():
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_sink_mode_beyond_context_matches_oracle(path):
     # pos >= max_seq_len: StreamingLLM ring with 2 sink tokens re-rotated each step
     # (reference src/infer.cpp:307-325, 489-494).
     cfg = dict(MICRO, max_seq_len=16)
     t = np_tensors(cfg, seed=26, std=0.1)
-    om, hm = _models(cfg, t)
+    om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(27)
     for pos in range(40):
         tok = int(rng.integers(0, cfg["vocab_size"]))
@@ -129,11 +179,12 @@ def test_sink_mode_beyond_context_matches_oracle():
     hm.close()
 
 
-def test_kv_write_then_decode_long_context():
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_kv_write_then_decode_long_context(path):
     # KV pre-filled from the host in the reference layout (the attention-heavy workload's setup).
     cfg = dict(MICRO, max_seq_len=2048)
     t = np_tensors(cfg, seed=28, std=0.1)
-    om, hm = _models(cfg, t)
+    om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(29)
     n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
     for layer in range(cfg["n_layers"]):
@@ -168,3 +219,7 @@ def test_bad_arguments_return_errors():
             m.set_option("nonsense", 1)
     with pytest.raises(H.HipError):
         H.HipModel(dict(MICRO, head_dim=24))
+    # a shape without a single-launch instantiation runs the per-op kernels and refuses the option
+    with H.HipModel(dict(MICRO, n_kv_heads=4)) as m:  # one q head per kv head: no instantiation
+        with pytest.raises(H.HipError):
+            m.set_option("single_launch", 1)

@@ -55,9 +55,10 @@ __device__ __forceinline__ float dpp_src(float old, float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
                                                                CTRL, ROW_MASK, 0xf, false));
 }
-__device__ __forceinline__ float lane63(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+__device__ __forceinline__ float lane_read(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
+__device__ __forceinline__ float lane63(float v) { return lane_read(v, 63); }
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_src<0x111, 0xf>(0.f, v);  // row_shr:1
   v += dpp_src<0x112, 0xf>(0.f, v);  // row_shr:2
@@ -112,6 +113,39 @@ __device__ __forceinline__ float dot8(u32x4 wbits, const float* xs, float acc) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Cross-workgroup hand-off without cache-wide fences.
+//
+// On a multi-XCD part each XCD has its own L2; an agent-scope fence would write back and
+// invalidate the whole L2 of every workgroup that executes it. Data that one workgroup hands to
+// another within a launch is instead written and read with agent-scope relaxed atomics (coherent,
+// written through past the XCD's L2), and `publish()` waits until this thread's stores have
+// completed before the workgroup signals.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void store_shared(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_shared(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Activation accesses: plain, or agent-coherent (COH) when a later workgroup of the same launch
+// consumes the value.
+template <bool COH>
+__device__ __forceinline__ float ld_act(const float* p) {
+  if constexpr (COH) return load_shared(p);
+  else return *p;
+}
+template <bool COH>
+__device__ __forceinline__ void st_act(float* p, float v) {
+  if constexpr (COH) store_shared(p, v);
+  else *p = v;
+}
+
+// ------------------------------------------------------------------------------------------
 // Fused matvec family.
 //
 // A "group" is R weight rows that one wavefront streams together. Groups are dealt to waves
@@ -133,17 +167,24 @@ struct MatvecArgs {
   int groups;  // number of groups
   int K;       // row length (elements), multiple of 8
   const float* x;      // input vector [K]
+  const uint16_t* x16; // or an fp16 input vector (the embedding row), when not null
   const float* gain;   // rmsnorm gain [K] or nullptr (no norm)
   float eps;
   float* out;
   int act;  // 1 silu, 0 gelu (SwiGLU epilogue)
   // QKV epilogue
-  int q_dim, kv_dim, head_dim, rotary_dim, msl;
-  float rope_theta, qkv_clip;
+  int q_dim, kv_dim, head_dim, msl;
+  float qkv_clip;
   uint16_t* kcache;
   uint16_t* vcache;
+  uint32_t* kvcur;       // coherent copy of this position's K/V (fp16 pairs), single-launch decode only
   const StepParams* params;
-  const float* rope_cs;  // [head_dim]: (cos, sin) per rotary pair at this step's position
+  int pos;               // position, or -1 to read params->pos
+  const float* rope_cs;  // [head_dim]: (cos, sin) per rotary pair at this step's position, or
+  const float* inv_freq; // [head_dim / 2]: compute that table from the rotary frequencies
+  // row-loop statistics for the lm_head: running (max, index) of the outputs, tie rule of
+  // src/sampler.cpp:27-38, kept per wave (argmax fused into the last matvec)
+  int track_max;
 };
 
 // Loads of one row segment for this lane: chunk c = lane + 64*u, u < KC (KC = K/512 when > 0).
@@ -166,41 +207,47 @@ __device__ __forceinline__ void group_rows(const MatvecArgs& a, int p, const uin
   }
 }
 
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
 // Epilogues run on every lane of the wave (all operands are wave-uniform after the reductions);
 // only lane 0 stores. Keeping the computation outside a lane-0 branch keeps the row loop's control
 // flow simple.
 // Operands an epilogue needs from memory, loaded together with the group's weights so that their
 // latency is not paid at the end of the group.
-template <int R, EpiKind EPI>
+template <int R, EpiKind EPI, bool COH>
 __device__ __forceinline__ void epilogue_prefetch(const MatvecArgs& a, int p, float (&pre)[R]) {
   if constexpr (EPI == kEpiResidual) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) pre[r] = a.out[(long)p * R + r];
+    for (int r = 0; r < R; ++r) pre[r] = ld_act<COH>(a.out + (long)p * R + r);
   }
 }
 
-template <int R, EpiKind EPI>
+template <int R, EpiKind EPI, bool COH>
 __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float (&acc)[R], const float (&pre)[R],
                                          int pos, const float* rope_cs, bool store) {
   if constexpr (EPI == kEpiStore) {
     if (store)
 #pragma unroll
-      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
+      for (int r = 0; r < R; ++r) st_act<COH>(a.out + (long)p * R + r, acc[r]);
   } else if constexpr (EPI == kEpiResidual) {
     if (store)
 #pragma unroll
-      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = pre[r] + acc[r];
+      for (int r = 0; r < R; ++r) st_act<COH>(a.out + (long)p * R + r, pre[r] + acc[r]);
   } else if constexpr (EPI == kEpiSwiGLU) {
     const float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
     const float v = h * acc[R - 1];
-    if (store) a.out[p] = v;
+    if (store) st_act<COH>(a.out + p, v);
   } else {  // kEpiQkvRope: rows i = 2p, 2p+1 of [Wq; Wk; Wv]  (reference src/infer.cpp:279-305)
     const int i = 2 * p;
     float v0 = clipf(acc[0], a.qkv_clip);
     float v1 = clipf(acc[R - 1], a.qkv_clip);
     if (i < a.q_dim + a.kv_dim) {  // RoPE on q and k (reference src/infer.cpp:202-215)
-      // (cos, sin) of pos * freq_j for this step (computed once per token by embed_kernel, staged
-      // into LDS with the input vector)
+      // (cos, sin) of pos * freq_j for this step, staged into LDS with the input vector
       const int j = i % a.head_dim;
       const float c = rope_cs[j], s = rope_cs[j + 1];
       const float r0 = v0 * c - v1 * s;
@@ -210,41 +257,65 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
     }
     if (!store) return;
     if (i < a.q_dim) {
-      a.out[i] = v0;
-      a.out[i + 1] = v1;
+      st_act<COH>(a.out + i, v0);
+      st_act<COH>(a.out + i + 1, v1);
     } else {
       const Positions ps = positions(pos, a.msl);
       const bool is_k = i < a.q_dim + a.kv_dim;
       const int ik = i - a.q_dim - (is_k ? 0 : a.kv_dim);
       const int g = ik / a.head_dim, j = ik % a.head_dim;
       const long head = (long)g * a.head_dim * a.msl;
-      const f16 h0 = (f16)v0, h1 = (f16)v1;  // RNE, as _cvtss_sh(x, 0)
+      const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0);  // RNE, as _cvtss_sh(x, 0)
+      const uint16_t h1 = __builtin_bit_cast(uint16_t, (f16)v1);
+      if constexpr (COH)  // the same launch's attention reads this position from the side buffer
+        store_shared_u32(a.kvcur + (is_k ? 0 : a.kv_dim / 2) + ik / 2, (uint32_t)h0 | ((uint32_t)h1 << 16));
       if (is_k) {
-        a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = __builtin_bit_cast(uint16_t, h0);
-        a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = __builtin_bit_cast(uint16_t, h1);
+        a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = h0;
+        a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = h1;
       } else {
-        a.vcache[head + (long)j * a.msl + ps.kv_pos] = __builtin_bit_cast(uint16_t, h0);
-        a.vcache[head + (long)(j + 1) * a.msl + ps.kv_pos] = __builtin_bit_cast(uint16_t, h1);
+        a.vcache[head + (long)j * a.msl + ps.kv_pos] = h0;
+        a.vcache[head + (long)(j + 1) * a.msl + ps.kv_pos] = h1;
       }
     }
   }
 }
 
+template <bool COH>
+__device__ __forceinline__ float stage_src(const MatvecArgs& a, int i) {
+  if (a.x16) return (float)__builtin_bit_cast(f16, a.x16[i]);
+  return ld_act<COH>(a.x + i);
+}
+
 // Stage the (optionally RMS-normalised) input vector into LDS: xs[i] = x[i] * inv * g[i] with
-// inv = 1/sqrt(mean(x^2) + eps) (reference src/infer.cpp:136-146). NPT > 0: K == 1024*NPT/... i.e.
+// inv = 1/sqrt(mean(x^2) + eps) (reference src/infer.cpp:136-146). NPT > 0: K == 1024*NPT, i.e.
 // exactly NPT float4 per thread, all loads issued before the first use; NPT == 0: any K % 4 == 0.
-template <int NPT>
-__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red) {
-  if (a.rope_cs)  // the step's RoPE table goes to LDS right after the input vector
+// The step's RoPE table (head_dim floats) goes to LDS right after the vector.
+template <int NPT, bool COH>
+__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red, int pos) {
+  if (a.rope_cs) {
     for (int i = threadIdx.x; i < a.head_dim; i += kBlock) xs[a.K + i] = a.rope_cs[i];
-  const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
-  const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
+  } else if (a.inv_freq) {  // reference src/infer.cpp:205-208
+    for (int k = threadIdx.x; k < a.head_dim / 2; k += kBlock) {
+      const float ang = (float)pos * a.inv_freq[k];
+      xs[a.K + 2 * k] = cosf(ang);
+      xs[a.K + 2 * k + 1] = sinf(ang);
+    }
+  }
   f32x4* o4 = reinterpret_cast<f32x4*>(xs);
   if constexpr (NPT > 0) {
     f32x4 xv[NPT], gv[NPT];
+    if (!COH && !a.x16) {
+      const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
 #pragma unroll
-    for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
+      for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < NPT; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[k][e] = stage_src<COH>(a, 4 * (threadIdx.x + kBlock * k) + e);
+    }
     if (a.gain) {
+      const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
 #pragma unroll
       for (int k = 0; k < NPT; ++k) gv[k] = g4[threadIdx.x + kBlock * k];
       float ss = 0.f;
@@ -268,16 +339,27 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
     }
   } else {
     const int n4 = a.K >> 2;
+    auto src4 = [&](int i) {
+      f32x4 v;
+      if (!COH && !a.x16) {
+        v = reinterpret_cast<const f32x4*>(a.x)[i];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = stage_src<COH>(a, 4 * i + e);
+      }
+      return v;
+    };
     if (a.gain) {
+      const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
       float ss = 0.f;
       for (int i = threadIdx.x; i < n4; i += kBlock) {
-        f32x4 v = x4[i];
+        f32x4 v = src4(i);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
       }
       ss = block_sum(ss, red);
       const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
       for (int i = threadIdx.x; i < n4; i += kBlock) {
-        f32x4 v = x4[i], g = g4[i];
+        f32x4 v = src4(i), g = g4[i];
         f32x4 o;
         o[0] = v[0] * inv * g[0];
         o[1] = v[1] * inv * g[1];
@@ -286,24 +368,43 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
         o4[i] = o;
       }
     } else {
-      for (int i = threadIdx.x; i < n4; i += kBlock) o4[i] = x4[i];
+      for (int i = threadIdx.x; i < n4; i += kBlock) o4[i] = src4(i);
     }
   }
   __syncthreads();
 }
 
+// Per-wave running maximum for the fused argmax (track_max); every lane holds the same values.
+struct RowMax {
+  float v = kNegBig;
+  int i = 0x7fffffff;
+};
+
+template <int R, EpiKind EPI>
+__device__ __forceinline__ void track_rows(const MatvecArgs& a, int p, const float (&acc)[R], RowMax& m) {
+  if constexpr (EPI == kEpiStore) {
+    if (a.track_max)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (acc[r] > kNegBig) better(m.v, m.i, acc[r], p * R + r);
+  }
+}
+
+// The fused matvec over groups p = blk*4 + wave + k*(nblk*4). `wait()` runs after the first
+// group's weight loads are issued and before anything that reads activations (the single-launch
+// decode waits there for the producing phase); COH selects coherent activation accesses.
 // KC > 0: K == 512*KC, fully unrolled row streaming. KC == 0: any K % 8 == 0.
 // One register buffer of weights per wave; latency is hidden by the other resident waves and by
 // issuing the next group's loads ahead of the current group's reductions and epilogue.
-template <int KC, int R, EpiKind EPI>
-__global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
-  extern __shared__ float lds[];
+template <int KC, int R, EpiKind EPI, bool COH, class Wait>
+__device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int nblk, float* lds, Wait wait) {
   float* red = lds;      // kWavesPerBlock floats (padded to 16)
-  float* xs = lds + 16;  // K floats
+  float* xs = lds + 16;  // K floats (+ the RoPE table)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int wave_stride = gridDim.x * kWavesPerBlock;
-  int p = blockIdx.x * kWavesPerBlock + wave;
+  const int wave_stride = nblk * kWavesPerBlock;
+  int p = blk * kWavesPerBlock + wave;
+  RowMax mx;
 
   if constexpr (KC > 0) {
     // One register buffer: the first group's loads are in flight while the workgroup stages x
@@ -311,14 +412,16 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
     // the previous iteration, after its registers are dead.
     u32x4 wv[R][KC];
     float pre[R];
-    const int pos = EPI == kEpiQkvRope ? a.params->pos : 0;
     if (p < a.groups) {
       const uint16_t* rows[R];
       group_rows<R>(a, p, rows);
       load_group<KC, R>(wv, rows, lane);
-      epilogue_prefetch<R, EPI>(a, p, pre);
+      if (!COH) epilogue_prefetch<R, EPI, COH>(a, p, pre);
     }
-    stage_input<KC / 2>(a, xs, red);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+    wait();
+    const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
+    if (COH && p < a.groups) epilogue_prefetch<R, EPI, COH>(a, p, pre);
+    stage_input<KC / 2, COH>(a, xs, red, pos);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
     while (p < a.groups) {
       float acc[R];
 #pragma unroll
@@ -333,24 +436,26 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      epilogue<R, EPI>(a, p, acc, pre, pos, xs + a.K, lane == 0);
+      epilogue<R, EPI, COH>(a, p, acc, pre, pos, xs + a.K, lane == 0);
+      track_rows<R, EPI>(a, p, acc, mx);
       p += wave_stride;
       if (p < a.groups) {
         const uint16_t* rows[R];
         group_rows<R>(a, p, rows);
         load_group<KC, R>(wv, rows, lane);
-        epilogue_prefetch<R, EPI>(a, p, pre);
+        epilogue_prefetch<R, EPI, COH>(a, p, pre);
       }
     }
   } else {
-    stage_input<0>(a, xs, red);
+    wait();
+    const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
+    stage_input<0, COH>(a, xs, red, pos);
     const int nch = a.K >> 3;
-    const int pos = EPI == kEpiQkvRope ? a.params->pos : 0;
     for (; p < a.groups; p += wave_stride) {
       const uint16_t* rows[R];
       group_rows<R>(a, p, rows);
       float pre[R];
-      epilogue_prefetch<R, EPI>(a, p, pre);
+      epilogue_prefetch<R, EPI, COH>(a, p, pre);
       float acc[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -363,9 +468,17 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      epilogue<R, EPI>(a, p, acc, pre, pos, xs + a.K, lane == 0);
+      epilogue<R, EPI, COH>(a, p, acc, pre, pos, xs + a.K, lane == 0);
+      track_rows<R, EPI>(a, p, acc, mx);
     }
   }
+  return mx;
+}
+
+template <int KC, int R, EpiKind EPI>
+__global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
+  extern __shared__ float lds[];
+  matvec_body<KC, R, EPI, false>(a, blockIdx.x, gridDim.x, lds, [] {});
 }
 
 // ------------------------------------------------------------------------------------------
@@ -396,23 +509,6 @@ __global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* emb, floa
     x[i] = (float)__builtin_bit_cast(f16, emb[base + i]);
   if (blockIdx.x == 0) fill_rope_table(inv_freq, rope_cs, half, params->pos);
 }
-
-// ------------------------------------------------------------------------------------------
-// Cross-workgroup hand-off without cache-wide fences.
-//
-// On a multi-XCD part each XCD has its own L2; an agent-scope fence would write back and
-// invalidate the whole L2 of every workgroup that executes it. Data that one workgroup hands to
-// another is instead written and read with agent-scope relaxed atomics (coherent, written through
-// past the XCD's L2), and `publish()` waits until this thread's stores have completed before the
-// workgroup signals.
-// ------------------------------------------------------------------------------------------
-__device__ __forceinline__ void store_shared(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_shared(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------------------------------
 // Split-KV GQA decode attention (reference src/infer.cpp:218-250, 327-336).
@@ -447,8 +543,9 @@ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice)
   return chunk < min_slice ? min_slice : chunk;
 }
 
-// Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32); every lane of a group gets the
-// group total. DPP quad permutes and row mirrors, plus one cross-row swap for N = 32.
+// Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the
+// group total. DPP quad permutes and row mirrors, one cross-row swap for N = 32 and two lane reads
+// for the whole wave.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
@@ -460,8 +557,40 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   if constexpr (N >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
   if constexpr (N >= 16) v += dpp_mov<0x140>(v); // row_mirror
   if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (N >= 64) v = lane_read(v, 0) + lane_read(v, 32);
   return v;
 }
+
+// Tile geometry of the attention workgroup for head_dim HD and NT threads.
+//   Score phase: LPT lanes per token, each owning CPL 16-dim chunks of K; TT tokens per tile.
+//   Value phase: LPD adjacent lanes cover one V row's TT tokens (8 tokens = 16 bytes each, so a
+//   wave instruction reads whole 128-byte lines); a thread owns DPT rows d = dgrp + NDG*m and
+//   tokens 8*oct .. 8*oct+7 of the tile.
+// Each lane keeps the query values of its CPL chunks for all G heads in registers (16*CPL*G
+// floats); the 512-thread layout gives every lane a single chunk (LPT = HD/16) to keep that small.
+template <int HD, int NT>
+struct AttnGeom {
+  static constexpr int NW = NT / kWave;
+  static constexpr int LPT = (NT >= 512 || HD < 64) ? HD / 16 : 4;
+  static constexpr int CPL = HD / 16 / LPT;
+  static constexpr int TT = NT / LPT;
+  static constexpr int LPD = TT / 8;
+  static constexpr int NDG = NT / LPD;
+  static constexpr int DPT = HD / NDG;
+  static_assert(DPT >= 1 && NDG * DPT == HD && LPD <= kWave, "attention tile layout");
+};
+
+// LDS of one attention workgroup. kcur/vcur hold the current token's fp16 K and V of the head
+// (used by the single-launch decode, which reads them from a coherent side buffer).
+template <int HD, int G, int NT>
+struct AttnSmem {
+  float qs[G * HD];
+  __attribute__((aligned(16))) float ps[G][AttnGeom<HD, NT>::TT];
+  float red[2][G][NT / kWave];
+  __attribute__((aligned(16))) uint32_t kcur[HD / 2];
+  uint32_t vcur[HD / 2];
+  unsigned last_flag;
+};
 
 // K and V registers for one tile of one thread (loaded one tile ahead of use).
 template <int CPL, int DPT>
@@ -470,31 +599,24 @@ struct AttnTileRegs {
   u32x4 v[DPT];     // 8 consecutive tokens of each of this thread's V rows
 };
 
-// HD: head_dim; G: query heads per kv head.
-template <int HD, int G>
-__global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
-  // Score phase: LPT lanes per token, each owning CPL 16-dim chunks of K; TT tokens per tile.
-  // Value phase: LPD adjacent lanes cover one V row's TT tokens (8 tokens = 16 bytes each, so a
-  // wave instruction reads whole 128-byte lines); thread owns DPT rows d = dgrp + NDG*m and
-  // tokens 8*oct .. 8*oct+7 of the tile. Partial sums stay per lane and are reduced over the LPD
-  // lanes once, after the last tile. Every tile issues the same loads (addresses clamped into the
-  // cache, results masked), so the compiler waits only for the tile it is about to use.
-  constexpr int LPT = HD >= 64 ? 4 : HD / 16;
-  constexpr int CPL = HD / 16 / LPT;
-  constexpr int TT = kBlock / LPT;
-  constexpr int LPD = TT / 8;
-  constexpr int NDG = kBlock / LPD;
-  constexpr int DPT = HD / NDG;
-  static_assert(DPT >= 1 && NDG * DPT == HD && LPD <= kWave && G >= 1 && G <= kMaxGroup, "tile layout");
-  __shared__ float qs[G * HD];
-  __shared__ __attribute__((aligned(16))) float ps[G][TT];
-  __shared__ float red[2][G][kWavesPerBlock];
-  __shared__ unsigned last_flag;
-
-  const int g = blockIdx.x, split = blockIdx.y;
-  const int tid = threadIdx.x;
+// One attention workgroup: kv head g, KV slice `split`, all G query heads of g; tid is the thread
+// index (passed in so that a caller's loop can keep lane-derived values from being hoisted).
+// HD: head_dim; G: query heads per kv head; NT: threads.
+// COH (single-launch decode): q is read and the output written with agent-coherent accesses, and
+// the current token's K/V (position kv_pos, just written by other workgroups of the same launch)
+// is taken from `kvcur` ([K pairs | V pairs] as packed fp16x2, coherent) instead of the cache.
+// Partial sums stay per lane and are reduced over the LPD lanes once, after the last tile. Every
+// tile issues the same loads (addresses clamped into the cache, results masked), so the compiler
+// waits only for the tile it is about to use.
+template <int HD, int G, int NT, bool COH>
+__device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, int pos, AttnSmem<HD, G, NT>& sm,
+                                         const uint32_t* kvcur, int tid) {
+  using Geo = AttnGeom<HD, NT>;
+  constexpr int LPT = Geo::LPT, CPL = Geo::CPL, TT = Geo::TT, LPD = Geo::LPD, NDG = Geo::NDG, DPT = Geo::DPT;
+  constexpr int NW = Geo::NW;
+  static_assert(G >= 1 && G <= kMaxGroup, "query heads per kv head");
   const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const Positions pss = positions(a.params->pos, a.msl);
+  const Positions pss = positions(pos, a.msl);
   const int kv_len = pss.kv_len;
   const int chunk = attn_chunk(kv_len, a.nsplit, a.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
@@ -507,7 +629,7 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
 
   if (pss.kv_sink > 0 && split == 0) {
     // Re-rotate sink keys r < kv_sink by angle freq*1 in place (fp16 round trip as reference).
-    for (int e = tid; e < pss.kv_sink * (HD / 2); e += kBlock) {
+    for (int e = tid; e < pss.kv_sink * (HD / 2); e += NT) {
       const int r = e / (HD / 2);
       const int j = 2 * (e % (HD / 2));
       const float freq = a.inv_freq[j / 2];
@@ -525,6 +647,8 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   const int oct = tid % LPD, dgrp = tid / LPD;
   const bool vec_ok = (a.msl & 7) == 0;
   const int vmax = vec_ok ? a.msl - 8 : 0;
+  const int kvp = pss.kv_pos;
+  const uint16_t* vcur_h = reinterpret_cast<const uint16_t*>(sm.vcur);
 
   auto load_tile = [&](int t0, AttnTileRegs<CPL, DPT>& r) {
     const int tok = min(t0 + tok_l, a.msl - 1);
@@ -542,7 +666,16 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
     }
   };
 
-  for (int e = tid; e < G * HD; e += kBlock) qs[e] = a.q[(long)g * G * HD + e];
+  if constexpr (COH) {
+    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = load_shared(a.q + (long)g * G * HD + e);
+    for (int e = tid; e < HD / 2; e += NT) {
+      sm.kcur[e] = __hip_atomic_load(kvcur + g * (HD / 2) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm.vcur[e] = __hip_atomic_load(kvcur + (a.n_kv_heads + g) * (HD / 2) + e, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = a.q[(long)g * G * HD + e];
+  }
   AttnTileRegs<CPL, DPT> cur, nxt;
   load_tile(t_begin, cur);
   float m_run[G], l_run[G], acc[DPT][G];
@@ -560,6 +693,29 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
     load_tile(t0 + TT < t_end ? t0 + TT : t0, nxt);  // next tile (or this one again) in flight
     const int tok = t0 + tok_l;
     const bool valid = tok < t_end;
+    const int tv = t0 + 8 * oct;
+    if constexpr (COH) {
+      if (kvp >= t0 && kvp < t0 + TT) {  // this tile holds the current token: take it from the side buffer
+        if (tok == kvp) {
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(sm.kcur + (sub * CPL + cc) * 8);
+            cur.k[cc][0] = src[0];
+            cur.k[cc][1] = src[1];
+          }
+        }
+        if (kvp >= tv && kvp < tv + 8) {
+#pragma unroll
+          for (int m = 0; m < DPT; ++m) {
+            f16x8 v8 = __builtin_bit_cast(f16x8, cur.v[m]);
+            const f16 vc = __builtin_bit_cast(f16, vcur_h[dgrp + NDG * m]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v8[e] = (kvp - tv == e) ? vc : v8[e];  // no dynamic register index
+            cur.v[m] = __builtin_bit_cast(u32x4, v8);
+          }
+        }
+      }
+    }
     // scores: partial dots over this lane's chunks, then summed over the LPT lanes of the token
     float s[G];
 #pragma unroll
@@ -571,7 +727,7 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
       const int c = sub * CPL + cc;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float* qh = qs + h * HD + c * 16;
+        const float* qh = sm.qs + h * HD + c * 16;
         float d = s[h];
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(qh[e], (float)k0[e], d);
@@ -585,41 +741,40 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
       s[h] = lane_group_sum<LPT>(s[h]);
       s[h] = valid ? s[h] * inv_sqrt_hd : kNegBig;
       const float m = wave_max(s[h]);
-      if (lane == 0) red[0][h][wave] = m;
+      if (lane == 0) sm.red[0][h][wave] = m;
     }
     __syncthreads();
     float corr[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float m = red[0][h][0];
+      float m = sm.red[0][h][0];
 #pragma unroll
-      for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, red[0][h][w]);
+      for (int w = 1; w < NW; ++w) m = fmaxf(m, sm.red[0][h][w]);
       const float m_new = fmaxf(m_run[h], m);
       corr[h] = expf(m_run[h] - m_new);
       m_run[h] = m_new;
       const float p = valid ? expf(s[h] - m_new) : 0.f;
       const bool mine = sub == (h % LPT);  // each (token, head) probability stored and summed once
-      if (mine) ps[h][tok_l] = p;
+      if (mine) sm.ps[h][tok_l] = p;
       const float t = wave_sum(mine ? p : 0.f);
-      if (lane == 0) red[1][h][wave] = t;
+      if (lane == 0) sm.red[1][h][wave] = t;
     }
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWavesPerBlock; ++w) t += red[1][h][w];
+      for (int w = 0; w < NW; ++w) t += sm.red[1][h][w];
       l_run[h] = l_run[h] * corr[h] + t;
 #pragma unroll
       for (int m = 0; m < DPT; ++m) acc[m][h] *= corr[h];
     }
     // values: acc[m][h] += sum over this lane's 8 tokens of p[h][t] * V[d_m][t]
-    const int tv = t0 + 8 * oct;
     if (vec_ok && tv + 8 <= t_end) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&ps[h][8 * oct]);
-        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&ps[h][8 * oct + 4]);
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ps[h][8 * oct]);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ps[h][8 * oct + 4]);
 #pragma unroll
         for (int m = 0; m < DPT; ++m) {
           const f16x8 v8 = __builtin_bit_cast(f16x8, cur.v[m]);
@@ -641,9 +796,13 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
         if (t < t_end) {
 #pragma unroll
           for (int m = 0; m < DPT; ++m) {
-            const float v = (float)__builtin_bit_cast(f16, vh[(long)(dgrp + NDG * m) * a.msl + t]);
+            const int d = dgrp + NDG * m;
+            float v = (float)__builtin_bit_cast(f16, vh[(long)d * a.msl + t]);
+            if constexpr (COH) {
+              if (t == kvp) v = (float)__builtin_bit_cast(f16, vcur_h[d]);
+            }
 #pragma unroll
-            for (int h = 0; h < G; ++h) acc[m][h] = fmaf(ps[h][8 * oct + e], v, acc[m][h]);
+            for (int h = 0; h < G; ++h) acc[m][h] = fmaf(sm.ps[h][8 * oct + e], v, acc[m][h]);
           }
         }
       }
@@ -663,7 +822,11 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int m = 0; m < DPT; ++m)
 #pragma unroll
-        for (int h = 0; h < G; ++h) a.out[(long)(g * G + h) * HD + dgrp + NDG * m] = acc[m][h] / l_run[h];
+        for (int h = 0; h < G; ++h) {
+          float* o = a.out + (long)(g * G + h) * HD + dgrp + NDG * m;
+          if constexpr (COH) store_shared(o, acc[m][h] / l_run[h]);
+          else *o = acc[m][h] / l_run[h];
+        }
     return;
   }
   const int stride = HD + 2;
@@ -687,25 +850,34 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   __syncthreads();
   if (tid == 0) {
     const unsigned t = __hip_atomic_fetch_add(&a.tickets[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = (t == (unsigned)(active - 1)) ? 1u : 0u;
+    sm.last_flag = (t == (unsigned)(active - 1)) ? 1u : 0u;
   }
   __syncthreads();
-  if (!last_flag) return;
-  for (int e = tid; e < G * HD; e += kBlock) {
+  if (!sm.last_flag) return;
+  for (int e = tid; e < G * HD; e += NT) {
     const int h = e / HD, i = e % HD;
     const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride;
     float M = kNegBig;
     for (int sp = 0; sp < active; ++sp) M = fmaxf(M, load_shared(src + sp * stride + HD));
-    float L = 0.f, O = 0.f;
+    float L = 0.f, Ov = 0.f;
     for (int sp = 0; sp < active; ++sp) {
       const float* pp = src + sp * stride;
       const float w = expf(load_shared(pp + HD) - M);
       L = fmaf(load_shared(pp + HD + 1), w, L);
-      O = fmaf(load_shared(pp + i), w, O);
+      Ov = fmaf(load_shared(pp + i), w, Ov);
     }
-    a.out[(long)(g * G + h) * HD + i] = O / L;
+    float* o = a.out + (long)(g * G + h) * HD + i;
+    if constexpr (COH) store_shared(o, Ov / L);
+    else *o = Ov / L;
   }
   if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-KV attention as its own launch: grid (n_kv_heads, nsplit) of 256-thread workgroups.
+template <int HD, int G>
+__global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
+  __shared__ AttnSmem<HD, G, kBlock> sm;
+  attn_run<HD, G, kBlock, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -714,13 +886,6 @@ __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
 // up front (n = 32000 -> 8 per thread).
 // ------------------------------------------------------------------------------------------
 constexpr int kArgmaxThreads = 1024;
-
-__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
 
 __global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const float* logits, int n, int* out) {
   __shared__ float sv[kArgmaxThreads / kWave];

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/yalm_hip.h"
+#include "decode_flow.h"
 #include "kernels.h"
 
 using namespace yk;
@@ -82,6 +83,25 @@ struct yhip_ctx {
   int attn_splits = 32;
   int attn_min_slice = 64;
   hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // hydrate, logits, argmax
+
+  // single-launch decode (decode_flow.h)
+  const void* flow_fn = nullptr;  // instantiation for this shape, or null when the shape has none
+  size_t flow_lds = 0;
+  bool use_flow = false;
+  unsigned flow_launches = 0;
+  int flow_bpc = 2, flow_bpc_w2 = 1;  // workgroups per CU of the matvec phases (W2 separately)
+  LayerLayout layout{};       // weight and KV addresses of every layer
+  unsigned* sync = nullptr;   // flow_sync_words(n_layers)
+  uint32_t* kvcur = nullptr;  // current position's K/V as fp16 pairs
+  float* best_v = nullptr;
+  int* best_i = nullptr;
+
+  // device timing of synchronised steps ("stats" option)
+  bool stats = false;
+  bool stats_pending = false;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double stats_us = 0.0;
+  int stats_steps = 0;
 
   int q_dim() const { return c.n_heads * c.head_dim; }
   int kv_dim() const { return c.n_kv_heads * c.head_dim; }
@@ -167,6 +187,7 @@ MatvecArgs mv_base() {
   MatvecArgs a;
   memset(&a, 0, sizeof(a));
   a.qkv_clip = 3.402823466e38f;
+  a.pos = -1;
   return a;
 }
 
@@ -234,9 +255,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.q_dim = qd;
     a.kv_dim = kvd;
     a.head_dim = c.head_dim;
-    a.rotary_dim = c.rotary_dim;
     a.msl = c.max_seq_len;
-    a.rope_theta = c.rope_theta;
     a.qkv_clip = c.qkv_clip;
     a.kcache = ctx->kcache(l);
     a.vcache = ctx->vcache(l);
@@ -325,7 +344,136 @@ void drop_graphs(yhip_ctx* ctx) {
   }
 }
 
+// ---- single-launch decode ---------------------------------------------------------------------
+// Instantiations of decode_flow_kernel (head_dim, query heads per kv head): the Mistral-7B shape
+// and the small test shapes; other shapes run the per-op kernels.
+const void* select_flow_kernel(const yhip_config& c) {
+  if (c.vocab_size % 2 || c.n_kv_heads <= 0) return nullptr;
+  const int G = c.n_heads / c.n_kv_heads;
+  if (c.head_dim == 128 && G == 4) return reinterpret_cast<const void*>(&decode_flow_kernel<128, 4>);
+  if (c.head_dim == 32 && G == 4) return reinterpret_cast<const void*>(&decode_flow_kernel<32, 4>);
+  if (c.head_dim == 16 && G == 2) return reinterpret_cast<const void*>(&decode_flow_kernel<16, 2>);
+  return nullptr;
+}
+
+size_t attn_smem_bytes(int hd, int G) {
+  switch (hd * 16 + G) {
+    case 128 * 16 + 4: return sizeof(AttnSmem<128, 4, kBlock>);
+    case 32 * 16 + 4: return sizeof(AttnSmem<32, 4, kBlock>);
+    case 16 * 16 + 2: return sizeof(AttnSmem<16, 2, kBlock>);
+    default: return 0;
+  }
+}
+
+// Workgroups of a matvec phase: the per-op kernels' grid for the same rows (`bpc` per CU).
+int phase_blocks(int groups, int num_cus, int bpc) {
+  return std::max(1, std::min((groups + kWavesPerBlock - 1) / kWavesPerBlock, num_cus * bpc));
+}
+
+int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
+  const yhip_config& c = ctx->c;
+  FlowArgs d;
+  memset(&d, 0, sizeof(d));
+  d.layers = ctx->layout;
+  d.embed = ctx->embed;
+  d.wcls = ctx->wcls;
+  d.rms_final = ctx->rms_final;
+  d.inv_freq = ctx->inv_freq;
+  d.x = ctx->x;
+  d.q = ctx->q;
+  d.att = ctx->att;
+  d.hb = ctx->hb;
+  d.logits = ctx->logits;
+  d.partial = ctx->partial;
+  d.tickets = ctx->tickets;
+  d.kvcur = ctx->kvcur;
+  d.sync = ctx->sync;
+  d.best_v = ctx->best_v;
+  d.best_i = ctx->best_i;
+  d.result = ctx->argmax_dev;
+  d.n_layers = c.n_layers;
+  d.dim = c.dim;
+  d.hidden = c.hidden_dim;
+  d.q_dim = ctx->q_dim();
+  d.kv_dim = ctx->kv_dim();
+  d.head_dim = c.head_dim;
+  d.n_heads = c.n_heads;
+  d.n_kv_heads = c.n_kv_heads;
+  d.vocab = c.vocab_size;
+  d.msl = c.max_seq_len;
+  d.token = token;
+  d.pos = pos;
+  d.mode = mode;
+  d.nsplit = ctx->attn_splits;
+  d.min_slice = ctx->attn_min_slice;
+  d.act = c.act;
+  d.eps = c.norm_eps;
+  d.qkv_clip = c.qkv_clip;
+  d.launch = ctx->flow_launches++;
+  // attention workgroups: the active KV slices at this position (same rule as attn_run)
+  const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
+  int chunk = (kv_len + ctx->attn_splits - 1) / ctx->attn_splits;
+  chunk = (chunk + 63) & ~63;
+  chunk = std::max(chunk, ctx->attn_min_slice);
+  const int active = (kv_len + chunk - 1) / chunk;
+  const int cus = ctx->num_cus;
+  d.nb[kPhQkv] = phase_blocks((d.q_dim + 2 * d.kv_dim) / 2, cus, ctx->flow_bpc);
+  d.nb[kPhAtt] = c.n_kv_heads * active;
+  d.nb[kPhO] = phase_blocks(c.dim / 2, cus, ctx->flow_bpc);
+  d.nb[kPhW13] = phase_blocks(c.hidden_dim, cus, ctx->flow_bpc);
+  d.nb[kPhW2] = phase_blocks(c.dim, cus, ctx->flow_bpc_w2);
+  d.nb[kPhLm] = phase_blocks(c.vocab_size / 2, cus, ctx->flow_bpc);
+  const int per_layer = d.nb[0] + d.nb[1] + d.nb[2] + d.nb[3] + d.nb[4];
+  const int grid = c.n_layers * per_layer + (mode != 0 ? d.nb[kPhLm] : 0);
+  hipLaunchKernelGGL(((void (*)(FlowArgs))ctx->flow_fn), dim3(grid), dim3(kBlock), ctx->flow_lds, ctx->stream, d);
+  HIP_TRY(ctx, hipGetLastError());
+  if (ctx->stats && mode != 0) HIP_TRY(ctx, hipEventRecord(ctx->ev1, ctx->stream));  // the kernel alone
+  if (mode == 1)
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
+                                hipMemcpyDeviceToHost, ctx->stream));
+  else if (mode == 2)
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+  if (mode != 0)  // wait time-out flag, checked after the caller's synchronisation
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 1, ctx->sync + kSyncAbort, sizeof(int), hipMemcpyDeviceToHost,
+                                ctx->stream));
+  return YHIP_OK;
+}
+
+// After a synchronised single-launch step: a wait that timed out poisons the step.
+int check_flow_status(yhip_ctx* ctx) {
+  if (!ctx->use_flow || ctx->argmax_host[1] == 0) return YHIP_OK;
+  ctx->argmax_host[1] = 0;
+  hipMemsetAsync(ctx->sync, 0, (size_t)flow_sync_words(ctx->c.n_layers) * sizeof(unsigned), ctx->stream);
+  hipStreamSynchronize(ctx->stream);
+  return fail(ctx, YHIP_EDEVICE, "single-launch decode: a dependency wait timed out");
+}
+
+int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode);
+
+// One step, bracketed by HIP events on the context's stream when "stats" is on (synchronised
+// modes only; the elapsed time is collected after the caller's synchronisation).
 int run_step(yhip_ctx* ctx, int token, int pos, int mode) {
+  const bool timed = ctx->stats && mode != 0;
+  if (timed) HIP_TRY(ctx, hipEventRecord(ctx->ev0, ctx->stream));
+  if (int rc = run_step_inner(ctx, token, pos, mode)) return rc;
+  if (timed) {
+    if (!ctx->use_flow) HIP_TRY(ctx, hipEventRecord(ctx->ev1, ctx->stream));
+    ctx->stats_pending = true;
+  }
+  return YHIP_OK;
+}
+
+void collect_stats(yhip_ctx* ctx) {
+  if (!ctx->stats_pending) return;
+  ctx->stats_pending = false;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) == hipSuccess) {
+    ctx->stats_us += 1000.0 * ms;
+    ctx->stats_steps += 1;
+  }
+}
+
+int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
   const yhip_config& c = ctx->c;
   if (token < 0 || token >= c.vocab_size) return fail(ctx, YHIP_EINVAL, "token id out of range");
   if (pos < 0) return fail(ctx, YHIP_EINVAL, "negative position");
@@ -333,6 +481,7 @@ int run_step(yhip_ctx* ctx, int token, int pos, int mode) {
   for (int l = 0; l < c.n_layers; ++l)
     if (!ctx->layers[l].loaded) return fail(ctx, YHIP_ESTATE, "layer " + std::to_string(l) + " not uploaded");
   HIP_TRY(ctx, hipSetDevice(ctx->device));
+  if (ctx->use_flow) return launch_flow_step(ctx, token, pos, mode);
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(1), 0, ctx->stream, ctx->params, token, pos);
   HIP_TRY(ctx, hipGetLastError());
   if (!ctx->use_graph) return enqueue_step(ctx, mode);
@@ -440,7 +589,10 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   const size_t a_x = atake(dim * 4), a_q = atake(qd * 4), a_att = atake(qd * 4), a_hb = atake(hid * 4),
                a_lg = atake(V * 4), a_part = atake((size_t)c.n_heads * 64 * (c.head_dim + 2) * 4),
                a_tk = atake(64 * 4), a_am = atake(64), a_par = atake(sizeof(StepParams)),
-               a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4);
+               a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
+               a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
+               a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
+               a_bi = atake((size_t)ctx->num_cus * 64 * 4);
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -454,6 +606,10 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->params = (StepParams*)(ctx->abase + a_par);
   ctx->inv_freq = (float*)(ctx->abase + a_if);
   ctx->rope_cs = (float*)(ctx->abase + a_cs);
+  ctx->sync = (unsigned*)(ctx->abase + a_sync);
+  ctx->kvcur = (uint32_t*)(ctx->abase + a_kvc);
+  ctx->best_v = (float*)(ctx->abase + a_bv);
+  ctx->best_i = (int*)(ctx->abase + a_bi);
   {
     const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
     if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -462,6 +618,18 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   if (hipHostMalloc((void**)&ctx->logits_host, V * 4, hipHostMallocDefault) != hipSuccess ||
       hipHostMalloc((void**)&ctx->argmax_host, 64, hipHostMallocDefault) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "pinned host allocation failed"));
+  memset(ctx->argmax_host, 0, 64);
+
+  // Single-launch decode: one workgroup per CU, all co-resident (cooperative launch).
+  ctx->layout = LayerLayout{ctx->wbase, (long)per_layer, (long)o_qkv, (long)o_wo, (long)o_w1, (long)o_w3,
+                            (long)o_w2, (long)o_ra, (long)o_rf, ctx->kv, (long)ctx->kv_elems};
+  ctx->flow_fn = select_flow_kernel(c);
+  if (ctx->flow_fn) {
+    const size_t kmax = std::max({(size_t)c.dim, (size_t)c.hidden_dim, (size_t)ctx->q_dim()});
+    ctx->flow_lds = std::max((16 + kmax + (size_t)c.head_dim) * sizeof(float), attn_smem_bytes(c.head_dim, c.n_heads / c.n_kv_heads));
+    // available as an option; the per-op graph is the default (measured faster on MI355X)
+    if (ctx->flow_lds > 65536) ctx->flow_fn = nullptr;
+  }
   *out = ctx;
   return YHIP_OK;
 }
@@ -471,6 +639,8 @@ extern "C" int yhip_destroy(yhip_ctx* ctx) {
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   drop_graphs(ctx);
+  if (ctx->ev0) hipEventDestroy(ctx->ev0);
+  if (ctx->ev1) hipEventDestroy(ctx->ev1);
   if (ctx->wbase) hipFree(ctx->wbase);
   if (ctx->kv) hipFree(ctx->kv);
   if (ctx->abase) hipFree(ctx->abase);
@@ -528,6 +698,8 @@ extern "C" int yhip_forward(yhip_ctx* ctx, int token, int pos, int mode, float* 
   if (int rc = run_step(ctx, token, pos, mode)) return rc;
   if (mode == YHIP_MODE_HYDRATE) return YHIP_OK;
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  collect_stats(ctx);
+  if (int rc = check_flow_status(ctx)) return rc;
   if (logits_host != ctx->logits_host) memcpy(logits_host, ctx->logits_host, (size_t)ctx->c.vocab_size * 4);
   return YHIP_OK;
 }
@@ -537,6 +709,8 @@ extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_
   if (!next_token) return fail(ctx, YHIP_EINVAL, "null output");
   if (int rc = run_step(ctx, token, pos, 2)) return rc;
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  collect_stats(ctx);
+  if (int rc = check_flow_status(ctx)) return rc;
   *next_token = *ctx->argmax_host;
   return YHIP_OK;
 }
@@ -579,6 +753,22 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   hipStreamSynchronize(ctx->stream);
   if (!strcmp(key, "graph")) {
     ctx->use_graph = value != 0;
+  } else if (!strcmp(key, "stats")) {
+    if (value && !ctx->ev0) {
+      HIP_TRY(ctx, hipEventCreate(&ctx->ev0));
+      HIP_TRY(ctx, hipEventCreate(&ctx->ev1));
+    }
+    ctx->stats = value != 0;
+    ctx->stats_pending = false;
+    ctx->stats_us = 0.0;
+    ctx->stats_steps = 0;
+    return YHIP_OK;  // graphs stay valid: the events are recorded outside them
+  } else if (!strcmp(key, "single_launch")) {
+    if (value && !ctx->flow_fn) return fail(ctx, YHIP_EINVAL, "no single-launch decode kernel for this shape");
+    ctx->use_flow = value != 0;
+  } else if (!strcmp(key, "flow_bpc") || !strcmp(key, "flow_bpc_w2")) {
+    if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "workgroups per CU must be in [1, 64]");
+    (!strcmp(key, "flow_bpc") ? ctx->flow_bpc : ctx->flow_bpc_w2) = value;
   } else if (!strcmp(key, "attn_splits")) {
     if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "attn_splits must be in [1, 64]");
     ctx->attn_splits = value;
@@ -609,6 +799,13 @@ extern "C" int yhip_debug_read(yhip_ctx* ctx, int which, float* host, size_t n) 
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   HIP_TRY(ctx, hipMemcpyAsync(host, src, n * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_step_stats(const yhip_ctx* ctx, double* us_total, int* steps) {
+  if (!ctx || !us_total || !steps) return fail(nullptr, YHIP_EINVAL, "null argument");
+  *us_total = ctx->stats_us;
+  *steps = ctx->stats_steps;
   return YHIP_OK;
 }
 
@@ -826,9 +1023,7 @@ extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const
   a.q_dim = (int)qd;
   a.kv_dim = (int)kvd;
   a.head_dim = head_dim;
-  a.rotary_dim = rotary_dim;
   a.msl = max_seq_len;
-  a.rope_theta = rope_theta;
   a.qkv_clip = qkv_clip;
   a.kcache = dk;
   a.vcache = dv;
@@ -943,8 +1138,8 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
     switch (kind) {
       case 0:
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
-        a.q_dim = rows - 2 * nkv * hd; a.kv_dim = nkv * hd; a.head_dim = hd; a.rotary_dim = hd; a.msl = msl;
-        a.rope_theta = 1e6f; a.kcache = kc; a.vcache = vc; a.params = dp; a.rope_cs = dcs; ek = kEpiQkvRope;
+        a.q_dim = rows - 2 * nkv * hd; a.kv_dim = nkv * hd; a.head_dim = hd; a.msl = msl;
+        a.kcache = kc; a.vcache = vc; a.params = dp; a.rope_cs = dcs; ek = kEpiQkvRope;
         if (a.q_dim < 0) return fail(nullptr, YHIP_EINVAL, "QKV bench needs rows >= 2048");
         break;
       case 1:

@@ -24,7 +24,7 @@ MODE_LOGITS = 1
 EXPORTS = (
     "yhip_create", "yhip_destroy", "yhip_upload_layer", "yhip_upload_globals", "yhip_forward",
     "yhip_forward_argmax", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
-    "yhip_debug_read", "yhip_last_error", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
+    "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
 )
 
@@ -66,6 +66,7 @@ def lib():
         "yhip_set_option": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.c_int]),
         "yhip_debug_read": (ctypes.c_int, [vp, ctypes.c_int, _f32p, ctypes.c_size_t]),
         "yhip_last_error": (ctypes.c_char_p, [vp]),
+        "yhip_step_stats": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_double), _ip]),
         "yhip_test_matvec": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, ctypes.c_int, ctypes.c_int,
                                             _f32p, _f32p]),
         "yhip_test_ffn": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p, ctypes.c_int,
@@ -184,6 +185,13 @@ class HipModel:
 
     def set_option(self, key, value):
         _check(lib().yhip_set_option(self.h, key.encode(), int(value)), self.h)
+
+    def step_stats(self):
+        """(device microseconds, steps) timed since set_option("stats", 1)."""
+        us = ctypes.c_double()
+        n = ctypes.c_int()
+        _check(lib().yhip_step_stats(self.h, ctypes.byref(us), ctypes.byref(n)), self.h)
+        return us.value, n.value
 
     def debug_read(self, which, n):
         out = np.zeros(n, np.float32)
