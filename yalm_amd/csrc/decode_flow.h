@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(kBlock) decode_flow_kernel(FlowArgs a) {
       at.inv_freq = a.inv_freq;
       at.params = nullptr;
       auto& sm = *reinterpret_cast<AttnSmem<HD, G, kBlock>*>(lds);
-      attn_run<HD, G, kBlock, true>(at, local % a.n_kv_heads, local / a.n_kv_heads, a.pos, sm, a.kvcur, tid);
+      attn_run<HD, G, kBlock, true, true>(at, local % a.n_kv_heads, local / a.n_kv_heads, a.pos, sm, a.kvcur, tid);
       break;
     }
     case kPhO: {  // reference src/infer.cpp:339-344

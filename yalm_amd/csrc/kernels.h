@@ -582,11 +582,14 @@ struct AttnGeom {
 
 // LDS of one attention workgroup. kcur/vcur hold the current token's fp16 K and V of the head
 // (used by the single-launch decode, which reads them from a coherent side buffer).
+constexpr int kMaxSplits = 64;  // KV slices per kv head (the partial buffer holds this many)
+
 template <int HD, int G, int NT>
 struct AttnSmem {
   float qs[G * HD];
   __attribute__((aligned(16))) float ps[G][AttnGeom<HD, NT>::TT];
   float red[2][G][NT / kWave];
+  float mrg[G][kMaxSplits][2];  // merge: per slice (weight, sum), then 1/L per head in red
   __attribute__((aligned(16))) uint32_t kcur[HD / 2];
   uint32_t vcur[HD / 2];
   unsigned last_flag;
@@ -602,13 +605,14 @@ struct AttnTileRegs {
 // One attention workgroup: kv head g, KV slice `split`, all G query heads of g; tid is the thread
 // index (passed in so that a caller's loop can keep lane-derived values from being hoisted).
 // HD: head_dim; G: query heads per kv head; NT: threads.
-// COH (single-launch decode): q is read and the output written with agent-coherent accesses, and
-// the current token's K/V (position kv_pos, just written by other workgroups of the same launch)
-// is taken from `kvcur` ([K pairs | V pairs] as packed fp16x2, coherent) instead of the cache.
+// COH: q is read and the output written with agent-coherent accesses (a later workgroup of the
+// same launch consumes it). SIDE_KV: the current token's K/V (position kv_pos, written by other
+// workgroups of the same launch) is taken from `kvcur` ([K pairs | V pairs] as packed fp16x2,
+// coherent) instead of the cache.
 // Partial sums stay per lane and are reduced over the LPD lanes once, after the last tile. Every
 // tile issues the same loads (addresses clamped into the cache, results masked), so the compiler
 // waits only for the tile it is about to use.
-template <int HD, int G, int NT, bool COH>
+template <int HD, int G, int NT, bool COH, bool SIDE_KV>
 __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, int pos, AttnSmem<HD, G, NT>& sm,
                                          const uint32_t* kvcur, int tid) {
   using Geo = AttnGeom<HD, NT>;
@@ -668,13 +672,15 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
 
   if constexpr (COH) {
     for (int e = tid; e < G * HD; e += NT) sm.qs[e] = load_shared(a.q + (long)g * G * HD + e);
+  } else {
+    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = a.q[(long)g * G * HD + e];
+  }
+  if constexpr (SIDE_KV) {
     for (int e = tid; e < HD / 2; e += NT) {
       sm.kcur[e] = __hip_atomic_load(kvcur + g * (HD / 2) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sm.vcur[e] = __hip_atomic_load(kvcur + (a.n_kv_heads + g) * (HD / 2) + e, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
     }
-  } else {
-    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = a.q[(long)g * G * HD + e];
   }
   AttnTileRegs<CPL, DPT> cur, nxt;
   load_tile(t_begin, cur);
@@ -694,7 +700,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
     const int tok = t0 + tok_l;
     const bool valid = tok < t_end;
     const int tv = t0 + 8 * oct;
-    if constexpr (COH) {
+    if constexpr (SIDE_KV) {
       if (kvp >= t0 && kvp < t0 + TT) {  // this tile holds the current token: take it from the side buffer
         if (tok == kvp) {
 #pragma unroll
@@ -798,7 +804,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
           for (int m = 0; m < DPT; ++m) {
             const int d = dgrp + NDG * m;
             float v = (float)__builtin_bit_cast(f16, vh[(long)d * a.msl + t]);
-            if constexpr (COH) {
+            if constexpr (SIDE_KV) {
               if (t == kvp) v = (float)__builtin_bit_cast(f16, vcur_h[d]);
             }
 #pragma unroll
@@ -854,21 +860,43 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
   }
   __syncthreads();
   if (!sm.last_flag) return;
+  // Merge (the last slice to finish): out = sum_s w_s o_s / sum_s w_s l_s, w_s = exp(m_s - max m).
+  // Every load of a round is issued before any is used: (max, sum) of all slices first, then each
+  // output's slices eight at a time (addresses clamped to the last slice, surplus dropped).
+  for (int e = tid; e < G * active; e += NT) {
+    const int h = e / active, sp = e - h * active;
+    const float* pp = a.partial + ((long)(g * G + h) * a.nsplit + sp) * stride;
+    sm.mrg[h][sp][0] = load_shared(pp + HD);
+    sm.mrg[h][sp][1] = load_shared(pp + HD + 1);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = kNegBig;
+    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, sm.mrg[tid][sp][0]);
+    float L = 0.f;
+    for (int sp = 0; sp < active; ++sp) {
+      const float w = expf(sm.mrg[tid][sp][0] - M);
+      sm.mrg[tid][sp][0] = w;
+      L = fmaf(sm.mrg[tid][sp][1], w, L);
+    }
+    sm.red[0][tid][0] = L;
+  }
+  __syncthreads();
   for (int e = tid; e < G * HD; e += NT) {
     const int h = e / HD, i = e % HD;
-    const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride;
-    float M = kNegBig;
-    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, load_shared(src + sp * stride + HD));
-    float L = 0.f, Ov = 0.f;
-    for (int sp = 0; sp < active; ++sp) {
-      const float* pp = src + sp * stride;
-      const float w = expf(load_shared(pp + HD) - M);
-      L = fmaf(load_shared(pp + HD + 1), w, L);
-      Ov = fmaf(load_shared(pp + i), w, Ov);
+    const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride + i;
+    float Ov = 0.f;
+    for (int sp0 = 0; sp0 < active; sp0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = load_shared(src + (long)min(sp0 + k, active - 1) * stride);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (sp0 + k < active) Ov = fmaf(v[k], sm.mrg[h][sp0 + k][0], Ov);
     }
     float* o = a.out + (long)(g * G + h) * HD + i;
-    if constexpr (COH) store_shared(o, Ov / L);
-    else *o = Ov / L;
+    if constexpr (COH) store_shared(o, Ov / sm.red[0][h][0]);
+    else *o = Ov / sm.red[0][h][0];
   }
   if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -877,7 +905,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
 template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   __shared__ AttnSmem<HD, G, kBlock> sm;
-  attn_run<HD, G, kBlock, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
+  attn_run<HD, G, kBlock, false, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------
