@@ -86,7 +86,8 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
  * kv head, default 512/n_kv_heads clamped to [1,64]),
- * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64), "stats" (1 = time
+ * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64; at least 128 from
+ * 1024 cached tokens on), "stats" (1 = time
  * every synchronised step on the device with HIP events and reset the totals; 0 = off).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default). */

@@ -113,9 +113,6 @@ template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) decode_flow_kernel(FlowArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ int s_bid;
-  __shared__ float s_best_v[kWavesPerBlock];
-  __shared__ int s_best_i[kWavesPerBlock];
-  __shared__ unsigned s_last;
   const int tid = threadIdx.x;
   const unsigned par = a.launch & 1u;
   const int ncnt = flow_counters(a.n_layers);
@@ -158,7 +155,6 @@ __global__ void __launch_bounds__(kBlock) decode_flow_kernel(FlowArgs a) {
   const char* lb = a.layers.wbase + (long)(layer < a.n_layers ? layer : 0) * a.layers.stride;
   uint16_t* kc = a.layers.kv + 2L * layer * a.layers.kv_elems;
   uint16_t* vc = kc + a.layers.kv_elems;
-  const uint16_t* erow = a.embed + (long)a.token * a.dim;
 
   MatvecArgs m;
   memset(&m, 0, sizeof(m));
@@ -168,15 +164,17 @@ __global__ void __launch_bounds__(kBlock) decode_flow_kernel(FlowArgs a) {
 
   switch (phase) {
     case kPhQkv: {  // reference src/infer.cpp:270-305
-      if (layer == 0 && local == 0)  // the residual stream starts as the embedding row (src/infer.cpp:460-481)
-        for (int i = tid; i < a.dim; i += kBlock) store_shared(a.x + i, (float)__builtin_bit_cast(f16, erow[i]));
       m.w0 = reinterpret_cast<const uint16_t*>(lb + a.layers.o_qkv);
       m.row_step = 2L * a.dim;
       m.r_step = a.dim;
       m.groups = (a.q_dim + 2 * a.kv_dim) / 2;
       m.K = a.dim;
       m.x = a.x;
-      m.x16 = layer == 0 ? erow : nullptr;
+      if (layer == 0) {  // the residual stream starts as the embedding row (src/infer.cpp:460-481)
+        m.emb = a.embed;
+        m.emb_out = a.x;
+        m.token = a.token;
+      }
       m.gain = reinterpret_cast<const float*>(lb + a.layers.o_ra);
       m.out = a.q;
       m.q_dim = a.q_dim;
@@ -247,46 +245,22 @@ __global__ void __launch_bounds__(kBlock) decode_flow_kernel(FlowArgs a) {
       break;
     }
     default: {  // final rmsnorm + lm_head (reference src/infer.cpp:501-527) + argmax (src/sampler.cpp:27-38)
-      if (a.n_layers == 0 && local == 0)
-        for (int i = tid; i < a.dim; i += kBlock) store_shared(a.x + i, (float)__builtin_bit_cast(f16, erow[i]));
       m.w0 = a.wcls;
       m.row_step = 2L * a.dim;
       m.r_step = a.dim;
       m.groups = a.vocab / 2;
       m.K = a.dim;
       m.x = a.x;
-      m.x16 = a.n_layers == 0 ? erow : nullptr;
+      if (a.n_layers == 0) {
+        m.emb = a.embed;
+        m.emb_out = a.x;
+        m.token = a.token;
+      }
       m.gain = a.rms_final;
       m.out = a.logits;
       m.track_max = 1;
       const RowMax mx = flow_matvec<2, kEpiStore>(m, local, a.nb[kPhLm], lds, wait);
-      const int lane = tid & (kWave - 1), wave = tid / kWave;
-      if (lane == 0) {
-        s_best_v[wave] = mx.v;
-        s_best_i[wave] = mx.i;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        float v = s_best_v[0];
-        int i = s_best_i[0];
-        for (int w = 1; w < kWavesPerBlock; ++w) better(v, i, s_best_v[w], s_best_i[w]);
-        store_shared(a.best_v + local, v);
-        __hip_atomic_store(a.best_i + local, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        publish();
-        const unsigned t =
-            __hip_atomic_fetch_add(a.sync + kSyncArgmax, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = t == (unsigned)(a.nb[kPhLm] - 1) ? 1u : 0u;
-      }
-      __syncthreads();
-      if (s_last && tid == 0) {
-        float v = kNegBig;
-        int i = 0x7fffffff;
-        for (int b = 0; b < a.nb[kPhLm]; ++b)
-          better(v, i, load_shared(a.best_v + b),
-                 __hip_atomic_load(a.best_i + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        a.result[0] = i == 0x7fffffff ? 0 : i;
-        __hip_atomic_store(a.sync + kSyncArgmax, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      argmax_finish(mx, local, a.nb[kPhLm], a.best_v, a.best_i, a.sync + kSyncArgmax, a.result);
       return;  // nothing waits for the lm_head
     }
   }

@@ -167,7 +167,9 @@ struct MatvecArgs {
   int groups;  // number of groups
   int K;       // row length (elements), multiple of 8
   const float* x;      // input vector [K]
-  const uint16_t* x16; // or an fp16 input vector (the embedding row), when not null
+  const uint16_t* emb; // or, when not null, row `token` of this fp16 embedding table [vocab][K]
+  float* emb_out;      // if not null, workgroup 0 also writes that row to it as fp32 (the residual stream)
+  int token;           // token id, or -1 to read params->token
   const float* gain;   // rmsnorm gain [K] or nullptr (no norm)
   float eps;
   float* out;
@@ -281,8 +283,8 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
 }
 
 template <bool COH>
-__device__ __forceinline__ float stage_src(const MatvecArgs& a, int i) {
-  if (a.x16) return (float)__builtin_bit_cast(f16, a.x16[i]);
+__device__ __forceinline__ float stage_src(const MatvecArgs& a, const uint16_t* x16, int i) {
+  if (x16) return (float)__builtin_bit_cast(f16, x16[i]);
   return ld_act<COH>(a.x + i);
 }
 
@@ -291,7 +293,7 @@ __device__ __forceinline__ float stage_src(const MatvecArgs& a, int i) {
 // exactly NPT float4 per thread, all loads issued before the first use; NPT == 0: any K % 4 == 0.
 // The step's RoPE table (head_dim floats) goes to LDS right after the vector.
 template <int NPT, bool COH>
-__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red, int pos) {
+__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red, int pos, const uint16_t* x16) {
   if (a.rope_cs) {
     for (int i = threadIdx.x; i < a.head_dim; i += kBlock) xs[a.K + i] = a.rope_cs[i];
   } else if (a.inv_freq) {  // reference src/infer.cpp:205-208
@@ -304,7 +306,7 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
   f32x4* o4 = reinterpret_cast<f32x4*>(xs);
   if constexpr (NPT > 0) {
     f32x4 xv[NPT], gv[NPT];
-    if (!COH && !a.x16) {
+    if (!COH && !x16) {
       const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
 #pragma unroll
       for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
@@ -312,7 +314,7 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
 #pragma unroll
       for (int k = 0; k < NPT; ++k)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[k][e] = stage_src<COH>(a, 4 * (threadIdx.x + kBlock * k) + e);
+        for (int e = 0; e < 4; ++e) xv[k][e] = stage_src<COH>(a, x16, 4 * (threadIdx.x + kBlock * k) + e);
     }
     if (a.gain) {
       const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
@@ -341,11 +343,11 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
     const int n4 = a.K >> 2;
     auto src4 = [&](int i) {
       f32x4 v;
-      if (!COH && !a.x16) {
+      if (!COH && !x16) {
         v = reinterpret_cast<const f32x4*>(a.x)[i];
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = stage_src<COH>(a, 4 * i + e);
+        for (int e = 0; e < 4; ++e) v[e] = stage_src<COH>(a, x16, 4 * i + e);
       }
       return v;
     };
@@ -405,6 +407,13 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
   const int wave_stride = nblk * kWavesPerBlock;
   int p = blk * kWavesPerBlock + wave;
   RowMax mx;
+  // embedding row as the input (reference src/infer.cpp:460-481: exact fp16 -> fp32)
+  const uint16_t* x16 = nullptr;
+  if (a.emb) {
+    x16 = a.emb + (long)(a.token >= 0 ? a.token : a.params->token) * a.K;
+    if (a.emb_out && blk == 0)
+      for (int i = threadIdx.x; i < a.K; i += kBlock) st_act<COH>(a.emb_out + i, (float)__builtin_bit_cast(f16, x16[i]));
+  }
 
   if constexpr (KC > 0) {
     // One register buffer: the first group's loads are in flight while the workgroup stages x
@@ -421,7 +430,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
     wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
     if (COH && p < a.groups) epilogue_prefetch<R, EPI, COH>(a, p, pre);
-    stage_input<KC / 2, COH>(a, xs, red, pos);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+    stage_input<KC / 2, COH>(a, xs, red, pos, x16);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
     while (p < a.groups) {
       float acc[R];
 #pragma unroll
@@ -449,7 +458,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
   } else {
     wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
-    stage_input<0, COH>(a, xs, red, pos);
+    stage_input<0, COH>(a, xs, red, pos, x16);
     const int nch = a.K >> 3;
     for (; p < a.groups; p += wave_stride) {
       const uint16_t* rows[R];
@@ -481,6 +490,67 @@ __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
   matvec_body<KC, R, EPI, false>(a, blockIdx.x, gridDim.x, lds, [] {});
 }
 
+// (max, index) over the lanes of a wave, then over the waves of the workgroup; tie rule of
+// reference src/sampler.cpp:27-38 (first index of the maximum). Every thread gets the result.
+__device__ __forceinline__ RowMax block_best(RowMax m, float* sv, int* si) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(m.v, o, kWave);
+    const int oi = __shfl_xor(m.i, o, kWave);
+    better(m.v, m.i, ov, oi);
+  }
+  if (lane == 0) {
+    sv[wave] = m.v;
+    si[wave] = m.i;
+  }
+  __syncthreads();
+  RowMax r;
+  r.v = sv[0];
+  r.i = si[0];
+  for (int w = 1; w < kWavesPerBlock; ++w) better(r.v, r.i, sv[w], si[w]);
+  __syncthreads();
+  return r;
+}
+
+// Per-workgroup (max, index) of a matvec's outputs combined into the argmax: workgroup `slot` of
+// `nslots` posts its best, the last to post (ticket) reduces all of them and zeroes the ticket for
+// the next launch.
+__device__ __forceinline__ void argmax_finish(RowMax mx, int slot, int nslots, float* best_v, int* best_i,
+                                              unsigned* ticket, int* result) {
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  __shared__ unsigned last;
+  const int tid = threadIdx.x;
+  const RowMax b = block_best(mx, sv, si);
+  if (tid == 0) {
+    store_shared(best_v + slot, b.v);
+    __hip_atomic_store(best_i + slot, b.i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    publish();
+    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = t == (unsigned)(nslots - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last) return;
+  RowMax m;
+  for (int s = tid; s < nslots; s += kBlock)
+    better(m.v, m.i, load_shared(best_v + s), __hip_atomic_load(best_i + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const RowMax r = block_best(m, sv, si);
+  if (tid == 0) {
+    result[0] = r.i == 0x7fffffff ? 0 : r.i;
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Final rmsnorm + lm_head with the greedy argmax fused in (a.track_max set).
+template <int KC>
+__global__ void __launch_bounds__(kBlock) lm_head_argmax_kernel(MatvecArgs a, float* best_v, int* best_i, unsigned* ticket,
+                                                               int* result) {
+  extern __shared__ float lds[];
+  const RowMax mx = matvec_body<KC, 2, kEpiStore, false>(a, blockIdx.x, gridDim.x, lds, [] {});
+  argmax_finish(mx, blockIdx.x, gridDim.x, best_v, best_i, ticket, result);
+}
+
 // ------------------------------------------------------------------------------------------
 // Per-step RoPE table: rope_cs[2k], rope_cs[2k+1] = cos, sin of (float)pos * inv_freq[k], the angle
 // of rotary pair k (reference src/infer.cpp:205-208: fp32 angle pos * freq, then cosf / sinf).
@@ -499,23 +569,12 @@ __global__ void rope_table_kernel(const float* inv_freq, float* rope_cs, int hal
 }
 
 // ------------------------------------------------------------------------------------------
-// Embedding gather (reference src/infer.cpp:460-481): x[i] = f32(E[token*dim + i]), exact.
-// Workgroup 0 also fills the step's RoPE table.
-// ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(kBlock) embed_kernel(const uint16_t* emb, float* x, int dim, const StepParams* params,
-                                                       const float* inv_freq, float* rope_cs, int half) {
-  const long base = (long)params->token * dim;
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < dim; i += gridDim.x * kBlock)
-    x[i] = (float)__builtin_bit_cast(f16, emb[base + i]);
-  if (blockIdx.x == 0) fill_rope_table(inv_freq, rope_cs, half, params->pos);
-}
-
-// ------------------------------------------------------------------------------------------
 // Split-KV GQA decode attention (reference src/infer.cpp:218-250, 327-336).
 //
 // Workgroup (g, s) handles kv head g and the s-th slice of [0, kv_len) for all G query heads
-// that share g, so each K/V byte is read once per token. Slices are at least min_slice tokens:
-//   chunk = max(min_slice, roundup(ceil(kv_len / nsplit), 64)),  active = ceil(kv_len / chunk)
+// that share g, so each K/V byte is read once per token. Slices are at least min_slice tokens
+// (128 from kv_len 1024 on):
+//   chunk = max(floor, roundup(ceil(kv_len / nsplit), 64)),  active = ceil(kv_len / chunk)
 // Workgroups past `active` exit at once. With one active slice the workgroup writes the output
 // directly; otherwise each writes (max, sum, acc) per head and the last to finish (atomic ticket)
 // merges them. Scores for a 256-token tile go to LDS; an online softmax keeps (max, sum, acc).
@@ -537,10 +596,13 @@ struct AttnArgs {
 
 constexpr int kMaxGroup = 8;
 
-__device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice) {
+// Tokens per KV slice. From 1024 cached tokens on, slices are at least 128 tokens (fewer, longer
+// slices: the merge and the per-workgroup start cost outweigh the extra parallelism there).
+__host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice) {
   int chunk = (kv_len + nsplit - 1) / nsplit;
   chunk = (chunk + 63) & ~63;
-  return chunk < min_slice ? min_slice : chunk;
+  const int floor = (kv_len >= 1024 && min_slice < 128) ? 128 : min_slice;
+  return chunk < floor ? floor : chunk;
 }
 
 // Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the

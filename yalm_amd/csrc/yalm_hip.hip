@@ -38,9 +38,14 @@ struct LayerW {
   bool loaded = false;
 };
 
-__global__ void set_params_kernel(StepParams* p, int token, int pos) {
-  p->token = token;
-  p->pos = pos;
+// The step's token and position, and its RoPE table (cos, sin of pos * inv_freq per rotary pair,
+// reference src/infer.cpp:205-208), written before each step so that a captured graph stays static.
+__global__ void set_params_kernel(StepParams* p, int token, int pos, const float* inv_freq, float* rope_cs, int half) {
+  if (threadIdx.x == 0) {
+    p->token = token;
+    p->pos = pos;
+  }
+  fill_rope_table(inv_freq, rope_cs, half, pos);
 }
 
 }  // namespace
@@ -147,7 +152,7 @@ int default_bpc(int K) { return K >= 8192 ? 1 : 2; }
 template <int KC, int R, EpiKind EPI>
 void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
   // reduction scratch + input vector (+ the RoPE table for the QKV epilogue)
-  const size_t lds = (16 + (size_t)a.K + (a.rope_cs ? (size_t)a.head_dim : 0)) * sizeof(float);
+  const size_t lds = (16 + (size_t)a.K + (a.rope_cs || a.inv_freq ? (size_t)a.head_dim : 0)) * sizeof(float);
   hipLaunchKernelGGL((matvec_kernel<KC, R, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
 }
 
@@ -188,6 +193,7 @@ MatvecArgs mv_base() {
   memset(&a, 0, sizeof(a));
   a.qkv_clip = 3.402823466e38f;
   a.pos = -1;
+  a.token = -1;
   return a;
 }
 
@@ -235,9 +241,6 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
   const yhip_config& c = ctx->c;
   hipStream_t s = ctx->stream;
   const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
-  hipLaunchKernelGGL(embed_kernel, dim3((c.dim + kBlock - 1) / kBlock), dim3(kBlock), 0, s, ctx->embed, ctx->x,
-                     c.dim, (const StepParams*)ctx->params, (const float*)ctx->inv_freq, ctx->rope_cs,
-                     c.head_dim / 2);
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& L = ctx->layers[l];
     int rc;
@@ -260,7 +263,11 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.kcache = ctx->kcache(l);
     a.vcache = ctx->vcache(l);
     a.params = ctx->params;
-    a.rope_cs = ctx->rope_cs;
+    a.rope_cs = ctx->rope_cs;  // the step's RoPE table, written by set_params_kernel
+    if (l == 0) {  // the residual stream starts as the token's embedding row (src/infer.cpp:460-481)
+      a.emb = ctx->embed;
+      a.emb_out = ctx->x;
+    }
     if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s))) return rc;
     // 2. attention
     AttnArgs t;
@@ -325,15 +332,33 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
   a.gain = ctx->rms_final;
   a.eps = c.norm_eps;
   a.out = ctx->logits;
-  if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s)) return rc;
-  if (mode == 1) {
+  a.params = ctx->params;
+  if (c.n_layers == 0) {
+    a.emb = ctx->embed;
+    a.emb_out = ctx->x;
+  }
+  if (mode == 1 || Rc != 2) {
+    if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s)) return rc;
+    if (mode == 2)
+      hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, (const float*)ctx->logits, c.vocab_size,
+                         ctx->argmax_dev);
+  } else {  // lm_head with the argmax fused in
+    a.track_max = 1;
+    const int blocks = std::max(1, std::min((a.groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * default_bpc(a.K)));
+    const size_t lds = (16 + (size_t)a.K) * sizeof(float);
+    if (a.K == 4096)
+      hipLaunchKernelGGL(lm_head_argmax_kernel<8>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->best_v, ctx->best_i,
+                         ctx->sync + kSyncArgmax, ctx->argmax_dev);
+    else
+      hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->best_v, ctx->best_i,
+                         ctx->sync + kSyncArgmax, ctx->argmax_dev);
+    HIP_TRY(ctx, hipGetLastError());
+  }
+  if (mode == 1)
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
-  } else {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, (const float*)ctx->logits, c.vocab_size,
-                       ctx->argmax_dev);
+  else
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, s));
-  }
   return YHIP_OK;
 }
 
@@ -412,9 +437,7 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.launch = ctx->flow_launches++;
   // attention workgroups: the active KV slices at this position (same rule as attn_run)
   const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
-  int chunk = (kv_len + ctx->attn_splits - 1) / ctx->attn_splits;
-  chunk = (chunk + 63) & ~63;
-  chunk = std::max(chunk, ctx->attn_min_slice);
+  const int chunk = attn_chunk(kv_len, ctx->attn_splits, ctx->attn_min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
   const int cus = ctx->num_cus;
   d.nb[kPhQkv] = phase_blocks((d.q_dim + 2 * d.kv_dim) / 2, cus, ctx->flow_bpc);
@@ -482,7 +505,8 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
     if (!ctx->layers[l].loaded) return fail(ctx, YHIP_ESTATE, "layer " + std::to_string(l) + " not uploaded");
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   if (ctx->use_flow) return launch_flow_step(ctx, token, pos, mode);
-  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(1), 0, ctx->stream, ctx->params, token, pos);
+  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->params, token, pos,
+                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2);
   HIP_TRY(ctx, hipGetLastError());
   if (!ctx->use_graph) return enqueue_step(ctx, mode);
   if (!ctx->graph[mode]) {
