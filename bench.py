@@ -6,7 +6,9 @@
 Workloads (synthetic, seeded; no checkpoint download):
   decode  dim 4096, hidden 14336, 32 layers, 32/8 heads, vocab 32000, ctx 4096: 32 prompt ids then
           K greedy tokens (default 120). This is the headline line.
-  long    same model; a 3200-token prompt hydrated token by token, then K greedy tokens at kv ~3200.
+  long    same model; a 3200-token prompt prefilled in one batched call (MFMA GEMMs + causal MFMA
+          attention; reported separately as prefill tok/s, TFLOP/s and matrix-core utilisation),
+          then K greedy tokens at kv ~3200.
   attn    same model at ctx 16448 with the KV cache pre-filled ~N(0,1) to 16384 positions, then K
           greedy tokens at kv ~16400.
 
@@ -40,6 +42,16 @@ PEAK_GBS = 8000.0
 WEIGHT_BYTES = 14_221_860_864       # all layer weights + lm_head + one embedding row + fp32 gains
 KV_BYTES_PER_POS = 131_072          # 32 layers x 8 kv heads x 128 x (K + V) x 2 bytes
 W13_BYTES = 2 * 14336 * 4096 * 2 + 4096 * 4 * 2 + 14336 * 4  # weights + x + gain + hb out
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
+
+
+def prefill_flops(cfg, n, start=0):
+    """Dense matmul FLOPs of n prompt tokens through every layer (2 per weight per token) plus the
+    causal attention (QK^T and PV: 4 * head_dim * n_heads per key-query pair)."""
+    d, hid, hd, nh, nkv = cfg["dim"], cfg["hidden_dim"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"]
+    w_layer = (nh * hd + 2 * nkv * hd) * d + d * nh * hd + 3 * d * hid
+    pairs = sum(start + i + 1 for i in range(n))
+    return cfg["n_layers"] * (2.0 * n * w_layer + 4.0 * hd * nh * pairs)
 
 
 def log(*a):
@@ -166,7 +178,34 @@ def main():
         start_pos = fill_pos
         log(f"[bench] KV cache pre-filled to {fill_pos} positions")
 
+    prefill = None
+    if wl == "long":
+        view = hip.HipModel.attach(ctxp, cfg)
+        view.prefill(prompt[:256])  # warm-up (kernels loaded, workspace sized)
+        view.prefill(prompt)
+        t0 = time.perf_counter()
+        lg = view.prefill(prompt)
+        pf_s = time.perf_counter() - t0
+        fl = prefill_flops(cfg, n_prompt)
+        prefill = {"tokens": n_prompt, "seconds": round(pf_s, 5), "tok_s": round(n_prompt / pf_s, 1),
+                   "tflops": round(fl / pf_s / 1e12, 1), "mfma_frac": round(fl / pf_s / 1e12 / PEAK_FP16_TFLOPS, 4),
+                   "flops": fl, "peak_tflops": PEAK_FP16_TFLOPS}
+        log(f"[bench] prefill {n_prompt} tokens: {pf_s * 1e3:.1f} ms = {n_prompt / pf_s:.0f} tok/s, "
+            f"{fl / pf_s / 1e12:.0f} TFLOP/s ({100 * fl / pf_s / 1e12 / PEAK_FP16_TFLOPS:.1f}% of fp16 peak)")
+        first_tok = int(np.argmax(lg))
+
     def run(n_steps):
+        if wl == "long":
+            # greedy decode from the prefilled cache
+            toks, secs = [], []
+            tok = first_tok
+            view = hip.HipModel.attach(ctxp, cfg)
+            for i in range(n_steps):
+                s = time.perf_counter()
+                tok = view.forward_argmax(tok, n_prompt + i)
+                secs.append(time.perf_counter() - s)
+                toks.append(tok)
+            return np.array(toks), np.array(secs), 0.0
         if wl != "attn":
             return sess.generate(prompt, n_steps, temperature=0.0, device_argmax=True)
         # decode directly from position 16384 with greedy argmax on the device
@@ -250,7 +289,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": {"decode": "Mistral-7B-shape fp16 decode: 32 random prompt ids then greedy tokens, ctx 4096",
-                         "long": "Mistral-7B-shape fp16 decode after a 3200-token prompt, ctx 4096",
+                         "long": "Mistral-7B-shape fp16 decode after a 3200-token batched prefill, ctx 4096",
                          "attn": "Mistral-7B-shape fp16 decode over a KV cache pre-filled to 16384, ctx 16448"}[wl],
             "dim": 4096, "hidden_dim": 14336, "n_layers": 32, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128,
             "vocab": 32000, "context": ctx_len, "prompt_tokens": n_prompt, "global_batch": 1,
@@ -263,6 +302,8 @@ def main():
         "device_us_per_step": round(step_us, 2),
         "cpu_baseline": cpu,
     }
+    if prefill is not None:
+        out["prefill"] = prefill
     print(json.dumps(out), flush=True)
     sess.close()
 

@@ -73,6 +73,16 @@ int yhip_forward(yhip_ctx* ctx, int token, int pos, int mode, float* logits_host
  * the device with the reference tie rule (src/sampler.cpp:27-38). */
 int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_token);
 
+/* Batched prompt prefill: tokens[0..n) at positions start_pos .. start_pos+n-1 go through every
+ * layer together (MFMA GEMMs with fused epilogues, causal MFMA attention) and their K/V land in the
+ * caches, as n calls of yhip_forward(YHIP_MODE_HYDRATE) would leave them (src/main.cpp:169-177,
+ * src/infer.cpp:256-392). If logits_host is not NULL the call returns after it holds the last
+ * token's logits; otherwise it may return before the device finishes. Ring positions
+ * (start_pos + n > max_seq_len) and shapes without the batched kernels (head_dim not 32/64/128;
+ * dim, hidden_dim, n_heads*head_dim or max_seq_len not a multiple of 32) run token by token.
+ * No reference counterpart: the reference hydrates one token per forward. */
+int yhip_prefill(yhip_ctx* ctx, const int* tokens, int n, int start_pos, float* logits_host);
+
 /* Pinned host buffer [vocab] that yhip_forward fills without an extra copy when passed back. */
 float* yhip_logits_host(yhip_ctx* ctx);
 
@@ -128,6 +138,11 @@ int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* 
                   const uint16_t* wv, int dim, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
                   int rotary_dim, float rope_theta, float qkv_clip, int pos, float* q_out, uint16_t* kcache,
                   uint16_t* vcache);
+/* The prefill GEMM: A [M][K], B and B3 [N][K] fp16, K a multiple of 32. mode 0: c = A B^T;
+ * mode 1: c += A B^T (c holds the addend on entry); mode 2: h = fp16(act(A B^T) * (A B3^T)) with
+ * act 1 silu, 0 gelu (the SwiGLU of src/infer.cpp:362-382). c [M][N] fp32, h [M][N] fp16. */
+int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16_t* b3, int M, int N, int K, int mode, int act,
+                   float* c, uint16_t* h);
 /* Greedy argmax on the device with the reference tie rule. */
 int yhip_test_argmax(const float* logits, int n, int* out);
 

@@ -1,0 +1,142 @@
+"""Batched prefill (MFMA GEMMs + causal MFMA attention) against the reference's sequential hydrate.
+
+The reference has no batched prefill: a prompt goes through forward() one token at a time
+(src/main.cpp:169-177). Prefill must leave the same K/V cache entries (indices exact, values within
+fp16-activation tolerance) and the same last-token logits (rel-L2 <= 1e-2, the decode contract).
+Activations enter the matrix cores as fp16, so the values differ from the fp32 oracle by about the
+fp16 rounding of an activation (~1e-3 relative)."""
+import numpy as np
+import pytest
+
+from oracle import binding as O
+from tests import npref
+from tests.util import MICRO, TINY, np_tensors, h2f, f16
+
+pytestmark = pytest.mark.gpu
+
+PREFILL_LOGIT_TOL = 1e-2
+
+
+def hip():
+    from yalm_amd import hip as H
+    H.lib()
+    return H
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096)])
+def test_gemm_store_and_residual(M, N, K):
+    H = hip()
+    rng = np.random.default_rng(M * 7 + N)
+    a = f16(rng.standard_normal((M, K)))
+    b = f16(rng.standard_normal((N, K)) * 0.05)
+    want = h2f(a).astype(np.float64) @ h2f(b).astype(np.float64).T
+    got = H.gemm(a, b, mode=0)
+    assert npref.rel_l2(got, want) < 1e-6
+    c0 = rng.standard_normal((M, N)).astype(np.float32)
+    got = H.gemm(a, b, mode=1, c=c0)
+    assert npref.rel_l2(got, c0 + want) < 1e-6
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 64, 64), (150, 192, 256), (33, 96, 32)])
+def test_gemm_swiglu(M, N, K):
+    H = hip()
+    rng = np.random.default_rng(M + N)
+    a = f16(rng.standard_normal((M, K)))
+    b1 = f16(rng.standard_normal((N, K)) * 0.1)
+    b3 = f16(rng.standard_normal((N, K)) * 0.1)
+    A = h2f(a).astype(np.float64)
+    g = A @ h2f(b1).astype(np.float64).T
+    u = A @ h2f(b3).astype(np.float64).T
+    want = g / (1 + np.exp(-g)) * u
+    got = h2f(H.gemm(a, b1, mode=2, b3=b3))
+    assert npref.rel_l2(got, want) < 2e-3  # fp16 output
+
+
+def _sequential(om, toks, start=0):
+    for i, t in enumerate(toks):
+        lo = om.forward(int(t), start + i, 1 if i == len(toks) - 1 else 0)
+    return lo
+
+
+def _check_kv_close(om, hm, n_layers, positions):
+    for layer in range(n_layers):
+        ko, vo = om.kv(layer)
+        kh, vh = hm.kv(layer)
+        assert np.array_equal(ko != 0, kh != 0)  # the same entries are written
+        assert np.array_equal(vo != 0, vh != 0)
+        for a, b in ((kh, ko), (vh, vo)):
+            fa, fb = h2f(a), h2f(b)
+            assert npref.rel_l2(fa, fb) < 1e-2, layer
+            assert np.max(np.abs(fa - fb)) <= 3e-2 * np.max(np.abs(fb)), layer
+
+
+@pytest.mark.parametrize("cfg_name,n", [("tiny", 40), ("tiny", 97), ("micro", 20)])
+def test_prefill_matches_sequential_hydrate(cfg_name, n):
+    # micro has head_dim 16: prefill runs it token by token through the decode path
+    cfg = dict(TINY if cfg_name == "tiny" else MICRO)
+    t = np_tensors(cfg, seed=41, std=0.02 if cfg_name == "tiny" else 0.1)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    toks = np.random.default_rng(42).integers(0, cfg["vocab_size"], n)
+    lo = _sequential(om, toks)
+    lh = hm.prefill(toks)
+    assert npref.rel_l2(lh, lo) < PREFILL_LOGIT_TOL
+    _check_kv_close(om, hm, cfg["n_layers"], n)
+    # decoding continues from the prefilled cache
+    nxt = O.argmax(lo)
+    assert npref.rel_l2(hm.forward(nxt, n), om.forward(nxt, n)) < PREFILL_LOGIT_TOL
+    hm.close()
+
+
+def test_prefill_in_chunks_and_after_decode_steps():
+    cfg = dict(TINY)
+    t = np_tensors(cfg, seed=43)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    toks = np.random.default_rng(44).integers(0, cfg["vocab_size"], 80)
+    for i in range(5):  # five decode steps first
+        om.forward(int(toks[i]), i, 0)
+        hm.forward(int(toks[i]), i, 0)
+    hm.prefill(toks[5:45], start_pos=5, logits=False)  # then two prefill chunks
+    lh = hm.prefill(toks[45:80], start_pos=45)
+    lo = _sequential(om, toks[5:80], start=5)
+    assert npref.rel_l2(lh, lo) < PREFILL_LOGIT_TOL
+    _check_kv_close(om, hm, cfg["n_layers"], 80)
+    hm.close()
+
+
+def test_prefill_mistral_shape_two_layers():
+    cfg = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32, n_kv_heads=8,
+               max_seq_len=512, rotary_dim=128)
+    t = np_tensors(cfg, seed=45)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    toks = np.random.default_rng(46).integers(0, cfg["vocab_size"], 200)
+    lo = _sequential(om, toks)
+    lh = hm.prefill(toks)
+    assert npref.rel_l2(lh, lo) < PREFILL_LOGIT_TOL
+    _check_kv_close(om, hm, cfg["n_layers"], 200)
+    hm.close()
+
+
+def test_prefill_ring_positions_fall_back_to_steps():
+    # start + n beyond max_seq_len: the StreamingLLM ring (src/infer.cpp:489-494) runs step by step
+    cfg = dict(TINY, max_seq_len=64)
+    t = np_tensors(cfg, seed=47)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    toks = np.random.default_rng(48).integers(0, cfg["vocab_size"], 80)
+    lo = _sequential(om, toks)
+    lh = hm.prefill(toks)
+    assert npref.rel_l2(lh, lo) < 1e-4  # the decode path: fp32 throughout
+    hm.close()
+
+
+def test_prefill_rejects_bad_arguments():
+    H = hip()
+    cfg = dict(TINY)
+    with H.HipModel(cfg, np_tensors(cfg, seed=49)) as m:
+        with pytest.raises(H.HipError):
+            m.prefill([1, 2, cfg["vocab_size"]])
+        with pytest.raises(H.HipError):
+            m.prefill([1, 2], start_pos=-1)

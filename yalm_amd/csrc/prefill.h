@@ -1,0 +1,341 @@
+// Batched prompt prefill on the CDNA4 matrix cores (gfx950).
+//
+// A prompt of n tokens goes through each layer as n rows at once, so the decode matvecs become
+// GEMMs (reference semantics: the sequential hydrate of src/main.cpp:169-177 through
+// src/infer.cpp:256-392, one token at a time; prefill computes the same K/V cache entries and the
+// last token's logits):
+//   X [n][dim] fp32 residual stream      -> rmsnorm rows -> Xn [n][dim] fp16
+//   Xn . Wqkv^T (MFMA)                    -> C [n][q+2kv] fp32 -> clip, RoPE -> Q fp16, K/V cache
+//   causal GQA attention (MFMA)           -> A [n][q] fp16
+//   X += A . Wo^T (MFMA, residual epilogue)
+//   rmsnorm rows -> Xn; H = act(Xn W1^T) * (Xn W3^T) (MFMA, SwiGLU epilogue) -> H [n][hidden] fp16
+//   X += H . W2^T (MFMA, residual epilogue)
+// Activations enter the matrix cores in fp16 and accumulate in fp32.
+//
+// MFMA operand layout (v_mfma_f32_32x32x16_f16, one wave): lane l holds row l%32 of A and column
+// l%32 of B, eight k values each, group l/32; which eight k a lane holds is free as long as A and
+// B agree. Accumulator register r of lane l is row 8(r/4) + 4(l/32) + r%4, column l%32.
+#pragma once
+#include "kernels.h"
+
+namespace yk {
+
+typedef f16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// ------------------------------------------------------------------------------------------
+// GEMM C[M][N] = A[M][K] . B[N][K]^T, A and B fp16 row-major (both K-contiguous, as activations
+// and .yalm weights are). Block tile 128 x 128 x 32, four waves in 2 x 2, each a 64 x 64 tile of
+// four 32x32 MFMA tiles; A and B tiles double-buffered through LDS (rows padded to 40 halves so
+// the fragment reads are conflict-free). Rows past M and columns past N are clamped on load and
+// masked on store. K must be a multiple of 32.
+// Epilogues: STORE C = acc; RESID C += acc; SWIGLU: the block's 128 B rows are 64 rows of W1 and
+// the same 64 rows of W3, interleaved by 32, so each lane holds act(w1) and w3 of one output;
+// H[m][j] = fp16(act(w1) * w3) with N counting output columns.
+// ------------------------------------------------------------------------------------------
+enum GemmEpi : int { kGemmStore = 0, kGemmResid = 1, kGemmSwiGLU = 2 };
+
+struct GemmArgs {
+  const uint16_t* A;
+  long lda;
+  const uint16_t* B;   // [N][K] (SwiGLU: W1)
+  const uint16_t* B3;  // SwiGLU: W3 [N][K]
+  long ldb;
+  float* C;            // STORE / RESID target [M][ldc]
+  long ldc;
+  uint16_t* H;         // SwiGLU target [M][ldh] fp16
+  long ldh;
+  int M, N, K;
+  int act;  // SwiGLU: 1 silu, 0 gelu
+};
+
+constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_nt_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kGBM * kGLds];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGBN * kGLds];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kGBM;
+  // SwiGLU: this block's 64 output columns j0..j0+63
+  const int n0 = EPI == kGemmSwiGLU ? blockIdx.x * (kGBN / 2) : blockIdx.x * kGBN;
+
+  // global -> LDS: 128 rows x 4 chunks of 8 halves per operand; thread t moves chunks t, t + 256
+  const uint16_t* arow[2];
+  const uint16_t* brow[2];
+  int lofs[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i, row = c >> 2, kc = c & 3;
+    lofs[i] = row * kGLds + kc * 8;
+    arow[i] = g.A + (long)min(m0 + row, g.M - 1) * g.lda + kc * 8;
+    if constexpr (EPI == kGemmSwiGLU) {
+      // B tile row r: W1 for (r/32) even, W3 for odd; output column n0 + (r/64)*32 + r%32
+      const int col = n0 + (row >> 6) * 32 + (row & 31);
+      const uint16_t* base = ((row >> 5) & 1) ? g.B3 : g.B;
+      brow[i] = base + (long)min(col, g.N - 1) * g.ldb + kc * 8;
+    } else {
+      brow[i] = g.B + (long)min(n0 + row, g.N - 1) * g.ldb + kc * 8;
+    }
+  }
+  u32x4 ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
+      rb[i] = *reinterpret_cast<const u32x4*>(brow[i] + k0);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<u32x4*>(&As[buf][lofs[i]]) = ra[i];
+      *reinterpret_cast<u32x4*>(&Bs[buf][lofs[i]]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int nk = g.K / kGBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * kGBK);
+#pragma unroll
+    for (int ks = 0; ks < kGBK / 16; ++ks) {
+      const int kofs = ks * 16 + 8 * (lane >> 5);
+      u32x4 fa[2], fb[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        fa[t] = *reinterpret_cast<const u32x4*>(&As[buf][(wm * 64 + t * 32 + (lane & 31)) * kGLds + kofs]);
+        fb[t] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wn * 64 + t * 32 + (lane & 31)) * kGLds + kofs]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + i * 32 + acc_row(r, lane);
+      if (m >= g.M) continue;
+      if constexpr (EPI == kGemmSwiGLU) {
+        const int j = n0 + wn * 32 + (lane & 31);
+        if (j < g.N) {
+          const float a1 = acc[i][0][r], a3 = acc[i][1][r];
+          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+          if (n >= g.N) continue;
+          float* cp = g.C + (long)m * g.ldc + n;
+          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
+          else *cp = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Row kernels of the prefill (one workgroup per row).
+// ------------------------------------------------------------------------------------------
+// X[t][i] = fp32(E[tokens[t]][i]) (reference src/infer.cpp:460-481, exact)
+__global__ void __launch_bounds__(kBlock) embed_rows_kernel(const uint16_t* emb, const int* tokens, float* X, int dim) {
+  const int t = blockIdx.x;
+  const uint16_t* e = emb + (long)tokens[t] * dim;
+  for (int i = threadIdx.x; i < dim; i += kBlock) X[(long)t * dim + i] = (float)__builtin_bit_cast(f16, e[i]);
+}
+
+// Xn[t] = fp16(X[t] * inv * g), inv = 1/sqrt(mean(X[t]^2) + eps) (reference src/infer.cpp:136-146)
+__global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, const float* gain, float eps, int dim,
+                                                              uint16_t* Xn) {
+  __shared__ float red[kWavesPerBlock];
+  const float* x = X + (long)blockIdx.x * dim;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += kBlock) ss += x[i] * x[i];
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+  uint16_t* o = Xn + (long)blockIdx.x * dim;
+  for (int i = threadIdx.x; i < dim; i += kBlock) o[i] = __builtin_bit_cast(uint16_t, (f16)(x[i] * inv * gain[i]));
+}
+
+// Row t of the QKV GEMM output (position start + t): clip, RoPE on q and k pairs
+// (reference src/infer.cpp:197-215, 284-305), q as fp16 into Q, k and v as fp16 into the caches at
+// the row's position (no ring: start + n <= max_seq_len).
+__global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int head_dim,
+                                                          float qkv_clip, const float* inv_freq, int start, int msl,
+                                                          uint16_t* Q, uint16_t* kcache, uint16_t* vcache) {
+  const int t = blockIdx.x, pos = start + t;
+  const float* c = C + (long)t * ldc;
+  const int pairs = (q_dim + 2 * kv_dim) / 2;
+  for (int p = threadIdx.x; p < pairs; p += kBlock) {
+    const int i = 2 * p;
+    float v0 = clipf(c[i], qkv_clip), v1 = clipf(c[i + 1], qkv_clip);
+    if (i < q_dim + kv_dim) {
+      const int j = i % head_dim;
+      const float ang = (float)pos * inv_freq[j / 2];
+      const float cs = cosf(ang), sn = sinf(ang);
+      const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
+      v0 = r0;
+      v1 = r1;
+    }
+    const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0), h1 = __builtin_bit_cast(uint16_t, (f16)v1);
+    if (i < q_dim) {
+      Q[(long)t * q_dim + i] = h0;
+      Q[(long)t * q_dim + i + 1] = h1;
+    } else {
+      const bool is_k = i < q_dim + kv_dim;
+      const int ik = i - q_dim - (is_k ? 0 : kv_dim);
+      const int g = ik / head_dim, j = ik % head_dim;
+      const long head = (long)g * head_dim * msl;
+      if (is_k) {
+        kcache[head + k_cache_idx(j, pos, msl)] = h0;
+        kcache[head + k_cache_idx(j + 1, pos, msl)] = h1;
+      } else {
+        vcache[head + (long)j * msl + pos] = h0;
+        vcache[head + (long)(j + 1) * msl + pos] = h1;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Causal GQA prefill attention on MFMA (reference src/infer.cpp:218-250 per query position:
+// scores over keys 0..pos read back from the fp16 cache, softmax with max subtraction, weighted
+// sum of V). Workgroup = one kv head g and 32 consecutive queries; wave w serves query head
+// g*G + w, so the four waves share the head's K/V.
+// Per 32-key tile a wave computes S^T = K Q^T (keys as rows), so each lane holds 16 scores of one
+// query (its partner lane l^32 the other 16) and runs the online softmax for that query with one
+// cross-half exchange; then O^T += V^T P^T, whose B operand is exactly the lane's own
+// probabilities (the MFMA k order is chosen to match the score layout), so nothing goes through
+// LDS. O^T keeps the query in the column, so the softmax rescale and the final 1/sum are
+// lane-local. Queries are at positions start + t; keys are the cache entries 0 .. position.
+// Requires HD % 32 == 0 and max_seq_len % 32 == 0.
+// ------------------------------------------------------------------------------------------
+struct PrefillAttnArgs {
+  const uint16_t* Q;   // [n][n_heads * HD] fp16
+  const uint16_t* kcache;
+  const uint16_t* vcache;
+  uint16_t* out;       // [n][n_heads * HD] fp16
+  int n, start, msl, n_heads, n_kv_heads, n_qtiles;
+};
+
+template <int HD, int G>
+__global__ void __launch_bounds__(64 * G) prefill_attn_kernel(PrefillAttnArgs a) {
+  static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
+  constexpr int KS = HD / 16;  // k steps of the score MFMA
+  constexpr int DT = HD / 32;  // 32-dim tiles of the output
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qt = a.n_qtiles - 1 - blockIdx.x;  // longest (latest) query tiles first
+  const int g = blockIdx.y;
+  const int h = g * G + wave;
+  const int q0 = qt * 32;
+  const int qd = a.n_heads * HD;
+  const int my_q = q0 + (lane & 31);                 // this lane's query row
+  const int q_pos = a.start + my_q;                  // its position
+  const int last_pos = a.start + min(q0 + 31, a.n - 1);
+  const uint16_t* kh = a.kcache + (long)g * HD * a.msl;
+  const uint16_t* vh = a.vcache + (long)g * HD * a.msl;
+  const int half = lane >> 5;
+
+  // Q^T fragments: column = query my_q, k = dims 16 ks + 8 half + e
+  u32x4 qf[KS];
+  {
+    const uint16_t* qrow = a.Q + (long)min(my_q, a.n - 1) * qd + h * HD + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks);
+  }
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x16{};
+  float m_run = kNegBig, l_run = 0.f;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  const int nkt = last_pos / 32 + 1;
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * 32;
+    // S^T: rows = keys k0 + (lane & 31) for the K operand; K[g][c][t][16], chunk c = ks
+    f32x16 s = f32x16{};
+    const uint16_t* krow = kh + (long)(k0 + (lane & 31)) * 16 + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + (long)ks * 16 * a.msl);
+      s = mfma32(kf, qf[ks], s);
+    }
+    // mask (key position > query position), scale, tile max of this query
+    float mt = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + acc_row(r, lane);
+      s[r] = key <= q_pos ? s[r] * scale : kNegBig;
+      mt = fmaxf(mt, s[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float corr = expf(m_run - m_new);
+    float ps = 0.f;
+    u32x4 pf[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      half8 p8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = 8 * kk + e;
+        const float p = s[r] > kNegBig ? expf(s[r] - m_new) : 0.f;
+        ps += p;
+        p8[e] = (f16)p;
+      }
+      pf[kk] = __builtin_bit_cast(u32x4, p8);
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * corr + ps;
+    m_run = m_new;
+    // O^T += V^T P^T; k order of step kk: keys k0 + 16 kk + {0..3, 8..11} + 4 half
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+      const uint16_t* vrow = vh + (long)(t * 32 + (lane & 31)) * a.msl + k0 + 4 * half;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * kk);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * kk + 8);
+        const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
+        o[t] = mfma32(vf, pf[kk], o[t]);
+      }
+    }
+  }
+  if (my_q < a.n) {
+    const float inv = 1.0f / l_run;
+    uint16_t* orow = a.out + (long)my_q * qd + h * HD;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) orow[t * 32 + acc_row(r, lane)] = __builtin_bit_cast(uint16_t, (f16)(o[t][r] * inv));
+  }
+}
+
+}  // namespace yk

@@ -16,6 +16,7 @@
 
 #include "../../include/yalm_hip.h"
 #include "decode_flow.h"
+#include "prefill.h"
 #include "kernels.h"
 
 using namespace yk;
@@ -100,6 +101,17 @@ struct yhip_ctx {
   uint32_t* kvcur = nullptr;  // current position's K/V as fp16 pairs
   float* best_v = nullptr;
   int* best_i = nullptr;
+
+  // batched prefill workspace (grown on demand, prefill.h)
+  int pf_cap = 0;
+  char* pf_base = nullptr;
+  float* pf_X = nullptr;     // [n][dim]
+  uint16_t* pf_Xn = nullptr; // [n][dim] fp16 normalised rows
+  uint16_t* pf_H = nullptr;  // [n][hidden] fp16 SwiGLU output
+  float* pf_C = nullptr;     // [n][q + 2kv]
+  uint16_t* pf_Q = nullptr;  // [n][q]
+  uint16_t* pf_A = nullptr;  // [n][q]
+  int* pf_tok = nullptr;     // [n]
 
   // device timing of synchronised steps ("stats" option)
   bool stats = false;
@@ -530,6 +542,171 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
   return YHIP_OK;
 }
 
+// ---- batched prefill ---------------------------------------------------------------------------
+template <int EPI>
+int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
+  if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
+  const int ncols = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;
+  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
+template <int HD>
+bool launch_prefill_attn_hd(const PrefillAttnArgs& p, int G, hipStream_t s) {
+  const dim3 grid(p.n_qtiles, p.n_kv_heads);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((prefill_attn_kernel<HD, 1>), grid, dim3(64), 0, s, p); return true;
+    case 2: hipLaunchKernelGGL((prefill_attn_kernel<HD, 2>), grid, dim3(128), 0, s, p); return true;
+    case 4: hipLaunchKernelGGL((prefill_attn_kernel<HD, 4>), grid, dim3(256), 0, s, p); return true;
+    case 8: hipLaunchKernelGGL((prefill_attn_kernel<HD, 8>), grid, dim3(512), 0, s, p); return true;
+    default: return false;
+  }
+}
+
+// The batched path needs head_dim a multiple of 32, row lengths multiples of 32 and a context
+// that is a multiple of 32; other shapes prefill token by token.
+bool prefill_supported(const yhip_config& c, int q_dim) {
+  const int G = c.n_heads / c.n_kv_heads;
+  return (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+         c.dim % 32 == 0 && c.hidden_dim % 32 == 0 && q_dim % 32 == 0 && c.max_seq_len % 32 == 0;
+}
+
+int ensure_prefill_ws(yhip_ctx* ctx, int n) {
+  if (n <= ctx->pf_cap) return YHIP_OK;
+  const yhip_config& c = ctx->c;
+  const size_t qd = ctx->q_dim(), kvd = ctx->kv_dim(), N = (size_t)n;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes, 256);
+    return o;
+  };
+  const size_t oX = take(N * c.dim * 4), oXn = take(N * c.dim * 2), oH = take(N * c.hidden_dim * 2),
+               oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oA = take(N * qd * 2), oT = take(N * 4);
+  if (ctx->pf_base) hipFree(ctx->pf_base);
+  ctx->pf_base = nullptr;
+  ctx->pf_cap = 0;
+  if (hipMalloc(&ctx->pf_base, off) != hipSuccess) return fail(ctx, YHIP_EDEVICE, "out of device memory for prefill");
+  ctx->pf_X = (float*)(ctx->pf_base + oX);
+  ctx->pf_Xn = (uint16_t*)(ctx->pf_base + oXn);
+  ctx->pf_H = (uint16_t*)(ctx->pf_base + oH);
+  ctx->pf_C = (float*)(ctx->pf_base + oC);
+  ctx->pf_Q = (uint16_t*)(ctx->pf_base + oQ);
+  ctx->pf_A = (uint16_t*)(ctx->pf_base + oA);
+  ctx->pf_tok = (int*)(ctx->pf_base + oT);
+  ctx->pf_cap = n;
+  return YHIP_OK;
+}
+
+int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logits_host) {
+  const yhip_config& c = ctx->c;
+  hipStream_t s = ctx->stream;
+  const int qd = ctx->q_dim(), kvd = ctx->kv_dim(), G = c.n_heads / c.n_kv_heads;
+  if (int rc = ensure_prefill_ws(ctx, n)) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->pf_tok, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const uint16_t*)ctx->embed,
+                     (const int*)ctx->pf_tok, ctx->pf_X, c.dim);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& L = ctx->layers[l];
+    int rc;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_X,
+                       (const float*)L.rms_att, c.norm_eps, c.dim, ctx->pf_Xn);
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.A = ctx->pf_Xn;
+    g.lda = c.dim;
+    g.B = L.wqkv;
+    g.ldb = c.dim;
+    g.C = ctx->pf_C;
+    g.ldc = qd + 2 * kvd;
+    g.M = n;
+    g.N = qd + 2 * kvd;
+    g.K = c.dim;
+    if ((rc = launch_gemm<kGemmStore>(ctx, g, s))) return rc;
+    hipLaunchKernelGGL(qkv_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_C, qd + 2 * kvd, qd, kvd,
+                       c.head_dim, c.qkv_clip, (const float*)ctx->inv_freq, start, c.max_seq_len, ctx->pf_Q,
+                       ctx->kcache(l), ctx->vcache(l));
+    PrefillAttnArgs pa;
+    pa.Q = ctx->pf_Q;
+    pa.kcache = ctx->kcache(l);
+    pa.vcache = ctx->vcache(l);
+    pa.out = ctx->pf_A;
+    pa.n = n;
+    pa.start = start;
+    pa.msl = c.max_seq_len;
+    pa.n_heads = c.n_heads;
+    pa.n_kv_heads = c.n_kv_heads;
+    pa.n_qtiles = (n + 31) / 32;
+    bool ok = false;
+    switch (c.head_dim) {
+      case 32: ok = launch_prefill_attn_hd<32>(pa, G, s); break;
+      case 64: ok = launch_prefill_attn_hd<64>(pa, G, s); break;
+      case 128: ok = launch_prefill_attn_hd<128>(pa, G, s); break;
+      default: break;
+    }
+    if (!ok) return fail(ctx, YHIP_EINVAL, "prefill: unsupported attention shape");
+    memset(&g, 0, sizeof(g));
+    g.A = ctx->pf_A;
+    g.lda = qd;
+    g.B = L.wo;
+    g.ldb = qd;
+    g.C = ctx->pf_X;
+    g.ldc = c.dim;
+    g.M = n;
+    g.N = c.dim;
+    g.K = qd;
+    if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_X,
+                       (const float*)L.rms_ffn, c.norm_eps, c.dim, ctx->pf_Xn);
+    memset(&g, 0, sizeof(g));
+    g.A = ctx->pf_Xn;
+    g.lda = c.dim;
+    g.B = L.w1;
+    g.B3 = L.w3;
+    g.ldb = c.dim;
+    g.H = ctx->pf_H;
+    g.ldh = c.hidden_dim;
+    g.M = n;
+    g.N = c.hidden_dim;
+    g.K = c.dim;
+    g.act = c.act;
+    if ((rc = launch_gemm<kGemmSwiGLU>(ctx, g, s))) return rc;
+    memset(&g, 0, sizeof(g));
+    g.A = ctx->pf_H;
+    g.lda = c.hidden_dim;
+    g.B = L.w2;
+    g.ldb = c.hidden_dim;
+    g.C = ctx->pf_X;
+    g.ldc = c.dim;
+    g.M = n;
+    g.N = c.dim;
+    g.K = c.hidden_dim;
+    if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
+  }
+  HIP_TRY(ctx, hipGetLastError());
+  if (!logits_host) return YHIP_OK;
+  // last token: final rmsnorm + lm_head (reference src/infer.cpp:501-527)
+  const int Rc = (c.vocab_size % 2 == 0) ? 2 : 1;
+  MatvecArgs a = mv_base();
+  a.w0 = ctx->wcls;
+  a.row_step = (long)Rc * c.dim;
+  a.r_step = c.dim;
+  a.groups = c.vocab_size / Rc;
+  a.K = c.dim;
+  a.x = ctx->pf_X + (size_t)(n - 1) * c.dim;
+  a.gain = ctx->rms_final;
+  a.eps = c.norm_eps;
+  a.out = ctx->logits;
+  if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s)) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
+                              hipMemcpyDeviceToHost, s));
+  HIP_TRY(ctx, hipStreamSynchronize(s));
+  if (logits_host != ctx->logits_host) memcpy(logits_host, ctx->logits_host, (size_t)c.vocab_size * 4);
+  return YHIP_OK;
+}
+
 }  // namespace
 
 // ============================================================================================
@@ -663,6 +840,7 @@ extern "C" int yhip_destroy(yhip_ctx* ctx) {
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   drop_graphs(ctx);
+  if (ctx->pf_base) hipFree(ctx->pf_base);
   if (ctx->ev0) hipEventDestroy(ctx->ev0);
   if (ctx->ev1) hipEventDestroy(ctx->ev1);
   if (ctx->wbase) hipFree(ctx->wbase);
@@ -736,6 +914,28 @@ extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_
   collect_stats(ctx);
   if (int rc = check_flow_status(ctx)) return rc;
   *next_token = *ctx->argmax_host;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_prefill(yhip_ctx* ctx, const int* tokens, int n, int start_pos, float* logits_host) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (!tokens || n <= 0 || start_pos < 0) return fail(ctx, YHIP_EINVAL, "bad prefill arguments");
+  const yhip_config& c = ctx->c;
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= c.vocab_size) return fail(ctx, YHIP_EINVAL, "token id out of range");
+  if (!ctx->globals_loaded) return fail(ctx, YHIP_ESTATE, "globals not uploaded");
+  for (int l = 0; l < c.n_layers; ++l)
+    if (!ctx->layers[l].loaded) return fail(ctx, YHIP_ESTATE, "layer " + std::to_string(l) + " not uploaded");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  if ((long)start_pos + n <= c.max_seq_len && prefill_supported(c, ctx->q_dim()))
+    return run_prefill(ctx, tokens, n, start_pos, logits_host);
+  // token by token through the decode path (ring positions, or shapes without the batched kernels)
+  for (int i = 0; i < n; ++i) {
+    const bool last = i == n - 1 && logits_host;
+    if (int rc = yhip_forward(ctx, tokens[i], start_pos + i, last ? YHIP_MODE_LOGITS : YHIP_MODE_HYDRATE,
+                              last ? logits_host : nullptr))
+      return rc;
+  }
   return YHIP_OK;
 }
 
@@ -1058,6 +1258,49 @@ extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const
   HIP_TRY(nullptr, hipMemcpy(q_out, dq, qd * 4, hipMemcpyDeviceToHost));
   HIP_TRY(nullptr, hipMemcpy(kcache, dk, kv * 2, hipMemcpyDeviceToHost));
   HIP_TRY(nullptr, hipMemcpy(vcache, dv, kv * 2, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16_t* b3, int M, int N, int K, int mode,
+                              int act, float* c, uint16_t* h) {
+  if (!a || !b || M <= 0 || N <= 0 || K <= 0 || mode < 0 || mode > 2) return fail(nullptr, YHIP_EINVAL, "bad argument");
+  if (mode == kGemmSwiGLU ? (!b3 || !h) : !c) return fail(nullptr, YHIP_EINVAL, "bad argument");
+  DevBufs d;
+  const uint16_t* da = d.alloc<uint16_t>((size_t)M * K, a);
+  const uint16_t* db = d.alloc<uint16_t>((size_t)N * K, b);
+  const uint16_t* db3 = mode == kGemmSwiGLU ? d.alloc<uint16_t>((size_t)N * K, b3) : nullptr;
+  float* dc = mode != kGemmSwiGLU ? d.alloc<float>((size_t)M * N, mode == kGemmResid ? c : nullptr) : nullptr;
+  uint16_t* dh = mode == kGemmSwiGLU ? d.alloc<uint16_t>((size_t)M * N) : nullptr;
+  TRY_ALLOC(da);
+  TRY_ALLOC(db);
+  if (mode == kGemmSwiGLU) {
+    TRY_ALLOC(db3);
+    TRY_ALLOC(dh);
+  } else {
+    TRY_ALLOC(dc);
+  }
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.A = da;
+  g.lda = K;
+  g.B = db;
+  g.B3 = db3;
+  g.ldb = K;
+  g.C = dc;
+  g.ldc = N;
+  g.H = dh;
+  g.ldh = N;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.act = act;
+  int rc = mode == kGemmStore ? launch_gemm<kGemmStore>(nullptr, g, nullptr)
+           : mode == kGemmResid ? launch_gemm<kGemmResid>(nullptr, g, nullptr)
+                                : launch_gemm<kGemmSwiGLU>(nullptr, g, nullptr);
+  if (rc) return rc;
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  if (mode == kGemmSwiGLU) HIP_TRY(nullptr, hipMemcpy(h, dh, (size_t)M * N * 2, hipMemcpyDeviceToHost));
+  else HIP_TRY(nullptr, hipMemcpy(c, dc, (size_t)M * N * 4, hipMemcpyDeviceToHost));
   return YHIP_OK;
 }
 

@@ -23,9 +23,9 @@ MODE_LOGITS = 1
 # Every symbol include/yalm_hip.h declares.
 EXPORTS = (
     "yhip_create", "yhip_destroy", "yhip_upload_layer", "yhip_upload_globals", "yhip_forward",
-    "yhip_forward_argmax", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
+    "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
-    "yhip_test_qkv", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
+    "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
 )
 
 
@@ -60,6 +60,7 @@ def lib():
         "yhip_upload_globals": (ctypes.c_int, [vp, _u16p, _f32p, _u16p]),
         "yhip_forward": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
         "yhip_forward_argmax": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int, _ip]),
+        "yhip_prefill": (ctypes.c_int, [vp, _ip, ctypes.c_int, ctypes.c_int, _f32p]),
         "yhip_logits_host": (_f32p, [vp]),
         "yhip_kv_read": (ctypes.c_int, [vp, ctypes.c_int, _u16p, _u16p]),
         "yhip_kv_write": (ctypes.c_int, [vp, ctypes.c_int, _u16p, _u16p]),
@@ -76,6 +77,7 @@ def lib():
                                                ctypes.c_int, _f32p]),
         "yhip_test_qkv": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p] + [ctypes.c_int] * 6
                           + [ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p, _u16p, _u16p]),
+        "yhip_test_gemm": (ctypes.c_int, [_u16p, _u16p, _u16p] + [ctypes.c_int] * 5 + [_f32p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
         "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
@@ -169,6 +171,14 @@ class HipModel:
         nxt = ctypes.c_int()
         _check(lib().yhip_forward_argmax(self.h, token, pos, ctypes.byref(nxt)), self.h)
         return nxt.value
+
+    def prefill(self, tokens, start_pos=0, logits=True):
+        """Batched prompt prefill; returns the last token's logits (or None with logits=False)."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(self.cfg.vocab_size, np.float32) if logits else None
+        _check(lib().yhip_prefill(self.h, toks.ctypes.data_as(_ip), len(toks), start_pos,
+                                  out.ctypes.data_as(_f32p) if logits else None), self.h)
+        return out
 
     def kv(self, layer):
         c = self.cfg
@@ -280,6 +290,22 @@ def qkv(x, gain, wq, wk, wv, n_heads, n_kv_heads, head_dim, max_seq_len, pos, kc
                                qkv_clip, pos, q.ctypes.data_as(_f32p), k.ctypes.data_as(_u16p),
                                v.ctypes.data_as(_u16p)))
     return q, k, v
+
+
+def gemm(a, b, mode=0, b3=None, c=None, act=1):
+    """Prefill GEMM hook: mode 0 a @ b.T, mode 1 c + a @ b.T, mode 2 fp16(act(a @ b.T) * (a @ b3.T))."""
+    A, ap = _u16(a)
+    B, bp = _u16(b)
+    M, K = A.shape
+    N = B.shape[0]
+    if mode == 2:
+        B3, b3p = _u16(b3)
+        h = np.zeros((M, N), np.uint16)
+        _check(lib().yhip_test_gemm(ap, bp, b3p, M, N, K, mode, act, None, h.ctypes.data_as(_u16p)))
+        return h
+    out = np.zeros((M, N), np.float32) if c is None else np.ascontiguousarray(c, np.float32).copy()
+    _check(lib().yhip_test_gemm(ap, bp, None, M, N, K, mode, act, out.ctypes.data_as(_f32p), None))
+    return out
 
 
 def argmax(logits):
