@@ -225,43 +225,50 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
 // ------------------------------------------------------------------------------------------
 // Causal GQA prefill attention on MFMA (reference src/infer.cpp:218-250 per query position:
 // scores over keys 0..pos read back from the fp16 cache, softmax with max subtraction, weighted
-// sum of V). Workgroup = one kv head g and 32 consecutive queries; wave w serves query head
-// g*G + w, so the four waves share the head's K/V.
-// Per 32-key tile a wave computes S^T = K Q^T (keys as rows), so each lane holds 16 scores of one
-// query (its partner lane l^32 the other 16) and runs the online softmax for that query with one
+// sum of V). A workgroup serves kv head g and QT consecutive 32-query tiles: wave (qs, gh) handles
+// query tile qs for query head g*G + gh. Each 32-key tile of K and V is staged once into LDS
+// (double-buffered: the next tile is loaded while the current one is used) and read by all the
+// workgroup's waves, so K/V reaches the CU once per workgroup instead of once per wave.
+// Per key tile a wave computes S^T = K Q^T (keys as rows), so each lane holds 16 scores of one query
+// (its partner lane l^32 the other 16) and runs the online softmax for that query with one
 // cross-half exchange; then O^T += V^T P^T, whose B operand is exactly the lane's own
-// probabilities (the MFMA k order is chosen to match the score layout), so nothing goes through
-// LDS. O^T keeps the query in the column, so the softmax rescale and the final 1/sum are
-// lane-local. Queries are at positions start + t; keys are the cache entries 0 .. position.
-// Requires HD % 32 == 0 and max_seq_len % 32 == 0.
+// probabilities (the MFMA k order is chosen to match the score layout). O^T keeps the query in the
+// column, so the softmax rescale and the final 1/sum are lane-local. Queries are at positions
+// start + t; keys are the cache entries 0 .. position.
+// Requires HD % 32 == 0, max_seq_len % 32 == 0 and 64 * G * QT threads <= 1024.
 // ------------------------------------------------------------------------------------------
 struct PrefillAttnArgs {
   const uint16_t* Q;   // [n][n_heads * HD] fp16
   const uint16_t* kcache;
   const uint16_t* vcache;
   uint16_t* out;       // [n][n_heads * HD] fp16
-  int n, start, msl, n_heads, n_kv_heads, n_qtiles;
+  int n, start, msl, n_heads, n_kv_heads, n_blocks;  // n_blocks: workgroups per kv head
 };
 
-template <int HD, int G>
-__global__ void __launch_bounds__(64 * G) prefill_attn_kernel(PrefillAttnArgs a) {
+template <int HD, int G, int QT>
+__global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnArgs a) {
   static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
-  constexpr int KS = HD / 16;  // k steps of the score MFMA
-  constexpr int DT = HD / 32;  // 32-dim tiles of the output
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int qt = a.n_qtiles - 1 - blockIdx.x;  // longest (latest) query tiles first
+  constexpr int NT = 64 * G * QT;
+  constexpr int KS = HD / 16;   // k steps of the score MFMA
+  constexpr int DT = HD / 32;   // 32-dim tiles of the output
+  constexpr int KLD = HD + 8;   // LDS row of a key (halves), padded
+  constexpr int VLD = 32 + 8;   // LDS row of a V dim (halves), padded
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][32 * KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][HD * VLD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gh = wave % G, qs = wave / G;
+  const int qb = a.n_blocks - 1 - blockIdx.x;  // latest (longest) query tiles first
   const int g = blockIdx.y;
-  const int h = g * G + wave;
-  const int q0 = qt * 32;
+  const int h = g * G + gh;
+  const int q0 = (qb * QT + qs) * 32;
   const int qd = a.n_heads * HD;
-  const int my_q = q0 + (lane & 31);                 // this lane's query row
-  const int q_pos = a.start + my_q;                  // its position
-  const int last_pos = a.start + min(q0 + 31, a.n - 1);
+  const int my_q = q0 + (lane & 31);
+  const int q_pos = a.start + my_q;
+  const int block_last = a.start + min((qb + 1) * QT * 32 - 1, a.n - 1);  // last query position of the workgroup
   const uint16_t* kh = a.kcache + (long)g * HD * a.msl;
   const uint16_t* vh = a.vcache + (long)g * HD * a.msl;
   const int half = lane >> 5;
 
-  // Q^T fragments: column = query my_q, k = dims 16 ks + 8 half + e
   u32x4 qf[KS];
   {
     const uint16_t* qrow = a.Q + (long)min(my_q, a.n - 1) * qd + h * HD + 8 * half;
@@ -274,17 +281,55 @@ __global__ void __launch_bounds__(64 * G) prefill_attn_kernel(PrefillAttnArgs a)
   float m_run = kNegBig, l_run = 0.f;
   const float scale = 1.0f / sqrtf((float)HD);
 
-  const int nkt = last_pos / 32 + 1;
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * 32;
-    // S^T: rows = keys k0 + (lane & 31) for the K operand; K[g][c][t][16], chunk c = ks
-    f32x16 s = f32x16{};
-    const uint16_t* krow = kh + (long)(k0 + (lane & 31)) * 16 + 8 * half;
+  // staging of a key tile: K (32 keys x HD dims, 16-byte pieces) and V (HD dims x 32 keys)
+  constexpr int KPIECES = 32 * HD / 8, VPIECES = HD * 32 / 8;
+  constexpr int KPT = (KPIECES + NT - 1) / NT, VPT = (VPIECES + NT - 1) / NT;
+  u32x4 kst[KPT], vst[VPT];
+  auto gload = [&](int k0) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + (long)ks * 16 * a.msl);
-      s = mfma32(kf, qf[ks], s);
+    for (int i = 0; i < KPT; ++i) {
+      const int pc = min(tid + NT * i, KPIECES - 1);  // piece: chunk c, key, 8-dim half of the chunk
+      const int c = pc / 64, key = (pc % 64) >> 1, hh = pc & 1;
+      kst[i] = *reinterpret_cast<const u32x4*>(kh + (long)c * 16 * a.msl + (long)(k0 + key) * 16 + 8 * hh);
     }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int pc = min(tid + NT * i, VPIECES - 1);  // piece: dim, 8 consecutive keys
+      const int d = pc >> 2, part = pc & 3;
+      vst[i] = *reinterpret_cast<const u32x4*>(vh + (long)d * a.msl + k0 + 8 * part);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int pc = tid + NT * i;
+      if (pc < KPIECES) {
+        const int c = pc / 64, key = (pc % 64) >> 1, hh = pc & 1;
+        *reinterpret_cast<u32x4*>(&Ks[buf][key * KLD + c * 16 + 8 * hh]) = kst[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int pc = tid + NT * i;
+      if (pc < VPIECES) {
+        const int d = pc >> 2, part = pc & 3;
+        *reinterpret_cast<u32x4*>(&Vs[buf][d * VLD + 8 * part]) = vst[i];
+      }
+    }
+  };
+
+  const int nkt = block_last / 32 + 1;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1, k0 = kt * 32;
+    if (kt + 1 < nkt) gload(k0 + 32);
+    // S^T = K Q^T
+    f32x16 s = f32x16{};
+    const uint16_t* krow = &Ks[buf][(lane & 31) * KLD + 8 * half];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(*reinterpret_cast<const u32x4*>(krow + 16 * ks), qf[ks], s);
     // mask (key position > query position), scale, tile max of this query
     float mt = kNegBig;
 #pragma unroll
@@ -313,20 +358,21 @@ __global__ void __launch_bounds__(64 * G) prefill_attn_kernel(PrefillAttnArgs a)
     ps += __shfl_xor(ps, 32, 64);
     l_run = l_run * corr + ps;
     m_run = m_new;
-    // O^T += V^T P^T; k order of step kk: keys k0 + 16 kk + {0..3, 8..11} + 4 half
+    // O^T += V^T P^T; k order of step kk: keys 16 kk + {0..3, 8..11} + 4 half of the tile
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-      const uint16_t* vrow = vh + (long)(t * 32 + (lane & 31)) * a.msl + k0 + 4 * half;
+      const uint16_t* vrow = &Vs[buf][(t * 32 + (lane & 31)) * VLD + 4 * half];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * kk);
         const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * kk + 8);
-        const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
-        o[t] = mfma32(vf, pf[kk], o[t]);
+        o[t] = mfma32(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[kk], o[t]);
       }
     }
+    if (kt + 1 < nkt) lstore(buf ^ 1);
+    __syncthreads();
   }
   if (my_q < a.n) {
     const float inv = 1.0f / l_run;

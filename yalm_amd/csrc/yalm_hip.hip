@@ -553,14 +553,18 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   return YHIP_OK;
 }
 
+// Workgroups of 64 * G * QT threads: G query heads x QT query tiles of 32 sharing each K/V tile.
 template <int HD>
-bool launch_prefill_attn_hd(const PrefillAttnArgs& p, int G, hipStream_t s) {
-  const dim3 grid(p.n_qtiles, p.n_kv_heads);
+bool launch_prefill_attn_hd(PrefillAttnArgs p, int G, int n_qtiles, hipStream_t s) {
+  auto go = [&](auto kernel, int qt, int threads) {
+    p.n_blocks = (n_qtiles + qt - 1) / qt;
+    hipLaunchKernelGGL(kernel, dim3(p.n_blocks, p.n_kv_heads), dim3(threads), 0, s, p);
+  };
   switch (G) {
-    case 1: hipLaunchKernelGGL((prefill_attn_kernel<HD, 1>), grid, dim3(64), 0, s, p); return true;
-    case 2: hipLaunchKernelGGL((prefill_attn_kernel<HD, 2>), grid, dim3(128), 0, s, p); return true;
-    case 4: hipLaunchKernelGGL((prefill_attn_kernel<HD, 4>), grid, dim3(256), 0, s, p); return true;
-    case 8: hipLaunchKernelGGL((prefill_attn_kernel<HD, 8>), grid, dim3(512), 0, s, p); return true;
+    case 1: go(prefill_attn_kernel<HD, 1, 4>, 4, 256); return true;
+    case 2: go(prefill_attn_kernel<HD, 2, 4>, 4, 512); return true;
+    case 4: go(prefill_attn_kernel<HD, 4, 2>, 2, 512); return true;
+    case 8: go(prefill_attn_kernel<HD, 8, 1>, 1, 512); return true;
     default: return false;
   }
 }
@@ -638,12 +642,12 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     pa.msl = c.max_seq_len;
     pa.n_heads = c.n_heads;
     pa.n_kv_heads = c.n_kv_heads;
-    pa.n_qtiles = (n + 31) / 32;
+    const int nqt = (n + 31) / 32;
     bool ok = false;
     switch (c.head_dim) {
-      case 32: ok = launch_prefill_attn_hd<32>(pa, G, s); break;
-      case 64: ok = launch_prefill_attn_hd<64>(pa, G, s); break;
-      case 128: ok = launch_prefill_attn_hd<128>(pa, G, s); break;
+      case 32: ok = launch_prefill_attn_hd<32>(pa, G, nqt, s); break;
+      case 64: ok = launch_prefill_attn_hd<64>(pa, G, nqt, s); break;
+      case 128: ok = launch_prefill_attn_hd<128>(pa, G, nqt, s); break;
       default: break;
     }
     if (!ok) return fail(ctx, YHIP_EINVAL, "prefill: unsupported attention shape");
