@@ -52,15 +52,21 @@ yhip_ctx* yalm_session_hip_ctx(yalm_session* s);
  * in YHIP_MODE_LOGITS. */
 int yalm_session_forward(yalm_session* s, int token, int pos, int mode, float* logits);
 
+/* Model::prefill(state, tokens, n, start_pos): the tokens in one batched pass; the last token's
+ * logits (vocab floats) are copied to `logits` when non-NULL. No reference counterpart: the
+ * reference hydrates a prompt one token at a time (src/main.cpp:169-177). */
+int yalm_session_prefill(yalm_session* s, const int* tokens, int n, int start_pos, float* logits);
+
 /* The reference completion loop (src/main.cpp:144-192) on token ids: warm-up forward(0, 0), prompt
- * hydrate (all but the last token in HYDRATE mode), then n_steps x [sample -> forward]. Greedy when
- * temperature == 0 (sampled on the device when `device_argmax` != 0, else from host logits).
- * Stops early at eos when stop_at_eos != 0. Writes the generated ids to out_tokens[n_steps] and, per
- * step, the wall time of sample+forward in seconds to step_seconds[n_steps] (either may be NULL);
- * *hydrate_seconds gets the prompt time. Returns the number of generated tokens (>= 0) or -1. */
+ * hydrate (all but the last token in HYDRATE mode; one batched Model::prefill instead when
+ * `batched_prefill` != 0), then n_steps x [sample -> forward]. Greedy when temperature == 0 (sampled
+ * on the device when `device_argmax` != 0, else from host logits). Stops early at eos when
+ * stop_at_eos != 0. Writes the generated ids to out_tokens[n_steps] and, per step, the wall time of
+ * sample+forward in seconds to step_seconds[n_steps] (either may be NULL); *hydrate_seconds gets the
+ * prompt time. Returns the number of generated tokens (>= 0) or -1. */
 int yalm_session_generate(yalm_session* s, const int* prompt, int n_prompt, int n_steps, float temperature,
-                          int device_argmax, int stop_at_eos, int* out_tokens, double* step_seconds,
-                          double* hydrate_seconds);
+                          int device_argmax, int batched_prefill, int stop_at_eos, int* out_tokens,
+                          double* step_seconds, double* hydrate_seconds);
 
 /* Config::active_bytes(pos) of the reference (src/model.cpp:73-98). */
 size_t yalm_session_active_bytes(const yalm_session* s, size_t pos);

@@ -15,7 +15,8 @@ LIB_PATH = os.path.join(_HERE, "libyalm_host.so")
 EXPORTS = (
     "yalm_session_open", "yalm_session_synthetic", "yalm_session_write", "yalm_session_hip", "yalm_session_close",
     "yalm_session_error", "yalm_session_config", "yalm_session_tensor", "yalm_session_hip_ctx",
-    "yalm_session_forward", "yalm_session_generate", "yalm_session_active_bytes", "yalm_uniform_ids",
+    "yalm_session_forward", "yalm_session_prefill", "yalm_session_generate", "yalm_session_active_bytes",
+    "yalm_uniform_ids",
     "yalm_fill_normal_f16", "yalm_f32_to_f16", "yalm_f16_to_f32",
 )
 
@@ -61,8 +62,9 @@ def lib():
                                                ctypes.POINTER(ctypes.c_size_t), _ip, _ip]),
         "yalm_session_hip_ctx": (vp, [vp]),
         "yalm_session_forward": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
+        "yalm_session_prefill": (ctypes.c_int, [vp, _ip, ctypes.c_int, ctypes.c_int, _f32p]),
         "yalm_session_generate": (ctypes.c_int, [vp, _ip, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int,
-                                                 ctypes.c_int, _ip, _dp, _dp]),
+                                                 ctypes.c_int, ctypes.c_int, _ip, _dp, _dp]),
         "yalm_session_active_bytes": (ctypes.c_size_t, [vp, ctypes.c_size_t]),
         "yalm_uniform_ids": (None, [_ip, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int]),
         "yalm_fill_normal_f16": (None, [_u16p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_float]),
@@ -190,14 +192,23 @@ class Session:
                                                out.ctypes.data_as(_f32p) if out is not None else None))
         return out
 
-    def generate(self, prompt, n_steps, temperature=0.0, device_argmax=True, stop_at_eos=False):
-        """Returns (tokens, step_seconds, hydrate_seconds) of the reference completion loop."""
+    def prefill(self, tokens, start_pos=0):
+        """Model::prefill: the tokens in one batched pass; returns the last token's logits."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros(self.config()["vocab_size"], np.float32)
+        self._check(lib().yalm_session_prefill(self.h, tokens.ctypes.data_as(_ip), tokens.size, start_pos,
+                                               out.ctypes.data_as(_f32p)))
+        return out
+
+    def generate(self, prompt, n_steps, temperature=0.0, device_argmax=True, stop_at_eos=False, prefill=False):
+        """Returns (tokens, step_seconds, hydrate_seconds) of the reference completion loop; with
+        prefill=True the prompt goes through one batched Model::prefill instead of token steps."""
         prompt = np.ascontiguousarray(prompt, np.int32)
         toks = np.zeros(max(n_steps, 1), np.int32)
         secs = np.zeros(max(n_steps, 1), np.float64)
         hyd = ctypes.c_double()
         n = self._check(lib().yalm_session_generate(self.h, prompt.ctypes.data_as(_ip), prompt.size, n_steps,
-                                                    temperature, int(device_argmax), int(stop_at_eos),
+                                                    temperature, int(device_argmax), int(prefill), int(stop_at_eos),
                                                     toks.ctypes.data_as(_ip), secs.ctypes.data_as(_dp),
                                                     ctypes.byref(hyd)))
         return toks[:n], secs[:n], hyd.value

@@ -134,9 +134,20 @@ extern "C" int yalm_session_forward(yalm_session* s, int token, int pos, int mod
   return 0;
 }
 
+extern "C" int yalm_session_prefill(yalm_session* s, const int* tokens, int n, int start_pos, float* logits) {
+  if (!s || !tokens || n <= 0) return set_err(s, "bad argument");
+  try {
+    s->model->prefill(*s->state, tokens, n, start_pos);
+  } catch (const std::exception& e) {
+    return set_err(s, e.what());
+  }
+  if (logits) memcpy(logits, s->state->logits(), sizeof(float) * (size_t)s->model->config->vocab_size);
+  return 0;
+}
+
 extern "C" int yalm_session_generate(yalm_session* s, const int* prompt, int n_prompt, int n_steps, float temperature,
-                                     int device_argmax, int stop_at_eos, int* out_tokens, double* step_seconds,
-                                     double* hydrate_seconds) {
+                                     int device_argmax, int batched_prefill, int stop_at_eos, int* out_tokens,
+                                     double* step_seconds, double* hydrate_seconds) {
   if (!s || !prompt || n_prompt <= 0 || n_steps < 0) return set_err(s, "bad argument");
   using clk = std::chrono::steady_clock;
   Model& m = *s->model;
@@ -147,12 +158,18 @@ extern "C" int yalm_session_generate(yalm_session* s, const int* prompt, int n_p
     auto t0 = clk::now();
     int pos = 0;
     int next = -1;
-    for (int i = 0; i < n_prompt; ++i, ++pos) {
-      const bool last = i + 1 == n_prompt;
-      if (last && greedy_dev)
-        next = m.forward_argmax(st, prompt[i], pos);
-      else
-        m.forward(st, prompt[i], pos, last ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
+    if (batched_prefill) {
+      m.prefill(st, prompt, n_prompt, 0);
+      pos = n_prompt;
+      if (greedy_dev) next = s->sampler->sample_argmax(st);
+    } else {
+      for (int i = 0; i < n_prompt; ++i, ++pos) {
+        const bool last = i + 1 == n_prompt;
+        if (last && greedy_dev)
+          next = m.forward_argmax(st, prompt[i], pos);
+        else
+          m.forward(st, prompt[i], pos, last ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
+      }
     }
     if (hydrate_seconds) *hydrate_seconds = std::chrono::duration<double>(clk::now() - t0).count();
     int produced = 0;

@@ -1,7 +1,7 @@
 // yalm: command-line driver with the reference's contract (src/main.cpp:20-544) on the HIP device.
 //
 //   yalm <checkpoint.yalm> [-d hip] [-m completion|perplexity|passkey] [-i prompt | -f file | -p ids]
-//        [-n steps] [-t temperature] [-T context] [-l passkey_pos]
+//        [-n steps] [-t temperature] [-T context] [-l passkey_pos] [-b 0|1]
 //   yalm --synth <out.yalm> <tiny|mistral-7b> [seed]     write a seeded random-init model
 //
 // `-p 5,17,900` feeds token ids directly (no tokenizer, no BOS), for synthetic checkpoints.
@@ -36,7 +36,8 @@ static void usage() {
           "  -p <ids>    comma-separated prompt token ids (no BOS added)\n"
           "  -n <int>    steps (completion, default 256; 0 = max_seq_len; -1 = until EOS) or junk lines (passkey)\n"
           "  -t <float>  temperature (default 1.0; 0 = greedy)\n"
-          "  -l <int>    passkey position (-1 = random)\n");
+          "  -l <int>    passkey position (-1 = random)\n"
+          "  -b <0|1>    1: ingest the prompt in one batched prefill instead of token by token (default 0)\n");
   exit(1);
 }
 
@@ -105,7 +106,21 @@ static std::vector<int> parse_ids(const std::string& s) {
   return out;
 }
 
-static void run_completion(Session& s, const std::string& prompt, const std::string& ids, int num_steps, float temp) {
+// Prompt ingestion: one token at a time in HYDRATE mode as the reference does (src/main.cpp:169-177),
+// the last one with logits; or one batched Model::prefill when `batched`.
+static void ingest(Session& s, const std::vector<int>& enc, bool batched) {
+  Model& m = *s.model;
+  if (batched) {
+    m.prefill(*s.state, enc.data(), (int)enc.size(), 0);
+    return;
+  }
+  for (size_t pos = 0; pos < enc.size(); ++pos)
+    m.forward(*s.state, enc[pos], (int)pos,
+              pos + 1 == enc.size() ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
+}
+
+static void run_completion(Session& s, const std::string& prompt, const std::string& ids, int num_steps, float temp,
+                           bool batched) {
   Model& m = *s.model;
   if (num_steps == 0) num_steps = m.config->max_seq_len;
   m.forward(*s.state, 0, 0);  // warm-up: loads weights, captures the step graph
@@ -123,11 +138,8 @@ static void run_completion(Session& s, const std::string& prompt, const std::str
     if (t < 0 || t >= m.config->vocab_size) throw Error("prompt token id out of range");
   const double start = now_s();
   size_t read_bytes = 0;
-  for (size_t pos = 0; pos < enc.size(); ++pos) {
-    m.forward(*s.state, enc[pos], (int)pos,
-              pos + 1 == enc.size() ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
-    read_bytes += m.config->active_bytes(pos);
-  }
+  ingest(s, enc, batched);
+  for (size_t pos = 0; pos < enc.size(); ++pos) read_bytes += m.config->active_bytes(pos);
   const double end_hydrate = now_s();
   for (int i = 0; i < num_steps || num_steps == -1; ++i) {
     const int tok = s.sampler->sample(*s.state, temp);
@@ -175,7 +187,7 @@ static void run_perplexity(Session& s, const std::string& prompt, const std::str
          N, ppl, err, N / elapsed, elapsed / N, (double)read_bytes / 1e9 / elapsed, elapsed);
 }
 
-static void run_passkey(Session& s, int n_junk, int passkey_pos) {
+static void run_passkey(Session& s, int n_junk, int passkey_pos, bool batched) {
   Model& m = *s.model;
   m.forward(*s.state, 0, 0);
   const std::string prefix =
@@ -196,9 +208,14 @@ static void run_passkey(Session& s, int n_junk, int passkey_pos) {
   printf("Passkey test:\n  prompt: %zu tokens\n  passkey: %d\n  passkey token index: ~%d\n\n", enc.size(), passkey,
          (int)((float)at / n_junk * enc.size()));
   const size_t N = enc.size();
-  for (size_t pos = 0; pos < N; ++pos) {
-    std::cout << "\r Running passkey test..." << pos + 1 << "/" << N << std::flush;
-    m.forward(*s.state, enc[pos], (int)pos, pos + 1 == N ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
+  if (batched) {
+    ingest(s, enc, true);
+  } else {
+    for (size_t pos = 0; pos < N; ++pos) {
+      std::cout << "\r Running passkey test..." << pos + 1 << "/" << N << std::flush;
+      m.forward(*s.state, enc[pos], (int)pos,
+                pos + 1 == N ? InferenceMode::OUTPUT_LOGITS : InferenceMode::HYDRATE_KV_CACHE);
+    }
   }
   std::cout << std::endl << suffix << std::flush;
   for (size_t pos = N; pos < N + 16; ++pos) {
@@ -215,7 +232,7 @@ int main(int argc, char** argv) {
   if (argc >= 2 && std::string(argv[1]) == "--synth") return synth_main(argc, argv);
   if (argc < 2) usage();
   std::string path = argv[1], device = "hip", mode = "completion", prompt, prompt_path, ids;
-  int context = 0, num_steps = 256, n_junk = 250, passkey_pos = -1;
+  int context = 0, num_steps = 256, n_junk = 250, passkey_pos = -1, batched = 0;
   float temperature = 1.0f;
   for (int i = 2; i < argc; i += 2) {
     if (i + 1 >= argc || argv[i][0] != '-' || strlen(argv[i]) != 2) usage();
@@ -241,6 +258,7 @@ int main(int argc, char** argv) {
       case 't': temperature = std::stof(v); break;
       case 'T': context = std::stoi(v); break;
       case 'l': passkey_pos = std::stoi(v); break;
+      case 'b': batched = std::stoi(v); break;
       case 'n':
         num_steps = std::stoi(v);
         n_junk = num_steps;
@@ -269,11 +287,11 @@ int main(int argc, char** argv) {
     Session s;
     open_session(s, path, context, device);
     if (mode == "completion")
-      run_completion(s, prompt, ids, num_steps, temperature);
+      run_completion(s, prompt, ids, num_steps, temperature, batched != 0);
     else if (mode == "perplexity")
       run_perplexity(s, prompt, ids);
     else
-      run_passkey(s, n_junk, passkey_pos);
+      run_passkey(s, n_junk, passkey_pos, batched != 0);
   } catch (const std::exception& e) {
     fprintf(stderr, "error: %s\n", e.what());
     return 1;

@@ -204,6 +204,13 @@ int Model::forward_argmax(InferenceState& s, int token, int pos) {
   return next;
 }
 
+void Model::prefill(InferenceState& s, const int* tokens, int n, int start_pos) {
+  if (s.device() != _device || _device != Device::HIP) throw Error("prefill needs a HIP model and state");
+  s._logits = yhip_logits_host(_ctx);
+  s._mode = InferenceMode::OUTPUT_LOGITS;
+  check(yhip_prefill(_ctx, tokens, n, start_pos, s._logits), "yhip_prefill");
+}
+
 // ---- Sampler (reference src/sampler.cpp) -------------------------------------------------------
 Sampler::Sampler(std::shared_ptr<Config> config, uint64_t seed) : vocab_size(config->vocab_size) {
   std::srand((unsigned)seed);

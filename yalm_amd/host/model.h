@@ -101,6 +101,11 @@ struct Model {
   void forward(InferenceState& s, int token, int pos, InferenceMode mode = InferenceMode::OUTPUT_LOGITS);
   // Greedy step on the device: returns argmax of the next-token logits (reference tie rule).
   int forward_argmax(InferenceState& s, int token, int pos);
+  // Ingests tokens[0..n) at positions start_pos.. in one batched pass (MFMA GEMMs and causal
+  // attention) and leaves the last token's logits in s.logits(). The reference has no batched form:
+  // it feeds a prompt one token at a time in HYDRATE mode (src/main.cpp:169-177), which this equals
+  // within fp16-activation tolerance; positions past the context fall back to that loop.
+  void prefill(InferenceState& s, const int* tokens, int n, int start_pos = 0);
   Device device() const { return _device; }
   yhip_ctx* hip_context() const { return _ctx; }
 
