@@ -95,12 +95,17 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * 0 = per-op kernels, the default), "flow_bpc" / "flow_bpc_w2" (workgroups per CU of the single
  * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
- * kv head, default 512/n_kv_heads clamped to [1,64]),
- * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64, default 64; at least 128 from
- * 1024 cached tokens on), "stats" (1 = time
- * every synchronised step on the device with HIP events and reset the totals; 0 = off).
+ * kv head, default compute units / n_kv_heads clamped to [1,64]),
+ * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default, 256
+ * for the MFMA attention and 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode attention on the matrix cores where head_dim %
+ * 32 == 0 and max_seq_len % 32 == 0, default; 0 = the SIMT kernel), "prefetch_o" /
+ * "prefetch_w13_mb" / "prefetch_blocks" (extra workgroups of the attention launch read the layer's
+ * O weights / the first MB of W1 and W3 into the caches; worker count, a multiple of 8; off by
+ * default), "stats" (1 = time every synchronised step on the device with HIP events and reset the
+ * totals; 0 = off).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
- * yhip_test_* hooks; 0 = the decode path's default). */
+ * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
+ * yhip_test_* / yhip_bench_* hooks, as above). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 
 /* Device time of the steps timed since "stats" was set: total microseconds between HIP events

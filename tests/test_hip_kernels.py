@@ -112,11 +112,25 @@ ATTN_CASES = [
     (128, 32, 8, 4096, 65, 0),    # a second slice holding one token
     (32, 8, 2, 520, 300, 5),
     (16, 8, 1, 333, 333, 0),
+    (128, 8, 8, 256, 200, 0),     # one query head per kv head
+    (128, 16, 8, 512, 300, 0),    # two
+    (64, 16, 2, 208, 150, 4),     # eight, head_dim 64
+    (32, 4, 1, 1024, 1000, 64),   # many slices
+    (128, 32, 8, 4096, 256, 0),
+    (128, 32, 8, 4096, 257, 0),
 ]
 
 
+@pytest.fixture(params=[1, 0], ids=["mfma", "simt"])
+def attn_impl(request):
+    """Runs a test with the MFMA decode attention (where the shape allows it) and with the SIMT kernel."""
+    hip().set_attn_mfma(request.param)
+    yield request.param
+    hip().set_attn_mfma(1)
+
+
 @pytest.mark.parametrize("hd,nh,nkv,msl,kv_len,nsplit", ATTN_CASES)
-def test_attention_parity(hd, nh, nkv, msl, kv_len, nsplit):
+def test_attention_parity(hd, nh, nkv, msl, kv_len, nsplit, attn_impl):
     rng = np.random.default_rng(hd * nh + kv_len)
     kb = f16(rng.standard_normal(nkv * hd * msl))
     vb = f16(rng.standard_normal(nkv * hd * msl))
@@ -127,7 +141,7 @@ def test_attention_parity(hd, nh, nkv, msl, kv_len, nsplit):
     assert np.array_equal(k_after, kb)  # no sink rotation below max_seq_len
 
 
-def test_attention_kv_len_one_returns_v0_exactly():
+def test_attention_kv_len_one_returns_v0_exactly(attn_impl):
     rng = np.random.default_rng(5)
     hd, nh, nkv, msl = 128, 32, 8, 256
     kb = f16(rng.standard_normal(nkv * hd * msl))
@@ -139,7 +153,7 @@ def test_attention_kv_len_one_returns_v0_exactly():
     assert np.array_equal(got, want)
 
 
-def test_attention_known_answer_one_hot_softmax():
+def test_attention_known_answer_one_hot_softmax(attn_impl):
     # The reference's known-answer construction (src/test.cpp:67-125) at head_dim 16: huge query
     # entries make each head's softmax one-hot on a chosen position.
     hd, msl, nh, nkv = 16, 4, 2, 1

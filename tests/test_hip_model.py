@@ -25,7 +25,7 @@ def hip():
 # The three ways a step can run: one launch per token (a dataflow of workgroups), the captured
 # hipGraph of per-op kernels (the default), and the same kernels launched directly.
 PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
-         "direct": dict(single_launch=0, graph=0)}
+         "direct": dict(single_launch=0, graph=0), "graph_simt": dict(single_launch=0, graph=1, attn_mfma=0)}
 
 
 def use_path(m, path):
@@ -157,11 +157,13 @@ def test_forward_argmax_matches_host_argmax(path):
             tok = nxt
 
 
-@pytest.mark.parametrize("path", ["single", "graph"])
-def test_sink_mode_beyond_context_matches_oracle(path):
+@pytest.mark.parametrize("path", ["single", "graph", "graph_simt"])
+@pytest.mark.parametrize("shape", ["micro", "hd32"])
+def test_sink_mode_beyond_context_matches_oracle(path, shape):
     # pos >= max_seq_len: StreamingLLM ring with 2 sink tokens re-rotated each step
-    # (reference src/infer.cpp:307-325, 489-494).
-    cfg = dict(MICRO, max_seq_len=16)
+    # (reference src/infer.cpp:307-325, 489-494). hd32 runs the MFMA attention (head_dim 32).
+    cfg = dict(MICRO, max_seq_len=16) if shape == "micro" else dict(
+        MICRO, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, max_seq_len=32)
     t = np_tensors(cfg, seed=26, std=0.1)
     om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(27)

@@ -581,6 +581,25 @@ __global__ void rope_table_kernel(const float* inv_freq, float* rope_cs, int hal
 // In sink mode (pos >= msl) slice 0 first re-rotates the two sink keys by one position
 // (reference src/infer.cpp:307-325).
 // ------------------------------------------------------------------------------------------
+// Weight prefetch riding on the attention launch. Attention waits on latency and leaves HBM idle,
+// so extra workgroups read the weights the next kernels will stream (O, then the first rows of
+// W1/W3) and leave them in the caches. Range r is split into chunks of `chunk` 16-byte units; worker
+// j reads chunks j, j + blocks, ... so that with `blocks` and the attention grid multiples of 8 a
+// chunk lands on the same XCD (and L2) as the consumer workgroup with the chunk's index.
+// The loaded words are folded into one value per thread that is stored to `sink` only if it equals
+// `magic` (keeps the loads alive; in practice never written).
+struct PrefetchRange {
+  const u32x4* p = nullptr;
+  long units = 0;  // 16-byte units
+  int chunk = 1;   // 16-byte units per chunk
+};
+struct AttnPrefetch {
+  PrefetchRange r[3];
+  int blocks = 0;  // worker workgroups (0: no prefetch)
+  unsigned magic = 0;
+  unsigned* sink = nullptr;  // one word per thread of the launch's workgroups
+};
+
 struct AttnArgs {
   const float* q;        // [nh][hd]
   uint16_t* kcache;      // layer base
@@ -592,15 +611,17 @@ struct AttnArgs {
   int min_slice;          // smallest KV slice per workgroup (multiple of 64)
   const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
+  AttnPrefetch pf;
 };
 
 constexpr int kMaxGroup = 8;
 
-// Tokens per KV slice. From 1024 cached tokens on, slices are at least 128 tokens (fewer, longer
-// slices: the merge and the per-workgroup start cost outweigh the extra parallelism there).
-__host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice) {
+// Tokens per KV slice, a multiple of `gran` (the kernel's tile). From 1024 cached tokens on,
+// slices are at least 128 tokens (fewer, longer slices: the merge and the per-workgroup start cost
+// outweigh the extra parallelism there).
+__host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int min_slice, int gran = 64) {
   int chunk = (kv_len + nsplit - 1) / nsplit;
-  chunk = (chunk + 63) & ~63;
+  chunk = (chunk + gran - 1) / gran * gran;
   const int floor = (kv_len >= 1024 && min_slice < 128) ? 128 : min_slice;
   return chunk < floor ? floor : chunk;
 }
@@ -657,6 +678,119 @@ struct AttnSmem {
   unsigned last_flag;
 };
 
+// Cross-workgroup merge of the slices of kv head g, after this workgroup stored its partial
+// (unnormalised output, running max m, sum l) for each of its G heads with coherent stores: the
+// last slice to finish computes out = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max m).
+// Every load of a round is issued before any is used: (m, l) of all slices first, then each
+// output's slices eight at a time (addresses clamped to the last slice, surplus dropped).
+// mrg: LDS [G][kMaxSplits][2]; Ls: LDS, G floats; last_flag: LDS word.
+template <int HD, int G, int NT, bool COH>
+__device__ __forceinline__ void attn_merge_slices(const AttnArgs& a, int g, int active, int tid,
+                                                  float (&mrg)[G][kMaxSplits][2], float* Ls, unsigned& last_flag) {
+  const int stride = HD + 2;
+  publish();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned t = __hip_atomic_fetch_add(&a.tickets[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = (t == (unsigned)(active - 1)) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  // One round trip: the (m, l) of every slice and this thread's first RND slices of its outputs
+  // are all requested before anything waits ((m, l) first, so waiting for them leaves the rest in
+  // flight); later rounds only when there are more than RND slices.
+  constexpr int MLPT = (kMaxGroup * kMaxSplits + NT - 1) / NT;
+  constexpr int OPT = (G * HD + NT - 1) / NT;  // outputs per thread
+  constexpr int RND = OPT == 1 ? 32 : (OPT == 2 ? 16 : 8);  // slices per round (<= 32 loads per thread)
+  float ml[MLPT][2];
+#pragma unroll
+  for (int i = 0; i < MLPT; ++i) {
+    const int e = tid + i * NT;
+    if (e < G * active) {
+      const int h = e / active, sp = e - h * active;
+      const float* pp = a.partial + ((long)(g * G + h) * a.nsplit + sp) * stride;
+      ml[i][0] = load_shared(pp + HD);
+      ml[i][1] = load_shared(pp + HD + 1);
+    }
+  }
+  auto load_round = [&](int sp0, float (&v)[OPT][RND]) {
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+      const int e = min(tid + j * NT, G * HD - 1);
+      const float* src = a.partial + (long)(g * G + e / HD) * a.nsplit * stride + e % HD;
+#pragma unroll
+      for (int k = 0; k < RND; ++k) v[j][k] = sp0 + k < active ? load_shared(src + (long)(sp0 + k) * stride) : 0.f;
+    }
+  };
+  float v[OPT][RND];
+  load_round(0, v);
+#pragma unroll
+  for (int i = 0; i < MLPT; ++i) {
+    const int e = tid + i * NT;
+    if (e < G * active) {
+      const int h = e / active, sp = e - h * active;
+      mrg[h][sp][0] = ml[i][0];
+      mrg[h][sp][1] = ml[i][1];
+    }
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = kNegBig;
+    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, mrg[tid][sp][0]);
+    float L = 0.f;
+    for (int sp = 0; sp < active; ++sp) {
+      const float w = expf(mrg[tid][sp][0] - M);
+      mrg[tid][sp][0] = w;
+      L = fmaf(mrg[tid][sp][1], w, L);
+    }
+    Ls[tid] = L;
+  }
+  __syncthreads();
+  float Ov[OPT];
+#pragma unroll
+  for (int j = 0; j < OPT; ++j) Ov[j] = 0.f;
+  for (int sp0 = 0;;) {
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+      const int h = min(tid + j * NT, G * HD - 1) / HD;
+#pragma unroll
+      for (int k = 0; k < RND; ++k)
+        if (sp0 + k < active) Ov[j] = fmaf(v[j][k], mrg[h][sp0 + k][0], Ov[j]);
+    }
+    sp0 += RND;
+    if (sp0 >= active) break;
+    load_round(sp0, v);
+  }
+#pragma unroll
+  for (int j = 0; j < OPT; ++j) {
+    const int e = tid + j * NT;
+    if (e < G * HD) {
+      const int h = e / HD;
+      float* o = a.out + (long)(g * G + h) * HD + e % HD;
+      if constexpr (COH) store_shared(o, Ov[j] / Ls[h]);
+      else *o = Ov[j] / Ls[h];
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Re-rotates the K of the sink tokens r < kv_sink by angle freq*1 in place, fp16 round trip as
+// the reference (src/infer.cpp:307-325); kh is the kv head's K cache.
+template <int HD, int NT>
+__device__ __forceinline__ void rotate_sinks(const AttnArgs& a, uint16_t* kh, int kv_sink, int tid) {
+  for (int e = tid; e < kv_sink * (HD / 2); e += NT) {
+    const int r = e / (HD / 2);
+    const int j = 2 * (e % (HD / 2));
+    const float freq = a.inv_freq[j / 2];
+    const float c = cosf(freq), s = sinf(freq);
+    uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
+    uint16_t* p1 = kh + k_cache_idx(j + 1, r, a.msl);
+    const float v0 = (float)__builtin_bit_cast(f16, *p0), v1 = (float)__builtin_bit_cast(f16, *p1);
+    *p0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
+    *p1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
+  }
+}
+
 // K and V registers for one tile of one thread (loaded one tile ahead of use).
 template <int CPL, int DPT>
 struct AttnTileRegs {
@@ -694,18 +828,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
   const uint16_t* vh = a.vcache + head_off;
 
   if (pss.kv_sink > 0 && split == 0) {
-    // Re-rotate sink keys r < kv_sink by angle freq*1 in place (fp16 round trip as reference).
-    for (int e = tid; e < pss.kv_sink * (HD / 2); e += NT) {
-      const int r = e / (HD / 2);
-      const int j = 2 * (e % (HD / 2));
-      const float freq = a.inv_freq[j / 2];
-      const float c = cosf(freq), s = sinf(freq);
-      uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
-      uint16_t* p1 = kh + k_cache_idx(j + 1, r, a.msl);
-      const float v0 = (float)__builtin_bit_cast(f16, *p0), v1 = (float)__builtin_bit_cast(f16, *p1);
-      *p0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
-      *p1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
-    }
+    rotate_sinks<HD, NT>(a, kh, pss.kv_sink, tid);
     __syncthreads();
   }
 
@@ -732,10 +855,22 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
     }
   };
 
-  if constexpr (COH) {
-    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = load_shared(a.q + (long)g * G * HD + e);
-  } else {
-    for (int e = tid; e < G * HD; e += NT) sm.qs[e] = a.q[(long)g * G * HD + e];
+  // The first K/V tile does not depend on q: its loads go out first, then all of this thread's q
+  // loads, and only then does anything wait.
+  AttnTileRegs<CPL, DPT> cur, nxt;
+  load_tile(t_begin, cur);
+  {
+    constexpr int QPT = (G * HD + NT - 1) / NT;
+    float qv[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int e = min(tid + i * NT, G * HD - 1);
+      if constexpr (COH) qv[i] = load_shared(a.q + (long)g * G * HD + e);
+      else qv[i] = a.q[(long)g * G * HD + e];
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; ++i)
+      if (tid + i * NT < G * HD) sm.qs[tid + i * NT] = qv[i];
   }
   if constexpr (SIDE_KV) {
     for (int e = tid; e < HD / 2; e += NT) {
@@ -744,8 +879,6 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
                                      __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  AttnTileRegs<CPL, DPT> cur, nxt;
-  load_tile(t_begin, cur);
   float m_run[G], l_run[G], acc[DPT][G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -914,58 +1047,41 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
         store_shared(dst + HD + 1, l_run[h]);
       }
   }
-  publish();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned t = __hip_atomic_fetch_add(&a.tickets[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm.last_flag = (t == (unsigned)(active - 1)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!sm.last_flag) return;
-  // Merge (the last slice to finish): out = sum_s w_s o_s / sum_s w_s l_s, w_s = exp(m_s - max m).
-  // Every load of a round is issued before any is used: (max, sum) of all slices first, then each
-  // output's slices eight at a time (addresses clamped to the last slice, surplus dropped).
-  for (int e = tid; e < G * active; e += NT) {
-    const int h = e / active, sp = e - h * active;
-    const float* pp = a.partial + ((long)(g * G + h) * a.nsplit + sp) * stride;
-    sm.mrg[h][sp][0] = load_shared(pp + HD);
-    sm.mrg[h][sp][1] = load_shared(pp + HD + 1);
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = kNegBig;
-    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, sm.mrg[tid][sp][0]);
-    float L = 0.f;
-    for (int sp = 0; sp < active; ++sp) {
-      const float w = expf(sm.mrg[tid][sp][0] - M);
-      sm.mrg[tid][sp][0] = w;
-      L = fmaf(sm.mrg[tid][sp][1], w, L);
-    }
-    sm.red[0][tid][0] = L;
-  }
-  __syncthreads();
-  for (int e = tid; e < G * HD; e += NT) {
-    const int h = e / HD, i = e % HD;
-    const float* src = a.partial + (long)(g * G + h) * a.nsplit * stride + i;
-    float Ov = 0.f;
-    for (int sp0 = 0; sp0 < active; sp0 += 8) {
-      float v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = load_shared(src + (long)min(sp0 + k, active - 1) * stride);
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (sp0 + k < active) Ov = fmaf(v[k], sm.mrg[h][sp0 + k][0], Ov);
-    }
-    float* o = a.out + (long)(g * G + h) * HD + i;
-    if constexpr (COH) store_shared(o, Ov / sm.red[0][h][0]);
-    else *o = Ov / sm.red[0][h][0];
-  }
-  if (tid == 0) __hip_atomic_store(&a.tickets[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  attn_merge_slices<HD, G, NT, COH>(a, g, active, tid, sm.mrg, &sm.red[0][0][0], sm.last_flag);
 }
 
-// Split-KV attention as its own launch: grid (n_kv_heads, nsplit) of 256-thread workgroups.
+// One prefetch worker of NT threads: 16 loads of 16 bytes per thread in flight per round.
+template <int NT>
+__device__ __forceinline__ void prefetch_worker(const AttnPrefetch& pf, int j) {
+  constexpr int U = 16;
+  unsigned fold = 0;
+#pragma unroll 1
+  for (int ri = 0; ri < 3; ++ri) {
+    const PrefetchRange r = pf.r[ri];
+    const long nch = (r.units + r.chunk - 1) / r.chunk;
+    for (long c = j; c < nch; c += pf.blocks) {
+      const long end = min((c + 1) * r.chunk, r.units);
+      for (long i0 = c * r.chunk + threadIdx.x; i0 < end; i0 += (long)NT * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = r.p[min(i0 + (long)u * NT, end - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) fold ^= v[u][0] ^ v[u][3];
+      }
+    }
+  }
+  if (fold == pf.magic) pf.sink[threadIdx.x] = fold;
+}
+
+// Split-KV attention as its own launch: grid (n_kv_heads, nsplit + prefetch rows) of 256-thread
+// workgroups; the rows beyond nsplit are prefetch workers.
 template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
+  if ((int)blockIdx.y >= a.nsplit) {
+    const int j = ((int)blockIdx.y - a.nsplit) * (int)gridDim.x + (int)blockIdx.x;
+    if (j < a.pf.blocks) prefetch_worker<kBlock>(a.pf, j);
+    return;
+  }
   __shared__ AttnSmem<HD, G, kBlock> sm;
   attn_run<HD, G, kBlock, false, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
 }

@@ -18,6 +18,7 @@
 #include "decode_flow.h"
 #include "prefill.h"
 #include "kernels.h"
+#include "decode_attn.h"
 
 using namespace yk;
 
@@ -27,6 +28,7 @@ thread_local std::string g_thread_err;
 // Workgroups per CU for the kernel-level test hooks (0 = the decode path's default); set with
 // yhip_set_option(NULL, "test_bpc", n) so tests can force many row groups per wave.
 int g_test_bpc = 0;
+bool g_attn_mfma = true;  // attention kernel of the kernel-level entry points (process-wide option)
 
 struct LayerW {
   uint16_t* wqkv = nullptr;  // [q_dim + 2*kv_dim][dim]
@@ -87,7 +89,12 @@ struct yhip_ctx {
 
   bool use_graph = true;
   int attn_splits = 32;
-  int attn_min_slice = 64;
+  int attn_min_slice = 0;  // 0: the kernel's own default (attn_min_slice_for)
+  // weight prefetch on the attention launch: O (prefetch_o), the first prefetch_w13_mb MB of each
+  // of W1 and W3, over prefetch_blocks worker workgroups
+  int prefetch_o = 0, prefetch_w13_mb = 0, prefetch_blocks = 256;
+  bool attn_mfma = true;  // MFMA decode attention where the shape allows it
+  unsigned* pf_sink = nullptr;
   hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // hydrate, logits, argmax
 
   // single-launch decode (decode_flow.h)
@@ -209,9 +216,23 @@ MatvecArgs mv_base() {
   return a;
 }
 
+// The MFMA kernel (decode_attn.h) where the shape allows it (head_dim % 32 == 0, max_seq_len % 32
+// == 0) unless `mfma` is off; otherwise the SIMT split-KV kernel. Workgroups of 512 and 256 threads.
 template <int HD>
-bool launch_attention_hd(const AttnArgs& a, hipStream_t s) {
-  const dim3 grid(a.n_kv_heads, a.nsplit);
+bool launch_attention_hd(const AttnArgs& a, bool mfma, hipStream_t s) {
+  const int pf_rows = a.pf.blocks > 0 ? (a.pf.blocks + a.n_kv_heads - 1) / a.n_kv_heads : 0;
+  const dim3 grid(a.n_kv_heads, a.nsplit + pf_rows);
+  if constexpr (HD % 32 == 0) {
+    if (mfma && a.msl % 32 == 0) {
+      switch (a.n_heads / a.n_kv_heads) {
+        case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, 8>), grid, dim3(512), 0, s, a); return true;
+        case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, 8>), grid, dim3(512), 0, s, a); return true;
+        case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, 8>), grid, dim3(512), 0, s, a); return true;
+        case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, 8>), grid, dim3(512), 0, s, a); return true;
+        default: return false;
+      }
+    }
+  }
   switch (a.n_heads / a.n_kv_heads) {
     case 1: hipLaunchKernelGGL((attention_kernel<HD, 1>), grid, dim3(kBlock), 0, s, a); return true;
     case 2: hipLaunchKernelGGL((attention_kernel<HD, 2>), grid, dim3(kBlock), 0, s, a); return true;
@@ -221,13 +242,25 @@ bool launch_attention_hd(const AttnArgs& a, hipStream_t s) {
   }
 }
 
+// Fewest tokens per KV slice: the option's value, else 256 for the MFMA kernel (one workgroup of
+// eight waves covers short contexts without a cross-workgroup merge) and 64 for the SIMT kernel.
+int attn_min_slice_for(const yhip_ctx* ctx, bool mfma) {
+  if (ctx->attn_min_slice > 0) return ctx->attn_min_slice;
+  return mfma ? 256 : 64;
+}
+
+bool attn_uses_mfma(const yhip_ctx* ctx) {
+  return ctx->attn_mfma && ctx->c.head_dim % 32 == 0 && ctx->c.max_seq_len % 32 == 0;
+}
+
 int launch_attention(yhip_ctx* ctx, const AttnArgs& a, hipStream_t s) {
   bool ok = false;
+  const bool mfma = ctx ? ctx->attn_mfma : g_attn_mfma;
   switch (a.head_dim) {
-    case 16: ok = launch_attention_hd<16>(a, s); break;
-    case 32: ok = launch_attention_hd<32>(a, s); break;
-    case 64: ok = launch_attention_hd<64>(a, s); break;
-    case 128: ok = launch_attention_hd<128>(a, s); break;
+    case 16: ok = launch_attention_hd<16>(a, mfma, s); break;
+    case 32: ok = launch_attention_hd<32>(a, mfma, s); break;
+    case 64: ok = launch_attention_hd<64>(a, mfma, s); break;
+    case 128: ok = launch_attention_hd<128>(a, mfma, s); break;
     default: break;
   }
   if (!ok) return fail(ctx, YHIP_EINVAL, "unsupported attention shape (head_dim 16/32/64/128, 1/2/4/8 q heads per kv head)");
@@ -294,9 +327,23 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     t.n_kv_heads = c.n_kv_heads;
     t.msl = c.max_seq_len;
     t.nsplit = ctx->attn_splits;
-    t.min_slice = ctx->attn_min_slice;
+    t.min_slice = attn_min_slice_for(ctx, attn_uses_mfma(ctx));
     t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
+    if (ctx->prefetch_o || ctx->prefetch_w13_mb) {
+      // O is read by its matvec in 64 KB pieces (8 rows of q_dim halves per workgroup for q_dim
+      // 4096), W1/W3 in 32 KB pieces per matrix; chunk i of a range feeds consumer workgroup i.
+      const long o_units = (long)c.dim * qd * 2 / 16;
+      const long w_units = std::min((long)c.hidden_dim * c.dim * 2, (long)ctx->prefetch_w13_mb << 20) / 16;
+      if (ctx->prefetch_o) t.pf.r[0] = PrefetchRange{reinterpret_cast<const u32x4*>(L.wo), o_units, 4096};
+      if (w_units > 0) {
+        t.pf.r[1] = PrefetchRange{reinterpret_cast<const u32x4*>(L.w1), w_units, 2048};
+        t.pf.r[2] = PrefetchRange{reinterpret_cast<const u32x4*>(L.w3), w_units, 2048};
+      }
+      t.pf.blocks = ctx->prefetch_blocks;
+      t.pf.magic = 0x9E3779B9u;
+      t.pf.sink = ctx->pf_sink;
+    }
     if ((rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
     a = mv_base();
@@ -442,14 +489,14 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.pos = pos;
   d.mode = mode;
   d.nsplit = ctx->attn_splits;
-  d.min_slice = ctx->attn_min_slice;
+  d.min_slice = attn_min_slice_for(ctx, false);  // the single launch runs the SIMT attention
   d.act = c.act;
   d.eps = c.norm_eps;
   d.qkv_clip = c.qkv_clip;
   d.launch = ctx->flow_launches++;
   // attention workgroups: the active KV slices at this position (same rule as attn_run)
   const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
-  const int chunk = attn_chunk(kv_len, ctx->attn_splits, ctx->attn_min_slice);
+  const int chunk = attn_chunk(kv_len, ctx->attn_splits, d.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
   const int cus = ctx->num_cus;
   d.nb[kPhQkv] = phase_blocks((d.q_dim + 2 * d.kv_dim) / 2, cus, ctx->flow_bpc);
@@ -735,7 +782,6 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   yhip_ctx* ctx = new yhip_ctx();
   ctx->c = c;
   ctx->device = device_ordinal;
-  ctx->attn_splits = std::max(1, std::min(64, 512 / std::max(1, c.n_kv_heads)));
   auto bail = [&](int rc) {
     yhip_destroy(ctx);
     return rc;
@@ -744,6 +790,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device_ordinal) == hipSuccess && prop.multiProcessorCount > 0)
     ctx->num_cus = prop.multiProcessorCount;
+  // KV slices per kv head: one attention workgroup per CU over all kv heads at long context
+  ctx->attn_splits = std::max(1, std::min(64, ctx->num_cus / std::max(1, c.n_kv_heads)));
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "stream create failed"));
 
@@ -797,7 +845,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
                a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
                a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
                a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
-               a_bi = atake((size_t)ctx->num_cus * 64 * 4);
+               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_pfs = atake(1024 * 4);
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -815,6 +863,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->kvcur = (uint32_t*)(ctx->abase + a_kvc);
   ctx->best_v = (float*)(ctx->abase + a_bv);
   ctx->best_i = (int*)(ctx->abase + a_bi);
+  ctx->pf_sink = (unsigned*)(ctx->abase + a_pfs);
   {
     const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
     if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -975,6 +1024,10 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       g_test_bpc = value;
       return YHIP_OK;
     }
+    if (!strcmp(key, "attn_mfma")) {
+      g_attn_mfma = value != 0;
+      return YHIP_OK;
+    }
     return fail(nullptr, YHIP_EINVAL, std::string("unknown process-wide option ") + key);
   }
   hipSetDevice(ctx->device);
@@ -1000,8 +1053,18 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "attn_splits")) {
     if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "attn_splits must be in [1, 64]");
     ctx->attn_splits = value;
+  } else if (!strcmp(key, "attn_mfma")) {
+    ctx->attn_mfma = value != 0;
+  } else if (!strcmp(key, "prefetch_o")) {
+    ctx->prefetch_o = value != 0;
+  } else if (!strcmp(key, "prefetch_w13_mb")) {
+    if (value < 0 || value > 4096) return fail(ctx, YHIP_EINVAL, "prefetch_w13_mb must be in [0, 4096]");
+    ctx->prefetch_w13_mb = value;
+  } else if (!strcmp(key, "prefetch_blocks")) {
+    if (value < 8 || value > 4096 || value % 8) return fail(ctx, YHIP_EINVAL, "prefetch_blocks must be a multiple of 8 in [8, 4096]");
+    ctx->prefetch_blocks = value;
   } else if (!strcmp(key, "attn_min_slice")) {
-    if (value < 64 || value % 64) return fail(ctx, YHIP_EINVAL, "attn_min_slice must be a positive multiple of 64");
+    if (value < 0 || value % 64) return fail(ctx, YHIP_EINVAL, "attn_min_slice must be 0 or a positive multiple of 64");
     ctx->attn_min_slice = value;
   } else {
     return fail(ctx, YHIP_EINVAL, std::string("unknown option ") + key);

@@ -232,6 +232,11 @@ def set_test_bpc(n):
     _check(lib().yhip_set_option(None, b"test_bpc", int(n)))
 
 
+def set_attn_mfma(on):
+    """Attention kernel of the kernel-level hooks: MFMA (where the shape allows) or SIMT."""
+    _check(lib().yhip_set_option(None, b"attn_mfma", int(bool(on))))
+
+
 def matvec(x, w, gain=None, eps=1e-5, resid=None):
     d, n = w.shape
     x, xp = _f32(x)
