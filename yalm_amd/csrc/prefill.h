@@ -56,8 +56,11 @@ struct GemmArgs {
 
 constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
 
+// At most 128 VGPRs (four waves per SIMD) so four workgroups fit on a CU: 1024 slots on the GPU,
+// which holds the 800 tiles of a 3200 x 4096 output in one round (with 768 slots the last 32
+// tiles would run as a second round of full length).
 template <int EPI>
-__global__ void __launch_bounds__(256) gemm_nt_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) gemm_nt_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][kGBM * kGLds];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGBN * kGLds];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
