@@ -105,7 +105,9 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * totals; 0 = off).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
- * yhip_test_* / yhip_bench_* hooks, as above). */
+ * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
+ * GEMM variant: stages -1 = chosen per shape (default), 0 = register-staged kernel, 1 = 256 x 256
+ * large tiles, 2..4 = LDS pipeline stages; k-step 32 or 64; workgroup rows 128 or 256). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 
 /* Device time of the steps timed since "stats" was set: total microseconds between HIP events
@@ -160,6 +162,11 @@ int yhip_test_argmax(const float* logits, int n, int* out);
  * Writes the mean kernel time in microseconds. ---- */
 int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, int blocks_per_cu,
                       float* us_per_launch);
+
+/* Times one prefill GEMM launch (mode as yhip_test_gemm) on device-filled operands: average
+ * microseconds over `reps` launches after `warmup`, with HIP events on a private stream. No
+ * reference counterpart (the reference has no batched prefill). */
+int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int reps, float* us_per_launch);
 
 /* ---- microbenchmark of the split-KV attention kernel over `copies` rotating KV caches (random
  * fp16), at position kv_len - 1, `nsplit` slices of at least `min_slice` tokens. Mean microseconds. */

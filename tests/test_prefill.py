@@ -23,8 +23,21 @@ def hip():
     return H
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096)])
-def test_gemm_store_and_residual(M, N, K):
+# (LDS stages, k-step, workgroup rows); 0 stages = the register-staged kernel
+GEMM_VARIANTS = [(-1, 32, 128), (4, 32, 128), (2, 64, 128), (3, 64, 128), (2, 64, 256), (3, 64, 256),
+                 (1, 64, 256), (1, 32, 256), (0, 32, 128)]  # -1: chosen per shape; 1: the 256 x 256 kernel
+
+
+@pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}" for s, k, m in GEMM_VARIANTS])
+def gemm_variant(request):
+    hip().set_gemm_stages(*request.param)
+    yield request.param
+    hip().set_gemm_stages(-1)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096),
+                                   (130, 128, 448), (520, 256, 128)])
+def test_gemm_store_and_residual(M, N, K, gemm_variant):
     H = hip()
     rng = np.random.default_rng(M * 7 + N)
     a = f16(rng.standard_normal((M, K)))
@@ -38,7 +51,7 @@ def test_gemm_store_and_residual(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 64, 64), (150, 192, 256), (33, 96, 32)])
-def test_gemm_swiglu(M, N, K):
+def test_gemm_swiglu(M, N, K, gemm_variant):
     H = hip()
     rng = np.random.default_rng(M + N)
     a = f16(rng.standard_normal((M, K)))

@@ -163,6 +163,297 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) g
 }
 
 // ------------------------------------------------------------------------------------------
+// The same GEMM with an S-stage LDS pipeline fed by direct-to-LDS loads (global_load_lds_dwordx4:
+// lane l of a wave instruction writes 16 bytes at the instruction's LDS address + 16 l). A stage
+// holds one BK-deep k-step of both operands, 128 rows x 2 BK bytes each, with the 16-byte k-chunk
+// c of row r stored at position c ^ ((r / RPW) % CPR) (CPR = BK / 8 chunks per row, RPW = rows per
+// 256 bytes): a fragment read (one chunk of 32 rows) is served 16 lanes at a time from 64 banks
+// (a 256-byte period), and the swizzle puts the 16 rows of each pass in distinct banks (measured:
+// no LDS bank conflicts). S - 1 k-steps are in flight while one is used; nothing passes through
+// registers on the way to LDS, and each 16-deep slice's fragments are read while the previous
+// slice's MFMAs run. Same tiles, waves and epilogues as gemm_nt_kernel.
+// ------------------------------------------------------------------------------------------
+// Tile order of the pipelined GEMMs (one-dimensional grid of 8 * ceil(tiles / 8) workgroups).
+// Workgroups are handed to the eight XCDs in turn (workgroup b runs on XCD b % 8), and each XCD
+// takes a contiguous run of tiles in M-fastest order: the row panels of A (the activations, a few
+// tens of MB) are walked for one column panel of B (the weights) after another, so each weight
+// panel is fetched by one XCD and reused from its L2 across the row panels, and the whole weight
+// matrix is read from HBM about once. Returns false for the surplus workgroups.
+__device__ __forceinline__ bool gemm_tile(int mt, int nt, int& tm, int& tn) {
+  const int tiles = mt * nt, per = (tiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= tiles) return false;
+  tm = t % mt;
+  tn = t / mt;
+  return true;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {  // s_waitcnt vmcnt(N), expcnt and lgkmcnt unconstrained
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ void load_lds16(const uint16_t* src, uint16_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+// BM = 128 (four waves, 2 x 2) or 256 (eight waves, 4 x 2); every wave computes 64 x 64.
+template <int EPI, int S, int BK, int BM>
+__global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
+  static_assert(S >= 2 && (BK == 32 || BK == 64) && (BM == 128 || BM == 256), "stages, k-step, tile");
+  constexpr int NW = BM / 32;               // waves
+  constexpr int ATILE = BM * BK;            // halves of the A operand per stage
+  constexpr int BTILE = kGBN * BK;          // halves of the B operand per stage
+  constexpr int CPR = BK / 8;               // 16-byte chunks per row
+  constexpr int RPI = 1024 / (2 * BK);      // rows per 1 KB load instruction
+  constexpr int RPW = 256 / (2 * BK);       // rows per 256-byte bank period
+  constexpr int IA = BM / RPI / NW;         // A load instructions per wave per stage
+  constexpr int IB = kGBN / RPI / NW;       // B load instructions per wave per stage
+  constexpr int LPS = IA + IB;              // loads per wave per stage
+  constexpr int KK = BK / 16;               // MFMA k-slices per stage
+  static_assert(IA >= 1 && IB >= 1, "load split");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S][ATILE + BTILE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int NC = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;  // output columns per tile
+  int tm, tn;
+  if (!gemm_tile((g.M + BM - 1) / BM, (g.N + NC - 1) / NC, tm, tn)) return;
+  const int m0 = tm * BM, n0 = tn * NC;
+  auto swz = [](int r) { return (r / RPW) % CPR; };
+
+  // wave w fills the 1 KB pieces w, w + NW, ... of each operand tile
+  const uint16_t* arow[IA];
+  const uint16_t* brow[IB];
+#pragma unroll
+  for (int j = 0; j < IA; ++j) {
+    const int r = RPI * (wave + NW * j) + lane / CPR;
+    const int c = (lane % CPR) ^ swz(r);  // the global k-chunk this lane's LDS slot holds
+    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * c;
+  }
+#pragma unroll
+  for (int j = 0; j < IB; ++j) {
+    const int r = RPI * (wave + NW * j) + lane / CPR;
+    const int c = (lane % CPR) ^ swz(r);
+    if constexpr (EPI == kGemmSwiGLU) {
+      const int col = n0 + (r >> 6) * 32 + (r & 31);
+      const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
+      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+    } else {
+      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+    }
+  }
+  auto issue = [&](int kt) {
+    const int st = kt % S, k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, &smem[st][(wave + NW * j) * 512]);
+#pragma unroll
+    for (int j = 0; j < IB; ++j) load_lds16(brow[j] + k0, &smem[st][ATILE + (wave + NW * j) * 512]);
+  };
+  auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[2], u32x4 (&fb)[2]) {
+    const int c = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int ra = wm * 64 + t * 32 + (lane & 31);
+      const int rb = wn * 64 + t * 32 + (lane & 31);
+      fa[t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ swz(ra)));
+      fb[t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ swz(rb)));
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int nk = g.K / BK;
+#pragma unroll
+  for (int kt = 0; kt < S - 1; ++kt)
+    if (kt < nk) issue(kt);
+  for (int kt = 0; kt < nk; ++kt) {
+    // k-step kt has landed once at most S - 2 later stages (LPS loads each) are outstanding
+    if (kt + S - 2 < nk) wait_vmcnt<LPS * (S - 2)>();
+    else wait_vmcnt<0>();
+    // Every wave's part of stage kt is in and stage kt - 1 is no longer read. A bare barrier: the
+    // wait above already covers this wave's loads, and a fence here would also wait for the
+    // later stages still in flight.
+    __asm__ volatile("" ::: "memory");  // no LDS access moves across the barrier
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (kt + S - 1 < nk) issue(kt + S - 1);
+    const uint16_t* As = smem[kt % S];
+    const uint16_t* Bs = smem[kt % S] + ATILE;
+    u32x4 fa[2][2], fb[2][2];
+    read_frags(As, Bs, 0, fa[0], fb[0]);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + i * 32 + acc_row(r, lane);
+      if (m >= g.M) continue;
+      if constexpr (EPI == kGemmSwiGLU) {
+        const int j = n0 + wn * 32 + (lane & 31);
+        if (j < g.N) {
+          const float a1 = acc[i][0][r], a3 = acc[i][1][r];
+          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+          if (n >= g.N) continue;
+          float* cp = g.C + (long)m * g.ldc + n;
+          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
+          else *cp = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Large-tile GEMM: 256 x 256 per workgroup, four waves in 2 x 2 each computing 128 x 128 (4 x 4
+// tiles of 32 x 32; the 256 fp32 accumulators live in the accumulation registers), BK-deep
+// k-steps in an S-stage LDS pipeline (S x BK x 1 KB) filled by direct-to-LDS loads with the same
+// swizzle as gemm_lds_kernel, one workgroup per CU. A wave issues 2 MFMAs per fragment read; the
+// loads are latency-bound, so the pipeline keeps S - 1 stages in flight (measured: with one
+// 64 KB stage in flight the loads alone take 70% of the GEMM's time).
+// SwiGLU: the 256 B rows are 128 rows of W1 and the same 128 rows of W3 interleaved by 32, so a
+// wave's tiles 2q and 2q + 1 hold W1 and W3 of the same 32 output columns.
+// ------------------------------------------------------------------------------------------
+constexpr int kBigM = 256, kBigN = 256;
+
+template <int EPI, int S, int BK>
+__global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
+  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
+  constexpr int CPR = BK / 8, RPI = 1024 / (2 * BK), RPW = 256 / (2 * BK);
+  constexpr int ATILE = kBigM * BK, BTILE = kBigN * BK;
+  constexpr int IA = kBigM / RPI / 4, IB = kBigN / RPI / 4;  // load instructions per wave per stage
+  constexpr int LPS = IA + IB;
+  constexpr int KK = BK / 16;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S][ATILE + BTILE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int NC = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;  // output columns per tile
+  int tm, tn;
+  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + NC - 1) / NC, tm, tn)) return;
+  const int m0 = tm * kBigM, n0 = tn * NC;
+  auto swz = [](int r) { return (r / RPW) % CPR; };
+
+  const uint16_t* arow[IA];
+  const uint16_t* brow[IB];
+#pragma unroll
+  for (int j = 0; j < IA; ++j) {
+    const int r = RPI * (wave + 4 * j) + lane / CPR;
+    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * ((lane % CPR) ^ swz(r));
+  }
+#pragma unroll
+  for (int j = 0; j < IB; ++j) {
+    const int r = RPI * (wave + 4 * j) + lane / CPR;
+    const int c = (lane % CPR) ^ swz(r);
+    if constexpr (EPI == kGemmSwiGLU) {
+      const int col = n0 + (r >> 6) * 32 + (r & 31);
+      const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
+      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+    } else {
+      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+    }
+  }
+  auto issue = [&](int kt) {
+    uint16_t* st = smem[kt % S];
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
+#pragma unroll
+    for (int j = 0; j < IB; ++j) load_lds16(brow[j] + k0, st + ATILE + (wave + 4 * j) * 512);
+  };
+  auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+    const int c = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int ra = wm * 128 + t * 32 + (lane & 31);
+      const int rb = wn * 128 + t * 32 + (lane & 31);
+      fa[t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ swz(ra)));
+      fb[t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ swz(rb)));
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int nk = g.K / BK;
+#pragma unroll
+  for (int kt = 0; kt < S - 1; ++kt)
+    if (kt < nk) issue(kt);
+  for (int kt = 0; kt < nk; ++kt) {
+    // k-step kt has landed once at most S - 2 later stages are outstanding
+    if (kt + S - 2 < nk) wait_vmcnt<LPS * (S - 2)>();
+    else wait_vmcnt<0>();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
+    __asm__ volatile("" ::: "memory");
+    if (kt + S - 1 < nk) issue(kt + S - 1);
+    const uint16_t* As = smem[kt % S];
+    const uint16_t* Bs = smem[kt % S] + ATILE;
+    u32x4 fa[2][4], fb[2][4];
+    read_frags(As, Bs, 0, fa[0], fb[0]);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 128 + i * 32 + acc_row(r, lane);
+      if (m >= g.M) continue;
+      if constexpr (EPI == kGemmSwiGLU) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int j = n0 + wn * 64 + q * 32 + (lane & 31);
+          if (j < g.N) {
+            const float a1 = acc[i][2 * q][r], a3 = acc[i][2 * q + 1][r];
+            const float h = g.act == 1 ? silu(a1) : gelu(a1);
+            g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n = n0 + wn * 128 + j * 32 + (lane & 31);
+          if (n >= g.N) continue;
+          float* cp = g.C + (long)m * g.ldc + n;
+          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
+          else *cp = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Row kernels of the prefill (one workgroup per row).
 // ------------------------------------------------------------------------------------------
 // X[t][i] = fp32(E[tokens[t]][i]) (reference src/infer.cpp:460-481, exact)

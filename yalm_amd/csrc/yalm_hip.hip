@@ -29,6 +29,10 @@ thread_local std::string g_thread_err;
 // yhip_set_option(NULL, "test_bpc", n) so tests can force many row groups per wave.
 int g_test_bpc = 0;
 bool g_attn_mfma = true;  // attention kernel of the kernel-level entry points (process-wide option)
+int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-staged kernel)
+int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
+int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
+bool g_gemm_auto = true;  // prefill GEMM variant chosen per shape (cleared by forcing one)
 
 struct LayerW {
   uint16_t* wqkv = nullptr;  // [q_dim + 2*kv_dim][dim]
@@ -590,11 +594,50 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 }
 
 // ---- batched prefill ---------------------------------------------------------------------------
+// Prefill GEMM launch. The variant is chosen per shape unless forced with the process-wide
+// options: the 256 x 256 large-tile kernel for the W1/W3 + SwiGLU GEMM and for long K (W2), the
+// 128 x 128 two-stage 64-deep pipeline otherwise (QKV, O), the four-stage 32-deep one when
+// K % 64 != 0 (measured per shape at n = 3200).
 template <int EPI>
 int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
+  if (g_gemm_auto) {
+    if (EPI == kGemmSwiGLU || g.K >= 8192) {
+      g_gemm_stages = 1;
+      g_gemm_bk = 64;
+    } else {
+      g_gemm_stages = g.K % 64 == 0 ? 2 : 4;
+      g_gemm_bk = g.K % 64 == 0 ? 64 : 32;
+      g_gemm_bm = 128;
+    }
+  }
+  // one-dimensional grids of 8 * ceil(tiles / 8) workgroups (gemm_tile)
+  auto tiles8 = [&](int bm, int nc) {
+    const int t = ((g.M + bm - 1) / bm) * ((g.N + nc - 1) / nc);
+    return dim3(8 * ((t + 7) / 8));
+  };
+  if (g_gemm_stages == 1) {  // 256 x 256 tiles
+    const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
+    if (g_gemm_bk == 64 && g.K % 64 == 0)
+      hipLaunchKernelGGL((gemm_big_kernel<EPI, 2, 64>), tiles8(kBigM, nc), dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_big_kernel<EPI, 4, 32>), tiles8(kBigM, nc), dim3(256), 0, s, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
+    return YHIP_OK;
+  }
   const int ncols = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;
-  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, g);
+  const int bk = g.K % 64 == 0 ? g_gemm_bk : 32;  // a 64-deep k-step needs K % 64 == 0
+  const int bm = bk == 64 ? g_gemm_bm : 128;
+  const dim3 grid = tiles8(bm, ncols);
+  switch (g_gemm_stages * 10000 + bk * 1000 / 8 + bm) {
+    case 4 * 10000 + 4000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 4, 32, 128>), grid, dim3(256), 0, s, g); break;
+    case 2 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 128>), grid, dim3(256), 0, s, g); break;
+    case 3 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 128>), grid, dim3(256), 0, s, g); break;
+    case 2 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 256>), grid, dim3(512), 0, s, g); break;
+    case 3 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 256>), grid, dim3(512), 0, s, g); break;
+    default: hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, g); break;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
   return YHIP_OK;
@@ -1026,6 +1069,22 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     }
     if (!strcmp(key, "attn_mfma")) {
       g_attn_mfma = value != 0;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 0 register-staged; 1 large tile; 2..4 LDS stages
+      if (value < -1 || value > 4) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 4]");
+      g_gemm_auto = value < 0;
+      if (value >= 0) g_gemm_stages = value;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "gemm_bk")) {
+      if (value != 32 && value != 64) return fail(nullptr, YHIP_EINVAL, "gemm_bk must be 32 or 64");
+      g_gemm_bk = value;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "gemm_bm")) {
+      if (value != 128 && value != 256) return fail(nullptr, YHIP_EINVAL, "gemm_bm must be 128 or 256");
+      g_gemm_bm = value;
       return YHIP_OK;
     }
     return fail(nullptr, YHIP_EINVAL, std::string("unknown process-wide option ") + key);
@@ -1576,5 +1635,66 @@ extern "C" int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, i
   if (rc) return rc;
   if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, hipGetErrorString(e));
   *us_per_launch = ms * 1000.0f / reps;
+  return YHIP_OK;
+}
+
+extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int reps, float* us_per_launch) {
+  if (!us_per_launch || M <= 0 || N <= 0 || K <= 0 || mode < 0 || mode > 2 || reps <= 0 || warmup < 0)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  DevBufs d;
+  uint16_t* da = d.alloc<uint16_t>((size_t)M * K);
+  uint16_t* db = d.alloc<uint16_t>((size_t)N * K);
+  uint16_t* db3 = d.alloc<uint16_t>((size_t)N * K);
+  float* dc = d.alloc<float>((size_t)M * N);
+  uint16_t* dh = d.alloc<uint16_t>((size_t)M * N);
+  TRY_ALLOC(da);
+  TRY_ALLOC(db);
+  TRY_ALLOC(db3);
+  TRY_ALLOC(dc);
+  TRY_ALLOC(dh);
+  hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, da, (size_t)M * K, 11u);
+  hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db, (size_t)N * K, 12u);
+  hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db3, (size_t)N * K, 13u);
+  HIP_TRY(nullptr, hipMemset(dc, 0, (size_t)M * N * 4));
+  HIP_TRY(nullptr, hipDeviceSynchronize());
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.A = da;
+  g.lda = K;
+  g.B = db;
+  g.B3 = db3;
+  g.ldb = K;
+  g.C = dc;
+  g.ldc = N;
+  g.H = dh;
+  g.ldh = N;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.act = 1;
+  hipStream_t s;
+  HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  auto launch = [&] {
+    return mode == kGemmStore ? launch_gemm<kGemmStore>(nullptr, g, s)
+           : mode == kGemmResid ? launch_gemm<kGemmResid>(nullptr, g, s)
+                                : launch_gemm<kGemmSwiGLU>(nullptr, g, s);
+  };
+  int rc = 0;
+  for (int i = 0; i < warmup && !rc; ++i) rc = launch();
+  hipEvent_t e0, e1;
+  hipEventCreate(&e0);
+  hipEventCreate(&e1);
+  hipEventRecord(e0, s);
+  for (int i = 0; i < reps && !rc; ++i) rc = launch();
+  hipEventRecord(e1, s);
+  hipError_t e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  hipStreamDestroy(s);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, std::string("gemm bench: ") + hipGetErrorString(e));
+  *us_per_launch = 1000.f * ms / reps;
   return YHIP_OK;
 }

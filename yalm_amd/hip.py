@@ -26,6 +26,7 @@ EXPORTS = (
     "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
+    "yhip_bench_gemm",
 )
 
 
@@ -81,6 +82,7 @@ def lib():
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
         "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
+        "yhip_bench_gemm": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -230,6 +232,20 @@ class HipModel:
 def set_test_bpc(n):
     """Workgroups per CU used by the kernel-level hooks (0 = the decode path's default)."""
     _check(lib().yhip_set_option(None, b"test_bpc", int(n)))
+
+
+def set_gemm_stages(n, bk=32, bm=128):
+    """Prefill GEMM variant: -1 = chosen per shape (default); 0 = register-staged kernel; 1 = large
+    tiles (k-step bk); 2..4 = LDS pipeline stages with k-step bk and workgroup rows bm."""
+    _check(lib().yhip_set_option(None, b"gemm_stages", int(n)))
+    _check(lib().yhip_set_option(None, b"gemm_bk", int(bk)))
+    _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
+
+
+def bench_gemm(M, N, K, mode, warmup=3, reps=20):
+    us = ctypes.c_float()
+    _check(lib().yhip_bench_gemm(M, N, K, mode, warmup, reps, ctypes.byref(us)))
+    return us.value
 
 
 def set_attn_mfma(on):
