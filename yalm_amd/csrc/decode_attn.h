@@ -5,7 +5,7 @@
 // both products run on MFMA and every wave streams its own keys:
 //   - workgroup (kv head g, slice s) of NW waves; wave w takes the 32-key tiles w, w + NW, ... of
 //     the slice and keeps its own online softmax (no workgroup barrier per tile); the next tile's
-//     loads are in flight while the current one is used;
+//     loads are in flight while the current one is used; a wave with no tile issues no loads;
 //   - scores S^T = K Q^T with v_mfma_f32_16x16x32_f16, two 16-key groups per tile: A = 16 keys x
 //     32 dims of K straight from the 16-tiled cache (16 bytes per lane), B = the G query heads as
 //     columns. fp32 q is split into q_hi = fp16(q) and q_lo = fp16(q - q_hi) in columns h and
@@ -84,7 +84,9 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
   __shared__ float Ls[G];
   __shared__ unsigned last_flag;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index in a scalar register: per-wave tile bounds and loop exits are then uniform
+  // branches rather than exec-masked ones
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int g = blockIdx.x, split = blockIdx.y;
   const Positions pss = positions(a.params->pos, a.msl);
@@ -106,108 +108,113 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  // first tile in flight before q is read
-  int t0 = t_begin + TS * wave;
-  KvFrag<HD> cur, nxt;
-  load_kv_frag<HD>(kr, vr, a.msl, t0, col, grp, cur);
-
-  // q as the B operand: column col is head col (hi part) or head col - G (lo part); others zero
-  u32x4 qf[KS];
-  {
-    const bool used = col < 2 * G;
-    const bool lo = col >= G;
-    const int h = used ? (lo ? col - G : col) : 0;
-    const float* qp = a.q + (long)(g * G + h) * HD + 8 * grp;
-    f32x4 q4[KS][2];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
-      q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      f16x8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = q4[ks][e >> 2][e & 3];
-        const f16 hi = (f16)x;
-        v[e] = !used ? (f16)0.f : (lo ? (f16)(x - (float)hi) : hi);
-      }
-      qf[ks] = __builtin_bit_cast(u32x4, v);
-    }
-  }
-
-  const float scale = 1.0f / sqrtf((float)HD);
   float m_run = kNegBig, l_run = 0.f;
   f32x4 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // one 32-key tile: scores, online softmax (per column = head), values
-  auto tile = [&](const KvFrag<HD>& f, int t0) {
-    f32x4 s[2];
+  // A wave past the slice's end loads nothing and computes nothing (not even q): it enters the
+  // workgroup merge with (m, l, o) = (-inf, 0, 0). At short context most waves are such, and
+  // keeping their loads out of the memory queues shortens the working waves' round trips.
+  int t0 = t_begin + TS * wave;
+  if (t0 < t_end) {
+    // first tile in flight before q is read
+    KvFrag<HD> cur, nxt;
+    load_kv_frag<HD>(kr, vr, a.msl, t0, col, grp, cur);
+
+    // q as the B operand: column col is head col (hi part) or head col - G (lo part); others zero
+    u32x4 qf[KS];
+    {
+      const bool used = col < 2 * G;
+      const bool lo = col >= G;
+      const int h = used ? (lo ? col - G : col) : 0;
+      const float* qp = a.q + (long)(g * G + h) * HD + 8 * grp;
+      f32x4 q4[KS][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
+        q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
+      }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[j] = mfma_16x16x32(f.k[j][ks], qf[ks], s[j]);
-    }
-    float sv[8];  // keys t0 + 8 grp + e
-    float mt = kNegBig;
+      for (int ks = 0; ks < KS; ++ks) {
+        f16x8 v;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float raw = s[e >> 2][e & 3];
-      const float v = raw + __shfl_xor(raw, G, 16);  // hi + lo columns (both partners get the sum)
-      sv[e] = (t0 + 8 * grp + e < t_end) ? v * scale : kNegBig;
-      mt = fmaxf(mt, sv[e]);
+        for (int e = 0; e < 8; ++e) {
+          const float x = q4[ks][e >> 2][e & 3];
+          const f16 hi = (f16)x;
+          v[e] = !used ? (f16)0.f : (lo ? (f16)(x - (float)hi) : hi);
+        }
+        qf[ks] = __builtin_bit_cast(u32x4, v);
+      }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float corr = expf(m_run - m_new);
-    m_run = m_new;
-    f16x8 pf;
-    float psum = 0.f;
+
+    const float scale = 1.0f / sqrtf((float)HD);
+    // one 32-key tile: scores, online softmax (per column = head), values
+    auto tile = [&](const KvFrag<HD>& f, int t0) {
+      f32x4 s[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = sv[e] > kNegBig ? expf(sv[e] - m_new) : 0.f;
-      psum += p;
-      const float ps = p * kPScale;
-      const f16 hi = (f16)ps;
-      pf[e] = col < G ? hi : (col < 2 * G ? (f16)(ps - (float)hi) : (f16)0.f);
-    }
-    l_run = l_run * corr + psum;
-    const u32x4 pb = __builtin_bit_cast(u32x4, pf);
+      for (int j = 0; j < 2; ++j) {
+        s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      acc[dt] *= corr;
-      acc[dt] = mfma_16x16x32(f.v[dt], pb, acc[dt]);
-    }
-  };
-  // Two register buffers used alternately (unrolled by two, no copies between them): while one
-  // tile is used the next one's loads are in flight, and the scheduling barrier keeps them at the
-  // top. The explicit wait for the current tile is free in the steady state and keeps the
-  // compiler from waiting on the in-flight tile inside the current one.
-  for (;;) {
-    int tn = t0 + TS * NW;
-    if (tn >= t_end) {
-      if (t0 < t_end) tile(cur, t0);  // a wave past the slice's end has no tile
-      break;
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
-    load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, nxt);
-    __builtin_amdgcn_sched_barrier(0);
-    tile(cur, t0);
-    t0 = tn;
-    tn = t0 + TS * NW;
-    if (tn >= t_end) {
+        for (int ks = 0; ks < KS; ++ks) s[j] = mfma_16x16x32(f.k[j][ks], qf[ks], s[j]);
+      }
+      float sv[8];  // keys t0 + 8 grp + e
+      float mt = kNegBig;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float raw = s[e >> 2][e & 3];
+        const float v = raw + __shfl_xor(raw, G, 16);  // hi + lo columns (both partners get the sum)
+        sv[e] = (t0 + 8 * grp + e < t_end) ? v * scale : kNegBig;
+        mt = fmaxf(mt, sv[e]);
+      }
+      mt = fmaxf(mt, __shfl_xor(mt, 16));
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float m_new = fmaxf(m_run, mt);
+      const float corr = expf(m_run - m_new);
+      m_run = m_new;
+      f16x8 pf;
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = sv[e] > kNegBig ? expf(sv[e] - m_new) : 0.f;
+        psum += p;
+        const float ps = p * kPScale;
+        const f16 hi = (f16)ps;
+        pf[e] = col < G ? hi : (col < 2 * G ? (f16)(ps - (float)hi) : (f16)0.f);
+      }
+      l_run = l_run * corr + psum;
+      const u32x4 pb = __builtin_bit_cast(u32x4, pf);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        acc[dt] *= corr;
+        acc[dt] = mfma_16x16x32(f.v[dt], pb, acc[dt]);
+      }
+    };
+    // Two register buffers used alternately (unrolled by two, no copies between them): while one
+    // tile is used the next one's loads are in flight, and the scheduling barrier keeps them at the
+    // top. The explicit wait for the current tile is free in the steady state and keeps the
+    // compiler from waiting on the in-flight tile inside the current one.
+    for (;;) {
+      int tn = t0 + TS * NW;
+      if (tn >= t_end) {
+        tile(cur, t0);
+        break;
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
+      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+      tile(cur, t0);
+      t0 = tn;
+      tn = t0 + TS * NW;
+      if (tn >= t_end) {
+        tile(nxt, t0);
+        break;
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, cur);
+      __builtin_amdgcn_sched_barrier(0);
       tile(nxt, t0);
-      break;
+      t0 = tn;
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, cur);
-    __builtin_amdgcn_sched_barrier(0);
-    tile(nxt, t0);
-    t0 = tn;
   }
 
   // this wave's (m, l, o): l summed over the four lane groups, o over the hi/lo columns

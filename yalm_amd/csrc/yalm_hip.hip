@@ -222,6 +222,11 @@ MatvecArgs mv_base() {
 
 // The MFMA kernel (decode_attn.h) where the shape allows it (head_dim % 32 == 0, max_seq_len % 32
 // == 0) unless `mfma` is off; otherwise the SIMT split-KV kernel. Workgroups of 512 and 256 threads.
+// Waves per MFMA attention workgroup. Measured on MI355X: 4 waves (a workgroup per 128 keys) is
+// faster at a few hundred keys but slower from ~16K keys on, where 8 waves keep twice the bytes in
+// flight per CU.
+constexpr int kAttnWaves = 8;
+
 template <int HD>
 bool launch_attention_hd(const AttnArgs& a, bool mfma, hipStream_t s) {
   const int pf_rows = a.pf.blocks > 0 ? (a.pf.blocks + a.n_kv_heads - 1) / a.n_kv_heads : 0;
@@ -229,10 +234,10 @@ bool launch_attention_hd(const AttnArgs& a, bool mfma, hipStream_t s) {
   if constexpr (HD % 32 == 0) {
     if (mfma && a.msl % 32 == 0) {
       switch (a.n_heads / a.n_kv_heads) {
-        case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, 8>), grid, dim3(512), 0, s, a); return true;
-        case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, 8>), grid, dim3(512), 0, s, a); return true;
-        case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, 8>), grid, dim3(512), 0, s, a); return true;
-        case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, 8>), grid, dim3(512), 0, s, a); return true;
+        case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, kAttnWaves>), grid, dim3(64 * kAttnWaves), 0, s, a); return true;
+        case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, kAttnWaves>), grid, dim3(64 * kAttnWaves), 0, s, a); return true;
+        case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, kAttnWaves>), grid, dim3(64 * kAttnWaves), 0, s, a); return true;
+        case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, kAttnWaves>), grid, dim3(64 * kAttnWaves), 0, s, a); return true;
         default: return false;
       }
     }
