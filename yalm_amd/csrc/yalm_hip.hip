@@ -606,24 +606,32 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 template <int EPI>
 int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
+  // Variant per shape, from a sweep of the Mistral-7B shapes over M = 64..3200 on MI355X: the
+  // 256 x 256 tiles win only from ~3K rows (W1/W3, and W2 with its 14336-long rows); below that the
+  // 128-row LDS pipeline wins (up to 2.9x for W2 at a few hundred rows), with 256-row workgroups
+  // in between for W1/W3 and W2.
+  int stages = g_gemm_stages, bk = g_gemm_bk, bm = g_gemm_bm;
   if (g_gemm_auto) {
-    if (EPI == kGemmSwiGLU || g.K >= 8192) {
-      g_gemm_stages = 1;
-      g_gemm_bk = 64;
-    } else {
-      g_gemm_stages = g.K % 64 == 0 ? 2 : 4;
-      g_gemm_bk = g.K % 64 == 0 ? 64 : 32;
-      g_gemm_bm = 128;
+    const bool big_rows = EPI == kGemmSwiGLU || g.K >= 8192;
+    stages = g.K % 64 == 0 ? 2 : 4;
+    bk = g.K % 64 == 0 ? 64 : 32;
+    bm = 128;
+    if (big_rows && g.K % 64 == 0) {
+      if (g.M >= 3072) {
+        stages = 1;
+      } else if (g.M >= (EPI == kGemmSwiGLU ? 192 : 1536)) {
+        bm = 256;
+      }
     }
   }
   // one-dimensional grids of 8 * ceil(tiles / 8) workgroups (gemm_tile)
-  auto tiles8 = [&](int bm, int nc) {
-    const int t = ((g.M + bm - 1) / bm) * ((g.N + nc - 1) / nc);
+  auto tiles8 = [&](int tm, int nc) {
+    const int t = ((g.M + tm - 1) / tm) * ((g.N + nc - 1) / nc);
     return dim3(8 * ((t + 7) / 8));
   };
-  if (g_gemm_stages == 1) {  // 256 x 256 tiles
+  if (stages == 1) {  // 256 x 256 tiles
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
-    if (g_gemm_bk == 64 && g.K % 64 == 0)
+    if (bk == 64 && g.K % 64 == 0)
       hipLaunchKernelGGL((gemm_big_kernel<EPI, 2, 64>), tiles8(kBigM, nc), dim3(256), 0, s, g);
     else
       hipLaunchKernelGGL((gemm_big_kernel<EPI, 4, 32>), tiles8(kBigM, nc), dim3(256), 0, s, g);
@@ -632,10 +640,10 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     return YHIP_OK;
   }
   const int ncols = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;
-  const int bk = g.K % 64 == 0 ? g_gemm_bk : 32;  // a 64-deep k-step needs K % 64 == 0
-  const int bm = bk == 64 ? g_gemm_bm : 128;
+  if (g.K % 64 != 0) bk = 32;  // a 64-deep k-step needs K % 64 == 0
+  if (bk != 64) bm = 128;
   const dim3 grid = tiles8(bm, ncols);
-  switch (g_gemm_stages * 10000 + bk * 1000 / 8 + bm) {
+  switch (stages * 10000 + bk * 1000 / 8 + bm) {
     case 4 * 10000 + 4000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 4, 32, 128>), grid, dim3(256), 0, s, g); break;
     case 2 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 128>), grid, dim3(256), 0, s, g); break;
     case 3 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 128>), grid, dim3(256), 0, s, g); break;
