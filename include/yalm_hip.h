@@ -52,7 +52,10 @@ typedef struct {
 int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx** out);
 int yhip_destroy(yhip_ctx* ctx);
 
-/* Weight upload (host -> HBM), replaces Block::cuda() (src/model.cpp:217-241).
+/* Weight upload (host -> HBM), replaces Block::cuda() (src/model.cpp:217-241) and its
+ * upload_cuda copies (src/infer.cu:34-39). The sources may be pageable (e.g. an mmapped .yalm):
+ * large tensors move through pinned staging chunks (option "upload_stage_mb"). Returns after the
+ * copies have completed, so the caller may release the host memory.
  * Shapes: rms_* [dim] fp32; wq [n_heads*hd][dim]; wk, wv [n_kv_heads*hd][dim]; wo [dim][n_heads*hd];
  * w1, w3 [hidden][dim]; w2 [dim][hidden]. */
 int yhip_upload_layer(yhip_ctx* ctx, int layer, const float* rms_att, const float* rms_ffn,
@@ -107,7 +110,11 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
  * GEMM variant: stages -1 = chosen per shape (default), 0 = register-staged kernel, 1 = 256 x 256
- * large tiles, 2..4 = LDS pipeline stages; k-step 32 or 64; workgroup rows 128 or 256). */
+ * large tiles, 2..4 = LDS pipeline stages; k-step 32 or 64; workgroup rows 128 or 256),
+ * "upload_stage_mb" (yhip_upload_layer / yhip_upload_globals copy tensors of 64 KB and more through
+ * a ring of three pinned staging chunks of this many MB, default 64; 0 = direct copies from the
+ * caller's pageable memory as the reference's upload_cuda, src/infer.cu:34-39) and
+ * "upload_threads" (host threads filling a staging chunk, default 8). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 
 /* Device time of the steps timed since "stats" was set: total microseconds between HIP events

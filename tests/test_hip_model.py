@@ -225,3 +225,30 @@ def test_bad_arguments_return_errors():
     with H.HipModel(dict(MICRO, n_kv_heads=4)) as m:  # one q head per kv head: no instantiation
         with pytest.raises(H.HipError):
             m.set_option("single_launch", 1)
+
+
+def test_staged_upload_is_bit_identical():
+    # Weight upload through pinned staging chunks (the default) and through direct pageable copies
+    # (the reference's upload_cuda) must leave the same bytes in HBM: the same logits bit for bit.
+    # 1 MB chunks split the 16 MB embedding over the three-chunk ring several times; the layer
+    # tensors (128-393 KB) take one chunk each.
+    H = hip()
+    cfg = dict(TINY)
+    t = np_tensors(cfg, seed=41)
+    toks = [1, 5, 900, 31999, 7]
+    out = {}
+    try:
+        for stage_mb, threads in ((0, 1), (1, 3), (64, 8)):
+            H.set_upload(stage_mb, threads)
+            with H.HipModel(cfg, t) as hm:
+                out[stage_mb] = np.stack([hm.forward(tok, pos) for pos, tok in enumerate(toks)])
+    finally:
+        H.set_upload()
+    assert np.all(np.isfinite(out[0]))
+    for k in (1, 64):
+        assert np.array_equal(out[k], out[0]), k
+    with pytest.raises(H.HipError):
+        H.set_upload(-1, 8)
+    with pytest.raises(H.HipError):
+        H.set_upload(64, 0)
+    H.set_upload()

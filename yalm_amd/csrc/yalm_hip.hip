@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/yalm_hip.h"
@@ -33,6 +34,8 @@ int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-
 int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
 bool g_gemm_auto = true;  // prefill GEMM variant chosen per shape (cleared by forcing one)
+int g_upload_stage_mb = 64;  // weight upload: pinned staging chunk in MB (0 = direct pageable copies)
+int g_upload_threads = 8;    // weight upload: host threads filling a staging chunk
 
 struct LayerW {
   uint16_t* wqkv = nullptr;  // [q_dim + 2*kv_dim][dim]
@@ -63,6 +66,13 @@ struct yhip_ctx {
   int num_cus = 256;
   hipStream_t stream = nullptr;
   std::string err;
+
+  // weight upload staging: a ring of pinned chunks (hipHostMalloc) with an event per chunk
+  static constexpr int kStageBufs = 3;
+  char* stage[kStageBufs] = {};
+  hipEvent_t stage_ev[kStageBufs] = {};
+  size_t stage_bytes = 0;
+  int stage_next = 0;
 
   char* wbase = nullptr;
   size_t wbytes = 0;
@@ -956,9 +966,80 @@ extern "C" int yhip_destroy(yhip_ctx* ctx) {
   if (ctx->kv) hipFree(ctx->kv);
   if (ctx->abase) hipFree(ctx->abase);
   if (ctx->logits_host) hipHostFree(ctx->logits_host);
+  for (int k = 0; k < yhip_ctx::kStageBufs; ++k) {
+    if (ctx->stage[k]) hipHostFree(ctx->stage[k]);
+    if (ctx->stage_ev[k]) hipEventDestroy(ctx->stage_ev[k]);
+  }
   if (ctx->argmax_host) hipHostFree(ctx->argmax_host);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
+  return YHIP_OK;
+}
+
+// ---- weight upload -------------------------------------------------------------------------
+// A copy from pageable memory makes the runtime bounce every byte through its own small pinned
+// buffers one piece at a time. Large tensors instead go through a ring of kStageBufs pinned chunks:
+// host threads fill chunk k from the source (an mmapped checkpoint or any host buffer) while the DMA
+// engine drains the chunks filled before it; a chunk is refilled once the event recorded after its
+// copy has completed. Tensors under 64 KB (norm gains) are copied directly.
+namespace {
+void parallel_copy(char* dst, const char* src, size_t n, int threads) {
+  constexpr size_t kMinPerThread = 4u << 20;
+  const int t = (int)std::max<size_t>(1, std::min<size_t>((size_t)std::max(threads, 1), n / kMinPerThread));
+  if (t == 1) {
+    memcpy(dst, src, n);
+    return;
+  }
+  const size_t per = (n / t + 4095) & ~(size_t)4095;
+  std::vector<std::thread> pool;
+  pool.reserve(t);
+  for (int i = 0; i < t; ++i) {
+    const size_t b = std::min(n, (size_t)i * per), e = std::min(n, b + per);
+    if (b < e) pool.emplace_back([=] { memcpy(dst + b, src + b, e - b); });
+  }
+  for (std::thread& th : pool) th.join();
+}
+}  // namespace
+
+static int ensure_stage(yhip_ctx* ctx, size_t chunk) {
+  if (ctx->stage_bytes == chunk) return YHIP_OK;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  for (int k = 0; k < yhip_ctx::kStageBufs; ++k) {
+    if (ctx->stage[k]) HIP_TRY(ctx, hipHostFree(ctx->stage[k]));
+    ctx->stage[k] = nullptr;
+  }
+  ctx->stage_bytes = 0;
+  for (int k = 0; k < yhip_ctx::kStageBufs; ++k) {
+    if (hipHostMalloc((void**)&ctx->stage[k], chunk, hipHostMallocDefault) != hipSuccess) {
+      ctx->stage[k] = nullptr;
+      return fail(ctx, YHIP_EDEVICE, "pinned staging buffer allocation failed");
+    }
+    if (!ctx->stage_ev[k]) HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->stage_ev[k], hipEventDisableTiming));
+  }
+  ctx->stage_bytes = chunk;
+  return YHIP_OK;
+}
+
+// Enqueues the host → device copy of `bytes` bytes on the context's stream. The source may be
+// released once the stream has been synchronised.
+static int upload_h2d(yhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  const size_t chunk = (size_t)g_upload_stage_mb << 20;
+  if (chunk == 0 || bytes < ((size_t)64 << 10)) {
+    HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    return YHIP_OK;
+  }
+  if (int rc = ensure_stage(ctx, chunk)) return rc;
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  for (size_t off = 0; off < bytes; off += chunk) {
+    const size_t n = std::min(chunk, bytes - off);
+    const int k = ctx->stage_next;
+    ctx->stage_next = (k + 1) % yhip_ctx::kStageBufs;
+    HIP_TRY(ctx, hipEventSynchronize(ctx->stage_ev[k]));  // chunk k's previous copy has drained
+    parallel_copy(ctx->stage[k], s + off, n, g_upload_threads);
+    HIP_TRY(ctx, hipMemcpyAsync(d + off, ctx->stage[k], n, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipEventRecord(ctx->stage_ev[k], ctx->stream));
+  }
   return YHIP_OK;
 }
 
@@ -974,15 +1055,15 @@ extern "C" int yhip_upload_layer(yhip_ctx* ctx, int layer, const float* rms_att,
   LayerW& L = ctx->layers[layer];
   hipStream_t s = ctx->stream;
   HIP_TRY(ctx, hipSetDevice(ctx->device));
-  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv, wq, qd * dim * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv + qd * dim, wk, kvd * dim * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.wqkv + (qd + kvd) * dim, wv, kvd * dim * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.wo, wo, dim * qd * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.w1, w1, hid * dim * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.w3, w3, hid * dim * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.w2, w2, dim * hid * 2, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.rms_att, rms_att, dim * 4, hipMemcpyHostToDevice, s));
-  HIP_TRY(ctx, hipMemcpyAsync(L.rms_ffn, rms_ffn, dim * 4, hipMemcpyHostToDevice, s));
+  int rc = 0;
+  if ((rc = upload_h2d(ctx, L.wqkv, wq, qd * dim * 2)) || (rc = upload_h2d(ctx, L.wqkv + qd * dim, wk, kvd * dim * 2)) ||
+      (rc = upload_h2d(ctx, L.wqkv + (qd + kvd) * dim, wv, kvd * dim * 2)) ||
+      (rc = upload_h2d(ctx, L.wo, wo, dim * qd * 2)) || (rc = upload_h2d(ctx, L.w1, w1, hid * dim * 2)) ||
+      (rc = upload_h2d(ctx, L.w3, w3, hid * dim * 2)) || (rc = upload_h2d(ctx, L.w2, w2, dim * hid * 2)) ||
+      (rc = upload_h2d(ctx, L.rms_att, rms_att, dim * 4)) || (rc = upload_h2d(ctx, L.rms_ffn, rms_ffn, dim * 4))) {
+    hipStreamSynchronize(s);
+    return rc;
+  }
   HIP_TRY(ctx, hipStreamSynchronize(s));  // host buffers may be released after return
   L.loaded = true;
   return YHIP_OK;
@@ -994,9 +1075,12 @@ extern "C" int yhip_upload_globals(yhip_ctx* ctx, const uint16_t* embed, const f
   const yhip_config& c = ctx->c;
   const size_t n = (size_t)c.vocab_size * c.dim;
   HIP_TRY(ctx, hipSetDevice(ctx->device));
-  HIP_TRY(ctx, hipMemcpyAsync(ctx->embed, embed, n * 2, hipMemcpyHostToDevice, ctx->stream));
-  HIP_TRY(ctx, hipMemcpyAsync(ctx->wcls, wcls ? wcls : embed, n * 2, hipMemcpyHostToDevice, ctx->stream));
-  HIP_TRY(ctx, hipMemcpyAsync(ctx->rms_final, rms_final, (size_t)c.dim * 4, hipMemcpyHostToDevice, ctx->stream));
+  int rc = 0;
+  if ((rc = upload_h2d(ctx, ctx->embed, embed, n * 2)) || (rc = upload_h2d(ctx, ctx->wcls, wcls ? wcls : embed, n * 2)) ||
+      (rc = upload_h2d(ctx, ctx->rms_final, rms_final, (size_t)c.dim * 4))) {
+    hipStreamSynchronize(ctx->stream);
+    return rc;
+  }
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   ctx->globals_loaded = true;
   return YHIP_OK;
@@ -1093,6 +1177,16 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     if (!strcmp(key, "gemm_bk")) {
       if (value != 32 && value != 64) return fail(nullptr, YHIP_EINVAL, "gemm_bk must be 32 or 64");
       g_gemm_bk = value;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "upload_stage_mb")) {
+      if (value < 0 || value > 1024) return fail(nullptr, YHIP_EINVAL, "upload_stage_mb must be in [0, 1024]");
+      g_upload_stage_mb = value;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "upload_threads")) {
+      if (value < 1 || value > 64) return fail(nullptr, YHIP_EINVAL, "upload_threads must be in [1, 64]");
+      g_upload_threads = value;
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_bm")) {

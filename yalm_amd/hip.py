@@ -242,6 +242,13 @@ def set_gemm_stages(n, bk=32, bm=128):
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
 
 
+def set_upload(stage_mb=64, threads=8):
+    """Weight upload: pinned staging chunk size in MB (0 = direct copies from pageable memory) and
+    the host threads that fill a chunk."""
+    _check(lib().yhip_set_option(None, b"upload_stage_mb", int(stage_mb)))
+    _check(lib().yhip_set_option(None, b"upload_threads", int(threads)))
+
+
 def bench_gemm(M, N, K, mode, warmup=3, reps=20):
     us = ctypes.c_float()
     _check(lib().yhip_bench_gemm(M, N, K, mode, warmup, reps, ctypes.byref(us)))
