@@ -98,7 +98,7 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * 0 = per-op kernels, the default), "flow_bpc" / "flow_bpc_w2" (workgroups per CU of the single
  * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
- * kv head, default compute units / n_kv_heads clamped to [1,64]),
+ * kv head, default 3/4 of compute units / n_kv_heads clamped to [1,64]),
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default, 256
  * for the MFMA attention and 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode attention on the matrix cores where head_dim %
  * 32 == 0 and max_seq_len % 32 == 0, default; 0 = the SIMT kernel), "prefetch_o" /
