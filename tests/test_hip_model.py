@@ -157,6 +157,27 @@ def test_forward_argmax_matches_host_argmax(path):
             tok = nxt
 
 
+@pytest.mark.parametrize("path", ["single", "graph"])
+def test_forward_argmax_tie_takes_the_first_index(path):
+    # The winning lm_head row copied to rows 7, 100 and 30001 (different workgroups): four exactly
+    # equal maxima. The reference's sampler (src/sampler.cpp:27-38) returns the first of them.
+    cfg = dict(TINY)
+    t = np_tensors(cfg, seed=26)
+    with hip().HipModel(cfg, t) as a:
+        use_path(a, "graph")
+        m = O.argmax(a.forward(5, 0))
+    w = t["model.output.weight"].copy()
+    for r in (7, 100, 30001):
+        w[r] = w[m]
+    t2 = dict(t, **{"model.output.weight": w})
+    with hip().HipModel(cfg, t2) as b, hip().HipModel(cfg, t2) as c:
+        use_path(b, path)
+        use_path(c, "graph")
+        lg = c.forward(5, 0)
+        assert lg[7] == lg[100] == lg[30001] == lg[m] == lg.max()
+        assert b.forward_argmax(5, 0) == min(7, m) == O.argmax(lg)
+
+
 @pytest.mark.parametrize("path", ["single", "graph", "graph_simt"])
 @pytest.mark.parametrize("shape", ["micro", "hd32"])
 def test_sink_mode_beyond_context_matches_oracle(path, shape):

@@ -542,13 +542,41 @@ __device__ __forceinline__ void argmax_finish(RowMax mx, int slot, int nslots, f
   }
 }
 
+// Packed (logit, index) whose unsigned order is the argmax order with the reference's tie rule
+// (src/sampler.cpp:27-38: the first index of the maximum): the float's bits made monotonic in the
+// high word (negative values complemented, positive ones with the sign bit set), the complement of
+// the index in the low word. NaN and -inf never reach it (track_rows keeps only v > kNegBig).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+  const unsigned u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 == +0 for the comparison
+  const unsigned ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (unsigned)(~i);
+}
+
+// Workgroup best of the waves' maxima (wave-uniform), posted with one 64-bit atomic max. The atomic
+// returns nothing, so no workgroup waits on it; the key is zeroed before each step by the step-
+// parameter kernel and read back after the launch.
+__device__ __forceinline__ void argmax_post(RowMax mx, unsigned long long* key) {
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  if (lane == 0) {
+    sv[wave] = mx.v;
+    si[wave] = mx.i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    RowMax r;
+    for (int w = 0; w < kWavesPerBlock; ++w) better(r.v, r.i, sv[w], si[w]);
+    if (r.i != 0x7fffffff) __hip_atomic_fetch_max(key, argmax_key(r.v, r.i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Final rmsnorm + lm_head with the greedy argmax fused in (a.track_max set).
 template <int KC>
-__global__ void __launch_bounds__(kBlock) lm_head_argmax_kernel(MatvecArgs a, float* best_v, int* best_i, unsigned* ticket,
-                                                               int* result) {
+__global__ void __launch_bounds__(kBlock) lm_head_argmax_kernel(MatvecArgs a, unsigned long long* key) {
   extern __shared__ float lds[];
   const RowMax mx = matvec_body<KC, 2, kEpiStore, false>(a, blockIdx.x, gridDim.x, lds, [] {});
-  argmax_finish(mx, blockIdx.x, gridDim.x, best_v, best_i, ticket, result);
+  argmax_post(mx, key);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -50,10 +50,13 @@ struct LayerW {
 
 // The step's token and position, and its RoPE table (cos, sin of pos * inv_freq per rotary pair,
 // reference src/infer.cpp:205-208), written before each step so that a captured graph stays static.
-__global__ void set_params_kernel(StepParams* p, int token, int pos, const float* inv_freq, float* rope_cs, int half) {
+// It also zeroes the packed key the fused lm_head argmax posts to.
+__global__ void set_params_kernel(StepParams* p, int token, int pos, const float* inv_freq, float* rope_cs, int half,
+                                  unsigned long long* argmax_key) {
   if (threadIdx.x == 0) {
     p->token = token;
     p->pos = pos;
+    *argmax_key = 0ull;
   }
   fill_rope_table(inv_freq, rope_cs, half, pos);
 }
@@ -94,6 +97,7 @@ struct yhip_ctx {
   float* partial = nullptr;
   unsigned* tickets = nullptr;
   int* argmax_dev = nullptr;
+  unsigned long long* argmax_key = nullptr;  // packed (logit, index) of the fused lm_head argmax
   StepParams* params = nullptr;
   float* inv_freq = nullptr;  // [head_dim / 2]
   float* rope_cs = nullptr;   // [head_dim], refreshed every step
@@ -425,18 +429,19 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     const int blocks = std::max(1, std::min((a.groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * default_bpc(a.K)));
     const size_t lds = (16 + (size_t)a.K) * sizeof(float);
     if (a.K == 4096)
-      hipLaunchKernelGGL(lm_head_argmax_kernel<8>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->best_v, ctx->best_i,
-                         ctx->sync + kSyncArgmax, ctx->argmax_dev);
+      hipLaunchKernelGGL(lm_head_argmax_kernel<8>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     else
-      hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->best_v, ctx->best_i,
-                         ctx->sync + kSyncArgmax, ctx->argmax_dev);
+      hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     HIP_TRY(ctx, hipGetLastError());
   }
-  if (mode == 1)
+  if (mode == 1) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
-  else
+  } else if (Rc == 2) {  // the packed key, decoded on the host (argmax_host[2..3])
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 2, ctx->argmax_key, 8, hipMemcpyDeviceToHost, s));
+  } else {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, s));
+  }
   return YHIP_OK;
 }
 
@@ -584,7 +589,7 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   if (ctx->use_flow) return launch_flow_step(ctx, token, pos, mode);
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->params, token, pos,
-                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2);
+                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key);
   HIP_TRY(ctx, hipGetLastError());
   if (!ctx->use_graph) return enqueue_step(ctx, mode);
   if (!ctx->graph[mode]) {
@@ -909,7 +914,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   };
   const size_t a_x = atake(dim * 4), a_q = atake(qd * 4), a_att = atake(qd * 4), a_hb = atake(hid * 4),
                a_lg = atake(V * 4), a_part = atake((size_t)c.n_heads * 64 * (c.head_dim + 2) * 4),
-               a_tk = atake(64 * 4), a_am = atake(64), a_par = atake(sizeof(StepParams)),
+               a_tk = atake(64 * 4), a_am = atake(64), a_key = atake(64), a_par = atake(sizeof(StepParams)),
                a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
                a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
                a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
@@ -924,6 +929,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->partial = (float*)(ctx->abase + a_part);
   ctx->tickets = (unsigned*)(ctx->abase + a_tk);
   ctx->argmax_dev = (int*)(ctx->abase + a_am);
+  ctx->argmax_key = (unsigned long long*)(ctx->abase + a_key);
   ctx->params = (StepParams*)(ctx->abase + a_par);
   ctx->inv_freq = (float*)(ctx->abase + a_if);
   ctx->rope_cs = (float*)(ctx->abase + a_cs);
@@ -1108,7 +1114,13 @@ extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   collect_stats(ctx);
   if (int rc = check_flow_status(ctx)) return rc;
-  *next_token = *ctx->argmax_host;
+  if (!ctx->use_flow && ctx->c.vocab_size % 2 == 0) {  // the fused lm_head's packed key (argmax_key)
+    unsigned long long key;
+    memcpy(&key, ctx->argmax_host + 2, sizeof(key));
+    *next_token = key == 0 ? 0 : (int)~(unsigned)(key & 0xffffffffull);
+  } else {
+    *next_token = *ctx->argmax_host;
+  }
   return YHIP_OK;
 }
 
