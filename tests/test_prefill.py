@@ -65,6 +65,46 @@ def test_gemm_swiglu(M, N, K, gemm_variant):
     assert npref.rel_l2(got, want) < 2e-3  # fp16 output
 
 
+@pytest.mark.parametrize("ksplit", [2, 4, 8])
+@pytest.mark.parametrize("M,N,K", [(37, 192, 1024), (128, 256, 4096), (200, 128, 512)])
+def test_gemm_split_k(M, N, K, ksplit):
+    # K split over workgroups: fp32 partials summed in split order by the reduce kernel, which then
+    # applies the epilogue (store, residual add, SwiGLU).
+    H = hip()
+    rng = np.random.default_rng(M + N + K + ksplit)
+    a = f16(rng.standard_normal((M, K)))
+    b = f16(rng.standard_normal((N, K)) * 0.05)
+    b3 = f16(rng.standard_normal((N, K)) * 0.05)
+    A = h2f(a).astype(np.float64)
+    want = A @ h2f(b).astype(np.float64).T
+    u = A @ h2f(b3).astype(np.float64).T
+    c0 = rng.standard_normal((M, N)).astype(np.float32)
+    try:
+        H.set_gemm_stages(2, 64, 128)
+        H.set_gemm_ksplit(ksplit)
+        assert npref.rel_l2(H.gemm(a, b, mode=0), want) < 1e-6
+        assert npref.rel_l2(H.gemm(a, b, mode=1, c=c0), c0 + want) < 1e-6
+        got = h2f(H.gemm(a, b, mode=2, b3=b3))
+        assert npref.rel_l2(got, want / (1 + np.exp(-want)) * u) < 2e-3  # fp16 output
+    finally:
+        H.set_gemm_ksplit(0)
+        H.set_gemm_stages(-1)
+
+
+def test_gemm_split_k_must_divide_the_k_steps():
+    H = hip()
+    a = f16(np.ones((64, 192)))
+    b = f16(np.ones((64, 192)))
+    try:
+        H.set_gemm_stages(2, 64, 128)
+        H.set_gemm_ksplit(2)  # 192 / 64 = 3 k-steps
+        with pytest.raises(H.HipError):
+            H.gemm(a, b, mode=0)
+    finally:
+        H.set_gemm_ksplit(0)
+        H.set_gemm_stages(-1)
+
+
 def _sequential(om, toks, start=0):
     for i, t in enumerate(toks):
         lo = om.forward(int(t), start + i, 1 if i == len(toks) - 1 else 0)

@@ -52,6 +52,12 @@ struct GemmArgs {
   long ldh;
   int M, N, K;
   int act;  // SwiGLU: 1 silu, 0 gelu
+  // Split-K (LDS-pipeline kernel): ksplit > 1 workgroups share an output tile, each over K / ksplit,
+  // and store fp32 partials to P ([ksplit][M][N], SwiGLU [ksplit][M][2][N]: W1 then W3 sums);
+  // gemm_splitk_reduce sums them in split order and applies the epilogue.
+  float* P;
+  long p_floats;  // capacity of P
+  int ksplit;     // 0 or 1: no split
 };
 
 constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
@@ -188,6 +194,17 @@ __device__ __forceinline__ bool gemm_tile(int mt, int nt, int& tm, int& tn) {
   return true;
 }
 
+// The same order over (tile, K split) units: tiles M-fastest, then the splits of the whole tile grid.
+__device__ __forceinline__ bool gemm_unit(int mt, int nt, int ks, int& tm, int& tn, int& split) {
+  const int units = mt * nt * ks, per = (units + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= units) return false;
+  tm = t % mt;
+  tn = (t / mt) % nt;
+  split = t / (mt * nt);
+  return true;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {  // s_waitcnt vmcnt(N), expcnt and lgkmcnt unconstrained
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -218,9 +235,11 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   constexpr int NC = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;  // output columns per tile
-  int tm, tn;
-  if (!gemm_tile((g.M + BM - 1) / BM, (g.N + NC - 1) / NC, tm, tn)) return;
+  const int ks = g.ksplit > 1 ? g.ksplit : 1;
+  int tm, tn, split;
+  if (!gemm_unit((g.M + BM - 1) / BM, (g.N + NC - 1) / NC, ks, tm, tn, split)) return;
   const int m0 = tm * BM, n0 = tn * NC;
+  const int kspan = g.K / ks, kbeg = split * kspan;  // this workgroup's K range (a multiple of BK)
   auto swz = [](int r) { return (r / RPW) % CPR; };
 
   // wave w fills the 1 KB pieces w, w + NW, ... of each operand tile
@@ -230,7 +249,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
   for (int j = 0; j < IA; ++j) {
     const int r = RPI * (wave + NW * j) + lane / CPR;
     const int c = (lane % CPR) ^ swz(r);  // the global k-chunk this lane's LDS slot holds
-    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * c;
+    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + kbeg + 8 * c;
   }
 #pragma unroll
   for (int j = 0; j < IB; ++j) {
@@ -239,9 +258,9 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
     if constexpr (EPI == kGemmSwiGLU) {
       const int col = n0 + (r >> 6) * 32 + (r & 31);
       const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
-      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + kbeg + 8 * c;
     } else {
-      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + kbeg + 8 * c;
     }
   }
   auto issue = [&](int kt) {
@@ -268,7 +287,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  const int nk = g.K / BK;
+  const int nk = kspan / BK;
 #pragma unroll
   for (int kt = 0; kt < S - 1; ++kt)
     if (kt < nk) issue(kt);
@@ -297,6 +316,31 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
     }
   }
 
+  if (ks > 1) {  // raw partial sums; gemm_splitk_reduce applies the epilogue
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + acc_row(r, lane);
+        if (m >= g.M) continue;
+        if constexpr (EPI == kGemmSwiGLU) {
+          const int j = n0 + wn * 32 + (lane & 31);
+          if (j < g.N) {
+            float* pp = g.P + ((long)split * g.M + m) * (2L * g.N) + j;
+            pp[0] = acc[i][0][r];
+            pp[g.N] = acc[i][1][r];
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n < g.N) g.P[((long)split * g.M + m) * g.N + n] = acc[i][j][r];
+          }
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -320,6 +364,32 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
           else *cp = acc[i][j][r];
         }
       }
+    }
+  }
+}
+
+// Sum of the split-K partials in split order (deterministic), then the GEMM's epilogue: C = sum,
+// C += sum, or H = fp16(act(sum W1) * sum W3). One thread per output element.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs g) {
+  const long total = (long)g.M * g.N;
+  for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (long)gridDim.x * blockDim.x) {
+    const int m = (int)(e / g.N), n = (int)(e % g.N);
+    if constexpr (EPI == kGemmSwiGLU) {
+      float a1 = 0.f, a3 = 0.f;
+      for (int sp = 0; sp < g.ksplit; ++sp) {
+        const float* pp = g.P + ((long)sp * g.M + m) * (2L * g.N) + n;
+        a1 += pp[0];
+        a3 += pp[g.N];
+      }
+      const float h = g.act == 1 ? silu(a1) : gelu(a1);
+      g.H[(long)m * g.ldh + n] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+    } else {
+      float v = 0.f;
+      for (int sp = 0; sp < g.ksplit; ++sp) v += g.P[((long)sp * g.M + m) * g.N + n];
+      float* cp = g.C + (long)m * g.ldc + n;
+      if constexpr (EPI == kGemmResid) *cp += v;
+      else *cp = v;
     }
   }
 }

@@ -34,6 +34,7 @@ int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-
 int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
 bool g_gemm_auto = true;  // prefill GEMM variant chosen per shape (cleared by forcing one)
+int g_gemm_ksplit = 0;    // prefill GEMM K splits on the LDS-pipeline kernel (0 = chosen per shape)
 int g_upload_stage_mb = 64;  // weight upload: pinned staging chunk in MB (0 = direct pageable copies)
 int g_upload_threads = 8;    // weight upload: host threads filling a staging chunk
 
@@ -137,6 +138,8 @@ struct yhip_ctx {
   uint16_t* pf_Q = nullptr;  // [n][q]
   uint16_t* pf_A = nullptr;  // [n][q]
   int* pf_tok = nullptr;     // [n]
+  float* pf_P = nullptr;     // split-K partials of the prefill GEMMs
+  long pf_Pn = 0;            // its capacity in floats
 
   // device timing of synchronised steps ("stats" option)
   bool stats = false;
@@ -204,6 +207,12 @@ void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
     else launch_mv<0, 2, EPI>(a, blocks, s);
   }
 }
+
+int device_cus();  // compute units of the current device (defined with the test hooks)
+
+// Split-K workspace bound: tiles x splits never exceed one workgroup per CU, and a 128 x 128 tile
+// (or 128 x 64 of W1 and of W3) holds 16384 partial sums.
+long splitk_ws_floats(int cus) { return (long)cus * 16384; }
 
 // Chooses the instantiation for row length K, rows-per-group R and epilogue kind.
 int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s, int bpc = 0) {
@@ -657,14 +666,43 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   const int ncols = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;
   if (g.K % 64 != 0) bk = 32;  // a 64-deep k-step needs K % 64 == 0
   if (bk != 64) bm = 128;
-  const dim3 grid = tiles8(bm, ncols);
+  // Split-K when the output has too few tiles to fill the GPU (short prompts): the largest power of
+  // two that keeps tiles x splits within one workgroup per CU, divides the k-steps and leaves each
+  // split at least two of them; the partials go to the caller's workspace (none: no split).
+  GemmArgs ga = g;
+  ga.ksplit = 1;
+  const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + ncols - 1) / ncols);
+  const long part_floats = (long)g.M * g.N * (EPI == kGemmSwiGLU ? 2 : 1);  // per split
+  const int ksteps = g.K / bk;
+  if (stages >= 2 && g.P) {
+    if (g_gemm_ksplit > 0) {
+      ga.ksplit = g_gemm_ksplit;
+      if (ksteps % ga.ksplit != 0) return fail(ctx, YHIP_EINVAL, "gemm_ksplit must divide the k-steps");
+    } else {
+      const long cus = ctx ? ctx->num_cus : device_cus();
+      while (tiles * ga.ksplit * 2 <= cus && ksteps % (ga.ksplit * 2) == 0 && ksteps / (ga.ksplit * 2) >= 2 &&
+             part_floats * ga.ksplit * 2 <= g.p_floats)
+        ga.ksplit *= 2;
+    }
+    if (ga.ksplit > 1 && part_floats * ga.ksplit > g.p_floats)
+      return fail(ctx, YHIP_EINVAL, "gemm: split-K workspace too small");
+  }
+  const dim3 grid(8 * (unsigned)((tiles * ga.ksplit + 7) / 8));
   switch (stages * 10000 + bk * 1000 / 8 + bm) {
-    case 4 * 10000 + 4000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 4, 32, 128>), grid, dim3(256), 0, s, g); break;
-    case 2 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 128>), grid, dim3(256), 0, s, g); break;
-    case 3 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 128>), grid, dim3(256), 0, s, g); break;
-    case 2 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 256>), grid, dim3(512), 0, s, g); break;
-    case 3 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 256>), grid, dim3(512), 0, s, g); break;
-    default: hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, g); break;
+    case 4 * 10000 + 4000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 4, 32, 128>), grid, dim3(256), 0, s, ga); break;
+    case 2 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 128>), grid, dim3(256), 0, s, ga); break;
+    case 3 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 128>), grid, dim3(256), 0, s, ga); break;
+    case 2 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 256>), grid, dim3(512), 0, s, ga); break;
+    case 3 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 256>), grid, dim3(512), 0, s, ga); break;
+    default:
+      ga.ksplit = 1;
+      hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, ga);
+      break;
+  }
+  if (ga.ksplit > 1) {
+    const long total = (long)g.M * g.N;
+    hipLaunchKernelGGL(gemm_splitk_reduce<EPI>, dim3((unsigned)std::min<long>(4096, (total + 255) / 256)), dim3(256), 0,
+                       s, ga);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
@@ -706,7 +744,8 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
     return o;
   };
   const size_t oX = take(N * c.dim * 4), oXn = take(N * c.dim * 2), oH = take(N * c.hidden_dim * 2),
-               oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oA = take(N * qd * 2), oT = take(N * 4);
+               oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oA = take(N * qd * 2), oT = take(N * 4),
+               oP = take((size_t)splitk_ws_floats(ctx->num_cus) * 4);
   if (ctx->pf_base) hipFree(ctx->pf_base);
   ctx->pf_base = nullptr;
   ctx->pf_cap = 0;
@@ -718,6 +757,8 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
   ctx->pf_Q = (uint16_t*)(ctx->pf_base + oQ);
   ctx->pf_A = (uint16_t*)(ctx->pf_base + oA);
   ctx->pf_tok = (int*)(ctx->pf_base + oT);
+  ctx->pf_P = (float*)(ctx->pf_base + oP);
+  ctx->pf_Pn = splitk_ws_floats(ctx->num_cus);
   ctx->pf_cap = n;
   return YHIP_OK;
 }
@@ -746,6 +787,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.M = n;
     g.N = qd + 2 * kvd;
     g.K = c.dim;
+    g.P = ctx->pf_P;
+    g.p_floats = ctx->pf_Pn;
     if ((rc = launch_gemm<kGemmStore>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(qkv_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_C, qd + 2 * kvd, qd, kvd,
                        c.head_dim, c.qkv_clip, (const float*)ctx->inv_freq, start, c.max_seq_len, ctx->pf_Q,
@@ -779,6 +822,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.M = n;
     g.N = c.dim;
     g.K = qd;
+    g.P = ctx->pf_P;
+    g.p_floats = ctx->pf_Pn;
     if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_X,
                        (const float*)L.rms_ffn, c.norm_eps, c.dim, ctx->pf_Xn);
@@ -794,6 +839,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.N = c.hidden_dim;
     g.K = c.dim;
     g.act = c.act;
+    g.P = ctx->pf_P;
+    g.p_floats = ctx->pf_Pn;
     if ((rc = launch_gemm<kGemmSwiGLU>(ctx, g, s))) return rc;
     memset(&g, 0, sizeof(g));
     g.A = ctx->pf_H;
@@ -805,6 +852,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.M = n;
     g.N = c.dim;
     g.K = c.hidden_dim;
+    g.P = ctx->pf_P;
+    g.p_floats = ctx->pf_Pn;
     if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
   }
   HIP_TRY(ctx, hipGetLastError());
@@ -1193,6 +1242,11 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       g_gemm_bk = value;
       return YHIP_OK;
     }
+    if (!strcmp(key, "gemm_ksplit")) {  // 0: chosen per shape; n >= 1: forced where the kernel allows
+      if (value < 0 || value > 64) return fail(nullptr, YHIP_EINVAL, "gemm_ksplit must be in [0, 64]");
+      g_gemm_ksplit = value;
+      return YHIP_OK;
+    }
     if (!strcmp(key, "upload_stage_mb")) {
       if (value < 0 || value > 1024) return fail(nullptr, YHIP_EINVAL, "upload_stage_mb must be in [0, 1024]");
       g_upload_stage_mb = value;
@@ -1518,8 +1572,11 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   const uint16_t* db3 = mode == kGemmSwiGLU ? d.alloc<uint16_t>((size_t)N * K, b3) : nullptr;
   float* dc = mode != kGemmSwiGLU ? d.alloc<float>((size_t)M * N, mode == kGemmResid ? c : nullptr) : nullptr;
   uint16_t* dh = mode == kGemmSwiGLU ? d.alloc<uint16_t>((size_t)M * N) : nullptr;
+  const long pf = splitk_ws_floats(device_cus());
+  float* dp = d.alloc<float>((size_t)pf);
   TRY_ALLOC(da);
   TRY_ALLOC(db);
+  TRY_ALLOC(dp);
   if (mode == kGemmSwiGLU) {
     TRY_ALLOC(db3);
     TRY_ALLOC(dh);
@@ -1541,6 +1598,8 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   g.N = N;
   g.K = K;
   g.act = act;
+  g.P = dp;
+  g.p_floats = pf;
   int rc = mode == kGemmStore ? launch_gemm<kGemmStore>(nullptr, g, nullptr)
            : mode == kGemmResid ? launch_gemm<kGemmResid>(nullptr, g, nullptr)
                                 : launch_gemm<kGemmSwiGLU>(nullptr, g, nullptr);
@@ -1768,11 +1827,14 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   uint16_t* db3 = d.alloc<uint16_t>((size_t)N * K);
   float* dc = d.alloc<float>((size_t)M * N);
   uint16_t* dh = d.alloc<uint16_t>((size_t)M * N);
+  const long pf = splitk_ws_floats(device_cus());
+  float* dp = d.alloc<float>((size_t)pf);
   TRY_ALLOC(da);
   TRY_ALLOC(db);
   TRY_ALLOC(db3);
   TRY_ALLOC(dc);
   TRY_ALLOC(dh);
+  TRY_ALLOC(dp);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, da, (size_t)M * K, 11u);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db, (size_t)N * K, 12u);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db3, (size_t)N * K, 13u);
@@ -1793,6 +1855,8 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   g.N = N;
   g.K = K;
   g.act = 1;
+  g.P = dp;
+  g.p_floats = pf;
   hipStream_t s;
   HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   auto launch = [&] {

@@ -242,6 +242,12 @@ def set_gemm_stages(n, bk=32, bm=128):
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
 
 
+def set_gemm_ksplit(n=0):
+    """Prefill GEMM K splits on the LDS-pipeline kernel: 0 = chosen per shape (split when the output
+    has too few tiles to fill the GPU), n >= 1 = forced (must divide the k-steps)."""
+    _check(lib().yhip_set_option(None, b"gemm_ksplit", int(n)))
+
+
 def set_upload(stage_mb=64, threads=8):
     """Weight upload: pinned staging chunk size in MB (0 = direct copies from pageable memory) and
     the host threads that fill a chunk."""
