@@ -118,6 +118,13 @@ ATTN_CASES = [
     (32, 4, 1, 1024, 1000, 64),   # many slices
     (128, 32, 8, 4096, 256, 0),
     (128, 32, 8, 4096, 257, 0),
+    # waves with no tile in their slice skip their loads: one tile, one key past it, seven tiles
+    # and a key, a last slice holding a single key, a last slice shorter than one tile
+    (128, 32, 8, 4096, 32, 0),
+    (128, 32, 8, 4096, 33, 0),
+    (128, 32, 8, 4096, 225, 0),
+    (128, 32, 8, 4096, 513, 2),
+    (128, 32, 8, 4096, 1030, 4),
 ]
 
 
