@@ -415,7 +415,62 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       for (int i = threadIdx.x; i < a.K; i += kBlock) st_act<COH>(a.emb_out + i, (float)__builtin_bit_cast(f16, x16[i]));
   }
 
-  if constexpr (KC > 0) {
+  if constexpr (KC > 0 && !COH) {
+    // Two register buffers, one group in flight: group i + 1's loads are issued as soon as group
+    // i's have landed and before group i's dot products, reduction and epilogue, so a wave's
+    // arithmetic overlaps its next memory round trip. (Two groups in flight per wave measured
+    // slower: the memory queues saturate.) The loop is unrolled by two with a single exit and a
+    // peeled tail so that every load inside it is unconditional and the compiler's wait for the
+    // older buffer stays "at most one group outstanding".
+    const int w_id = __builtin_amdgcn_readfirstlane(wave);
+    const int p0 = blk * kWavesPerBlock + w_id;
+    const int n = p0 < a.groups ? (a.groups - 1 - p0) / wave_stride + 1 : 0;  // this wave's groups
+    u32x4 wa[R][KC], wb[R][KC];
+    float prea[R], preb[R];
+    auto issue = [&](u32x4 (&wv)[R][KC], float (&pre)[R], int i) {
+      const uint16_t* rows[R];
+      group_rows<R>(a, p0 + i * wave_stride, rows);
+      load_group<KC, R>(wv, rows, lane);
+      epilogue_prefetch<R, EPI, COH>(a, p0 + i * wave_stride, pre);
+    };
+    if (n > 0) issue(wa, prea, 0);
+    wait();
+    const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
+    stage_input<KC / 2, COH>(a, xs, red, pos, x16);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+    auto use = [&](const u32x4 (&wv)[R][KC], const float (&pre)[R], int i) {
+      const int pg = p0 + i * wave_stride;
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int u = 0; u < KC; ++u) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8(wv[r][u], xs + 8 * (lane + kWave * u), acc[r]);
+        if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+      epilogue<R, EPI, COH>(a, pg, acc, pre, pos, xs + a.K, lane == 0);
+      track_rows<R, EPI>(a, pg, acc, mx);
+    };
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      issue(wb, preb, i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wa, prea, i);
+      issue(wa, prea, i + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wb, preb, i + 1);
+    }
+    if (i + 2 == n) {
+      issue(wb, preb, i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wa, prea, i);
+      use(wb, preb, i + 1);
+    } else if (i + 1 == n) {
+      use(wa, prea, i);
+    }
+  } else if constexpr (KC > 0) {
     // One register buffer: the first group's loads are in flight while the workgroup stages x
     // (every wave takes part in the staging barrier); each later group is loaded at the end of
     // the previous iteration, after its registers are dead.
