@@ -114,6 +114,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode budget (0 = skip)")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--attn-min-slice", type=int, default=0, help="override the attention slice floor")
+    ap.add_argument("--option", action="append", default=[], metavar="KEY=VALUE",
+                    help="a context option of the HIP library (yhip_set_option), repeatable")
     ap.add_argument("--profile-kernel", choices=["w13", "copy"], default=None,
                     help="run only that kernel (for hardware-counter passes) and exit")
     args = ap.parse_args()
@@ -151,6 +153,9 @@ def main():
     opts = [(b"single_launch", int(args.path == "single")), (b"graph", int(args.path == "graph"))]
     if args.attn_min_slice:
         opts.append((b"attn_min_slice", args.attn_min_slice))
+    for kv in args.option:
+        key, _, val = kv.partition("=")
+        opts.append((key.encode(), int(val)))
     for key, val in opts:
         if hip.lib().yhip_set_option(ctxp, key, val) != 0:
             raise RuntimeError(hip.lib().yhip_last_error(ctxp).decode())
@@ -302,6 +307,8 @@ def main():
         "device_us_per_step": round(step_us, 2),
         "cpu_baseline": cpu,
     }
+    if args.option:
+        out["config"]["options"] = dict(kv.partition("=")[::2] for kv in args.option)
     if prefill is not None:
         out["prefill"] = prefill
     print(json.dumps(out), flush=True)

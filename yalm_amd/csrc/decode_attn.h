@@ -44,8 +44,6 @@ struct KvFrag {
 // Buffer loads: the K/V regions of the kv head are addressed by a descriptor in scalar registers,
 // so each load takes one 32-bit lane offset plus a wave-uniform scalar offset (the dims / k-step
 // strides) instead of a 64-bit address per load; reads past the region return zero.
-constexpr int kBufferConfig = 0x00020000;  // raw buffer descriptor word 3 on gfx9-family GPUs
-
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
 }

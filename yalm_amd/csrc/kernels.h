@@ -132,6 +132,15 @@ __device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+constexpr int kBufferConfig = 0x00020000;  // raw buffer descriptor word 3 on gfx9-family GPUs
+constexpr int kCpolSc1 = 16;               // cache-policy operand: sc1, the agent-scope coherent load
+
+// 16 bytes that another workgroup of the same launch wrote with store_shared: one dwordx4 load
+// with the agent-coherence bit (the access load_shared makes per float).
+__device__ __forceinline__ f32x4 load_shared4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
+}
+
 // Activation accesses: plain, or agent-coherent (COH) when a later workgroup of the same launch
 // consumes the value.
 template <bool COH>
@@ -310,6 +319,11 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
       const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
 #pragma unroll
       for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
+    } else if (!x16) {
+      const __amdgpu_buffer_rsrc_t xr =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, a.K * (int)sizeof(float), kBufferConfig);
+#pragma unroll
+      for (int k = 0; k < NPT; ++k) xv[k] = load_shared4(xr, 16 * (threadIdx.x + kBlock * k));
     } else {
 #pragma unroll
       for (int k = 0; k < NPT; ++k)
