@@ -208,6 +208,25 @@ __device__ __forceinline__ void load_group(u32x4 (&wv)[R][KC > 0 ? KC : 1], cons
       wv[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[r]) + lane + kWave * u);
 }
 
+// The same loads when the row pointers are wave-uniform (scalar registers): one buffer descriptor
+// per row in scalar registers and one shared lane offset, so no per-lane 64-bit addresses are
+// formed. Only for call sites whose group index is uniform by construction (readfirstlane).
+constexpr int kCpolNt = 2;  // cache-policy operand: nt (streaming)
+// valid == false: the descriptors cover no bytes and every load returns zero without a memory
+// access (the loads are still issued, so the caller's wait counts do not depend on a branch).
+template <int KC, int R>
+__device__ __forceinline__ void load_group_uniform(u32x4 (&wv)[R][KC], const uint16_t* const (&rows)[R], int lane,
+                                                   bool valid = true) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(rows[r]), 0, valid ? KC * 1024 : 0, kBufferConfig);
+#pragma unroll
+    for (int u = 0; u < KC; ++u)
+      wv[r][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, u * 1024, kCpolNt));
+  }
+}
+
 template <int R>
 __device__ __forceinline__ void group_rows(const MatvecArgs& a, int p, const uint16_t* (&rows)[R]) {
 #pragma unroll
@@ -390,6 +409,83 @@ __device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, floa
   __syncthreads();
 }
 
+// The same staging in two halves, for the pipelined matvec (K == 1024*NPT, plain accesses):
+// stage_load issues every global read the staging needs (x or the raw fp16 embedding row, the
+// gains, the RoPE table) into registers; the caller then issues its first weight loads, and
+// stage_store normalises, fills LDS and synchronises the workgroup. Loads complete in issue order,
+// so consuming reads issued before the weights does not wait for the weights, and the first row
+// group stays in flight across the staging barrier. GAIN / EMB: whether the call site can have an
+// RMS gain / an embedding-row input (the residual epilogue has neither), which keeps registers for
+// the other cases out of the kernel.
+// Which inputs an epilogue kind's call sites can have (the host rejects the others).
+template <EpiKind EPI>
+constexpr bool kEpiGain = EPI != kEpiResidual;
+template <EpiKind EPI>
+constexpr bool kEpiEmb = EPI == kEpiQkvRope || EPI == kEpiStore;
+
+template <int NPT, bool GAIN, bool EMB>
+struct StagedInput {
+  f32x4 xv[NPT], gv[GAIN ? NPT : 1];
+  unsigned long long hv[EMB ? NPT : 1];  // four fp16 of the embedding row
+  float rc;
+};
+
+template <int NPT, bool GAIN, bool EMB>
+__device__ __forceinline__ void stage_load(const MatvecArgs& a, StagedInput<NPT, GAIN, EMB>& st, const uint16_t* x16) {
+  if (EMB && x16) {
+    const unsigned long long* h4 = reinterpret_cast<const unsigned long long*>(x16);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) st.hv[k] = h4[threadIdx.x + kBlock * k];
+  } else {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) st.xv[k] = x4[threadIdx.x + kBlock * k];
+  }
+  if (GAIN && a.gain) {
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) st.gv[k] = g4[threadIdx.x + kBlock * k];
+  }
+  st.rc = a.rope_cs && (int)threadIdx.x < a.head_dim ? a.rope_cs[threadIdx.x] : 0.f;
+}
+
+template <int NPT, bool GAIN, bool EMB>
+__device__ __forceinline__ void stage_store(const MatvecArgs& a, StagedInput<NPT, GAIN, EMB>& st, float* xs, float* red,
+                                            int pos, const uint16_t* x16) {
+  // the RoPE table comes precomputed (rope_cs); the per-launch cos/sin form (inv_freq) belongs to
+  // the single-launch path, which stages through stage_input
+  if (a.rope_cs && (int)threadIdx.x < a.head_dim) xs[a.K + threadIdx.x] = st.rc;
+  if (EMB && x16) {
+#pragma unroll
+    for (int k = 0; k < NPT; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        st.xv[k][e] = (float)__builtin_bit_cast(f16, (uint16_t)(st.hv[k] >> (16 * e)));
+  }
+  f32x4* o4 = reinterpret_cast<f32x4*>(xs);
+  if (GAIN && a.gain) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k)
+      ss += st.xv[k][0] * st.xv[k][0] + st.xv[k][1] * st.xv[k][1] + st.xv[k][2] * st.xv[k][2] + st.xv[k][3] * st.xv[k][3];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+      f32x4 o;
+      o[0] = st.xv[k][0] * inv * st.gv[k][0];
+      o[1] = st.xv[k][1] * inv * st.gv[k][1];
+      o[2] = st.xv[k][2] * inv * st.gv[k][2];
+      o[3] = st.xv[k][3] * inv * st.gv[k][3];
+      o4[threadIdx.x + kBlock * k] = o;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) o4[threadIdx.x + kBlock * k] = st.xv[k];
+  }
+  __syncthreads();
+}
+
 // Per-wave running maximum for the fused argmax (track_max); every lane holds the same values.
 struct RowMax {
   float v = kNegBig;
@@ -409,10 +505,9 @@ __device__ __forceinline__ void track_rows(const MatvecArgs& a, int p, const flo
 // The fused matvec over groups p = blk*4 + wave + k*(nblk*4). `wait()` runs after the first
 // group's weight loads are issued and before anything that reads activations (the single-launch
 // decode waits there for the producing phase); COH selects coherent activation accesses.
-// KC > 0: K == 512*KC, fully unrolled row streaming. KC == 0: any K % 8 == 0.
-// One register buffer of weights per wave; latency is hidden by the other resident waves and by
-// issuing the next group's loads ahead of the current group's reductions and epilogue.
-template <int KC, int R, EpiKind EPI, bool COH, class Wait>
+// KC > 0: K == 512*KC*H, fully unrolled row streaming. KC == 0: any K % 8 == 0.
+// H == 2 (R == 1 only): each row is streamed as two pieces of K/2 (see below).
+template <int KC, int R, EpiKind EPI, bool COH, int H = 1, class Wait>
 __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int nblk, float* lds, Wait wait) {
   float* red = lds;      // kWavesPerBlock floats (padded to 16)
   float* xs = lds + 16;  // K floats (+ the RoPE table)
@@ -429,7 +524,68 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       for (int i = threadIdx.x; i < a.K; i += kBlock) st_act<COH>(a.emb_out + i, (float)__builtin_bit_cast(f16, x16[i]));
   }
 
-  if constexpr (KC > 0 && !COH) {
+  static_assert(H == 1 || (H == 2 && R == 1 && KC > 0 && !COH), "two-piece rows: one row per group, unrolled");
+  if constexpr (H == 2) {
+    // Long rows (W2: 28 KB) in two pieces through the two register buffers: piece 0 of a group in
+    // wa, piece 1 in wb, so each buffer holds half a row and the pair fits the register file with
+    // room to spare (two whole-row buffers need ~250 VGPRs, and the compiler then reuses buffer
+    // registers as address temporaries, which forces a wait for the older buffer before every
+    // issue). Piece 1 is issued before piece 0 is used and the next group's piece 0 before piece 1
+    // is used; the loop has a single exit and a peeled last group, as below.
+    const int w_id = __builtin_amdgcn_readfirstlane(wave);
+    const int p0 = blk * kWavesPerBlock + w_id;
+    const int n = p0 < a.groups ? (a.groups - 1 - p0) / wave_stride + 1 : 0;  // this wave's groups
+    const int half = a.K / 2;
+    u32x4 wa[1][KC], wb[1][KC];
+    float pre[1];
+    auto issue = [&](u32x4 (&wv)[1][KC], int i, int piece, bool valid = true) {
+      const uint16_t* rows[1];
+      group_rows<1>(a, valid ? p0 + i * wave_stride : 0, rows);
+      rows[0] += piece * half;
+      load_group_uniform<KC, 1>(wv, rows, lane, valid);
+      if (piece == 1) epilogue_prefetch<1, EPI, COH>(a, p0 + i * wave_stride, pre);
+    };
+    StagedInput<KC, kEpiGain<EPI>, kEpiEmb<EPI>> st;  // K = 1024*KC -> KC float4 per thread
+    stage_load(a, st, x16);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(wa, 0, 0, n > 0);  // unconditional: a branch here would make the staging wait for it
+    wait();
+    const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
+    stage_store(a, st, xs, red, pos, x16);
+    float carry = 0.f;
+    auto use = [&](const u32x4 (&wv)[1][KC], int i, int piece) {
+      const float* xp = xs + piece * half;
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < KC; ++u) {
+        acc = dot8(wv[0][u], xp + 8 * (lane + kWave * u), acc);
+        if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+      if (piece == 0) {
+        carry = acc;
+        return;
+      }
+      float accs[1] = {wave_sum(carry + acc)};
+      const int pg = p0 + i * wave_stride;
+      epilogue<1, EPI, COH>(a, pg, accs, pre, pos, xs + a.K, lane == 0);
+      track_rows<1, EPI>(a, pg, accs, mx);
+    };
+    int i = 0;
+    for (; i + 1 < n; ++i) {
+      issue(wb, i, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wa, i, 0);
+      issue(wa, i + 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wb, i, 1);
+    }
+    if (i < n) {
+      issue(wb, i, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      use(wa, i, 0);
+      use(wb, i, 1);
+    }
+  } else if constexpr (KC > 0 && !COH) {
     // Two register buffers, one group in flight: group i + 1's loads are issued as soon as group
     // i's have landed and before group i's dot products, reduction and epilogue, so a wave's
     // arithmetic overlaps its next memory round trip. (Two groups in flight per wave measured
@@ -441,16 +597,20 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
     const int n = p0 < a.groups ? (a.groups - 1 - p0) / wave_stride + 1 : 0;  // this wave's groups
     u32x4 wa[R][KC], wb[R][KC];
     float prea[R], preb[R];
-    auto issue = [&](u32x4 (&wv)[R][KC], float (&pre)[R], int i) {
+    auto issue = [&](u32x4 (&wv)[R][KC], float (&pre)[R], int i, bool valid = true) {
       const uint16_t* rows[R];
-      group_rows<R>(a, p0 + i * wave_stride, rows);
-      load_group<KC, R>(wv, rows, lane);
-      epilogue_prefetch<R, EPI, COH>(a, p0 + i * wave_stride, pre);
+      const int g = valid ? p0 + i * wave_stride : 0;
+      group_rows<R>(a, g, rows);
+      load_group_uniform<KC, R>(wv, rows, lane, valid);
+      epilogue_prefetch<R, EPI, COH>(a, g, pre);
     };
-    if (n > 0) issue(wa, prea, 0);
+    StagedInput<KC / 2, kEpiGain<EPI>, kEpiEmb<EPI>> st;  // K = 512*KC -> KC/2 float4 per thread
+    stage_load(a, st, x16);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(wa, prea, 0, n > 0);  // unconditional: a branch here would make the staging wait for it
     wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
-    stage_input<KC / 2, COH>(a, xs, red, pos, x16);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
+    stage_store(a, st, xs, red, pos, x16);
     auto use = [&](const u32x4 (&wv)[R][KC], const float (&pre)[R], int i) {
       const int pg = p0 + i * wave_stride;
       float acc[R];
@@ -553,10 +713,10 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
   return mx;
 }
 
-template <int KC, int R, EpiKind EPI>
+template <int KC, int R, EpiKind EPI, int H = 1>
 __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
   extern __shared__ float lds[];
-  matvec_body<KC, R, EPI, false>(a, blockIdx.x, gridDim.x, lds, [] {});
+  matvec_body<KC, R, EPI, false, H>(a, blockIdx.x, gridDim.x, lds, [] {});
 }
 
 // (max, index) over the lanes of a wave, then over the waves of the workgroup; tie rule of

@@ -189,18 +189,18 @@ std::vector<float> make_inv_freq(int head_dim, int rotary_dim, float theta) {
 // for 14336-long rows (W2, whose 57 KB LDS input already limits residency).
 int default_bpc(int K) { return K >= 8192 ? 1 : 2; }
 
-template <int KC, int R, EpiKind EPI>
+template <int KC, int R, EpiKind EPI, int H = 1>
 void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
   // reduction scratch + input vector (+ the RoPE table for the QKV epilogue)
   const size_t lds = (16 + (size_t)a.K + (a.rope_cs || a.inv_freq ? (size_t)a.head_dim : 0)) * sizeof(float);
-  hipLaunchKernelGGL((matvec_kernel<KC, R, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
+  hipLaunchKernelGGL((matvec_kernel<KC, R, EPI, H>), dim3(blocks), dim3(kBlock), lds, s, a);
 }
 
 template <EpiKind EPI>
 void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
   if (R == 1) {
     if (a.K == 4096) launch_mv<8, 1, EPI>(a, blocks, s);
-    else if (a.K == 14336) launch_mv<28, 1, EPI>(a, blocks, s);
+    else if (a.K == 14336) launch_mv<14, 1, EPI, 2>(a, blocks, s);  // two 7168-long pieces per row
     else launch_mv<0, 1, EPI>(a, blocks, s);
   } else {
     if (a.K == 4096) launch_mv<8, 2, EPI>(a, blocks, s);
@@ -219,6 +219,9 @@ int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hip
   if (a.K % 8 != 0 || (16 + (size_t)a.K + 128) * sizeof(float) > 65536)
     return fail(ctx, YHIP_EINVAL, "matvec: row length must be a multiple of 8 and at most 16240");
   if (R != 1 && R != 2) return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
+  if (kind == kEpiResidual && (a.gain || a.emb)) return fail(ctx, YHIP_EINVAL, "matvec: the residual epilogue takes no gain or embedding input");
+  if (kind == kEpiSwiGLU && a.emb) return fail(ctx, YHIP_EINVAL, "matvec: the SwiGLU epilogue takes no embedding input");
+  if (a.inv_freq && !a.rope_cs) return fail(ctx, YHIP_EINVAL, "matvec: the RoPE epilogue takes a precomputed table (rope_cs)");
   if (bpc <= 0) bpc = default_bpc(a.K);
   int blocks = (a.groups + kWavesPerBlock - 1) / kWavesPerBlock;
   blocks = std::max(1, std::min(blocks, num_cus * bpc));
