@@ -107,6 +107,8 @@ struct yhip_ctx {
   int* argmax_host = nullptr;    // pinned
 
   bool use_graph = true;
+  // workgroups per CU of the decode matvecs: QKV, O, W1/W3, W2, lm_head (0: default_bpc)
+  int mv_bpc[5] = {0, 0, 0, 0, 0};
   int attn_splits = 32;
   int attn_min_slice = 0;  // 0: the kernel's own default (attn_min_slice_for)
   // weight prefetch on the attention launch: O (prefetch_o), the first prefetch_w13_mb MB of each
@@ -185,9 +187,17 @@ std::vector<float> make_inv_freq(int head_dim, int rotary_dim, float theta) {
 }
 
 // ---- matvec launch -------------------------------------------------------------------------
-// Workgroups per CU: measured best on MI355X is 2 for 4096-long rows (QKV, O, W1/W3, lm_head) and 1
-// for 14336-long rows (W2, whose 57 KB LDS input already limits residency).
-int default_bpc(int K) { return K >= 8192 ? 1 : 2; }
+// Workgroups per CU, measured best on MI355X in the decode step: 2 for 4096-long rows (QKV, O,
+// lm_head), 1 for 14336-long rows (W2, whose 57 KB LDS input already limits residency), and 12 for
+// W1/W3 + SwiGLU. With 149 VGPRs three of its workgroups fit a CU, so a 12-per-CU grid (about one
+// row pair per wave) leaves most workgroups queued, and the hardware dispatcher hands each CU a new
+// one as soon as one finishes: the CUs whose loads are served late simply take fewer. That
+// balances the launch's tail (2.621 -> 2.570 ms per token); 2-8 per CU are in between, 14 and 16
+// no better.
+int default_bpc(int K, int kind = -1) {
+  if (kind == kEpiSwiGLU) return 12;
+  return K >= 8192 ? 1 : 2;
+}
 
 template <int KC, int R, EpiKind EPI, int H = 1>
 void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
@@ -222,7 +232,7 @@ int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hip
   if (kind == kEpiResidual && (a.gain || a.emb)) return fail(ctx, YHIP_EINVAL, "matvec: the residual epilogue takes no gain or embedding input");
   if (kind == kEpiSwiGLU && a.emb) return fail(ctx, YHIP_EINVAL, "matvec: the SwiGLU epilogue takes no embedding input");
   if (a.inv_freq && !a.rope_cs) return fail(ctx, YHIP_EINVAL, "matvec: the RoPE epilogue takes a precomputed table (rope_cs)");
-  if (bpc <= 0) bpc = default_bpc(a.K);
+  if (bpc <= 0) bpc = default_bpc(a.K, kind);
   int blocks = (a.groups + kWavesPerBlock - 1) / kWavesPerBlock;
   blocks = std::max(1, std::min(blocks, num_cus * bpc));
   switch (kind) {
@@ -348,7 +358,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
       a.emb = ctx->embed;
       a.emb_out = ctx->x;
     }
-    if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s))) return rc;
+    if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
     // 2. attention
     AttnArgs t;
     t.q = ctx->q;
@@ -389,7 +399,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.K = qd;
     a.x = ctx->att;
     a.out = ctx->x;
-    if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s))) return rc;
+    if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s, ctx->mv_bpc[1]))) return rc;
     // 4. rmsnorm + W1/W3 + SwiGLU
     a = mv_base();
     a.w0 = L.w1;
@@ -402,7 +412,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.eps = c.norm_eps;
     a.out = ctx->hb;
     a.act = c.act;
-    if ((rc = launch_matvec(ctx, a, kEpiSwiGLU, 2, ctx->num_cus, s))) return rc;
+    if ((rc = launch_matvec(ctx, a, kEpiSwiGLU, 2, ctx->num_cus, s, ctx->mv_bpc[2]))) return rc;
     // 5. W2 + residual
     a = mv_base();
     a.w0 = L.w2;
@@ -412,7 +422,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.K = c.hidden_dim;
     a.x = ctx->hb;
     a.out = ctx->x;
-    if ((rc = launch_matvec(ctx, a, kEpiResidual, 1, ctx->num_cus, s))) return rc;
+    if ((rc = launch_matvec(ctx, a, kEpiResidual, 1, ctx->num_cus, s, ctx->mv_bpc[3]))) return rc;
   }
   if (mode == 0) return YHIP_OK;
   const int Rc = (c.vocab_size % 2 == 0) ? 2 : 1;
@@ -432,13 +442,14 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     a.emb_out = ctx->x;
   }
   if (mode == 1 || Rc != 2) {
-    if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s)) return rc;
+    if (int rc = launch_matvec(ctx, a, kEpiStore, Rc, ctx->num_cus, s, ctx->mv_bpc[4])) return rc;
     if (mode == 2)
       hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, (const float*)ctx->logits, c.vocab_size,
                          ctx->argmax_dev);
   } else {  // lm_head with the argmax fused in
     a.track_max = 1;
-    const int blocks = std::max(1, std::min((a.groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * default_bpc(a.K)));
+    const int bpc = ctx->mv_bpc[4] > 0 ? ctx->mv_bpc[4] : default_bpc(a.K);
+    const int blocks = std::max(1, std::min((a.groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * bpc));
     const size_t lds = (16 + (size_t)a.K) * sizeof(float);
     if (a.K == 4096)
       hipLaunchKernelGGL(lm_head_argmax_kernel<8>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
@@ -1300,6 +1311,13 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "prefetch_blocks")) {
     if (value < 8 || value > 4096 || value % 8) return fail(ctx, YHIP_EINVAL, "prefetch_blocks must be a multiple of 8 in [8, 4096]");
     ctx->prefetch_blocks = value;
+  } else if (!strncmp(key, "bpc_", 4)) {
+    static const char* names[5] = {"bpc_qkv", "bpc_o", "bpc_w13", "bpc_w2", "bpc_lm"};
+    int i = 0;
+    while (i < 5 && strcmp(key, names[i])) ++i;
+    if (i == 5) return fail(ctx, YHIP_EINVAL, std::string("unknown option ") + key);
+    if (value < 0 || value > 16) return fail(ctx, YHIP_EINVAL, "workgroups per CU must be in [0, 16]");
+    ctx->mv_bpc[i] = value;
   } else if (!strcmp(key, "attn_min_slice")) {
     if (value < 0 || value % 64) return fail(ctx, YHIP_EINVAL, "attn_min_slice must be 0 or a positive multiple of 64");
     ctx->attn_min_slice = value;
