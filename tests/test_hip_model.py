@@ -240,12 +240,34 @@ def test_bad_arguments_return_errors():
             m.forward(-1, 0)
         with pytest.raises(H.HipError):
             m.set_option("nonsense", 1)
+        with pytest.raises(H.HipError):
+            m.set_option("bpc_w13", 99)  # workgroups per CU of a decode matvec: 0..16
+        with pytest.raises(H.HipError):
+            m.set_option("bpc_nonsense", 1)
     with pytest.raises(H.HipError):
         H.HipModel(dict(MICRO, head_dim=24))
     # a shape without a single-launch instantiation runs the per-op kernels and refuses the option
     with H.HipModel(dict(MICRO, n_kv_heads=4)) as m:  # one q head per kv head: no instantiation
         with pytest.raises(H.HipError):
             m.set_option("single_launch", 1)
+
+
+@pytest.mark.parametrize("opts", [dict(bpc_w13=2), dict(bpc_w13=16, bpc_qkv=1, bpc_o=3, bpc_w2=2, bpc_lm=4)])
+def test_matvec_grids_do_not_change_results(opts):
+    # The decode matvecs' grid sizes (workgroups per CU) change which wave computes which rows, never
+    # a row's arithmetic: the logits are bit-identical across grids.
+    cfg = dict(TINY)
+    t = np_tensors(cfg, seed=43)
+    toks = [3, 17, 2900, 31000, 8]
+    out = []
+    for o in (None, opts):
+        with hip().HipModel(cfg, t) as m:
+            use_path(m, "graph")
+            for k, v in (o or {}).items():
+                m.set_option(k, v)
+            out.append([m.forward(tok, pos) for pos, tok in enumerate(toks)])
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)
 
 
 def test_staged_upload_is_bit_identical():
