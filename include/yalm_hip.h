@@ -104,8 +104,10 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * 32 == 0 and max_seq_len % 32 == 0, default; 0 = the SIMT kernel), "prefetch_o" /
  * "prefetch_w13_mb" / "prefetch_blocks" (extra workgroups of the attention launch read the layer's
  * O weights / the first MB of W1 and W3 into the caches; worker count, a multiple of 8; off by
- * default), "stats" (1 = time every synchronised step on the device with HIP events and reset the
- * totals; 0 = off).
+ * default), "bpc_qkv" / "bpc_o" / "bpc_w13" / "bpc_w2" / "bpc_lm" (workgroups per CU of the decode
+ * matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for W2; the
+ * results do not depend on it), "stats" (1 = time every synchronised step on the device with HIP
+ * events and reset the totals; 0 = off).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
