@@ -99,8 +99,10 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
  * kv head, default 3/4 of compute units / n_kv_heads clamped to [1,64]),
- * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default, 256
- * for the MFMA attention and 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode attention on the matrix cores where head_dim %
+ * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for
+ * the MFMA attention one slice up to 320 cached tokens, then 64 up to 1536, 256 up to 4096 and 384
+ * beyond; 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode
+ * attention on the matrix cores where head_dim %
  * 32 == 0 and max_seq_len % 32 == 0, default; 0 = the SIMT kernel), "prefetch_o" /
  * "prefetch_w13_mb" / "prefetch_blocks" (extra workgroups of the attention launch read the layer's
  * O weights / the first MB of W1 and W3 into the caches; worker count, a multiple of 8; off by

@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
   const int g = blockIdx.x, split = blockIdx.y;
   const Positions pss = positions(a.params->pos, a.msl);
   const int kv_len = pss.kv_len;
-  const int chunk = attn_chunk(kv_len, a.nsplit, a.min_slice, TS);
+  const int chunk = attn_mfma_chunk(kv_len, a.nsplit, a.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
   if (split >= active) return;
   const int t_begin = split * chunk;

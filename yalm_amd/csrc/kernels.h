@@ -865,7 +865,7 @@ struct AttnArgs {
   unsigned* tickets;     // [nkv]
   float* out;            // [nh][hd]
   int head_dim, n_heads, n_kv_heads, msl, nsplit;
-  int min_slice;          // smallest KV slice per workgroup (multiple of 64)
+  int min_slice;          // smallest KV slice per workgroup (multiple of 64; MFMA kernel: 0 = by length)
   const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
   AttnPrefetch pf;
@@ -881,6 +881,20 @@ __host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int m
   chunk = (chunk + gran - 1) / gran * gran;
   const int floor = (kv_len >= 1024 && min_slice < 128) ? 128 : min_slice;
   return chunk < floor ? floor : chunk;
+}
+
+// Slice length of the MFMA decode attention: min_slice > 0 is a fixed floor; 0 picks it by context
+// length, from a sweep on MI355X (Mistral shape, 24 slices per kv head; µs per layer):
+//   - up to 320 keys one slice per kv head, no cross-workgroup merge (300 keys: 7.8 against 9.7
+//     with two 256-key slices);
+//   - up to 1536 keys slices of 64 (128 from 1024 keys on): the merge of many short slices costs
+//     less than two or three long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1);
+//   - up to 4096 keys 256 (2048: 10.5 against 11.0 with 128), beyond that 384 (6000: 13.8
+//     against 14.8); from ~8K keys the slice count (nsplit) decides and the floor does not matter.
+__host__ __device__ __forceinline__ int attn_mfma_chunk(int kv_len, int nsplit, int min_slice) {
+  if (min_slice > 0) return attn_chunk(kv_len, nsplit, min_slice, 32);
+  if (kv_len <= 320) return (kv_len + 31) / 32 * 32;
+  return attn_chunk(kv_len, nsplit, kv_len <= 1536 ? 64 : (kv_len <= 4096 ? 256 : 384), 32);
 }
 
 // Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the

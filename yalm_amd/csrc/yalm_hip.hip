@@ -287,11 +287,11 @@ bool launch_attention_hd(const AttnArgs& a, bool mfma, hipStream_t s) {
   }
 }
 
-// Fewest tokens per KV slice: the option's value, else 256 for the MFMA kernel (one workgroup of
-// eight waves covers short contexts without a cross-workgroup merge) and 64 for the SIMT kernel.
+// Fewest tokens per KV slice: the option's value, else for the MFMA kernel 0 (the kernel picks it
+// from the context length, attn_mfma_chunk) and 64 for the SIMT kernel.
 int attn_min_slice_for(const yhip_ctx* ctx, bool mfma) {
   if (ctx->attn_min_slice > 0) return ctx->attn_min_slice;
-  return mfma ? 256 : 64;
+  return mfma ? 0 : 64;
 }
 
 bool attn_uses_mfma(const yhip_ctx* ctx) {
@@ -1775,7 +1775,7 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
 extern "C" int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, int max_seq_len, int kv_len, int nsplit,
                                     int min_slice, int copies, int warmup, int reps, float* us_per_launch) {
   if (!us_per_launch || kv_len <= 0 || kv_len > max_seq_len || copies <= 0 || reps <= 0 || warmup < 0 || nsplit < 1 ||
-      nsplit > 64 || min_slice < 64 || min_slice % 64)
+      nsplit > 64 || min_slice < 0 || min_slice % 64)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
   const size_t kv = (size_t)n_kv_heads * head_dim * max_seq_len;
