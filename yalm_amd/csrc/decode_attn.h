@@ -145,7 +145,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       }
     }
 
-    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale = kLog2e / sqrtf((float)HD);  // scores in log2 units (exp2_fast)
     // one 32-key tile: scores, online softmax (per column = head), values
     auto tile = [&](const KvFrag<HD>& f, int t0) {
       f32x4 s[2];
@@ -167,13 +167,13 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       mt = fmaxf(mt, __shfl_xor(mt, 16));
       mt = fmaxf(mt, __shfl_xor(mt, 32));
       const float m_new = fmaxf(m_run, mt);
-      const float corr = expf(m_run - m_new);
+      const float corr = exp2_fast(m_run - m_new);
       m_run = m_new;
       f16x8 pf;
       float psum = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float p = sv[e] > kNegBig ? expf(sv[e] - m_new) : 0.f;
+        const float p = sv[e] > kNegBig ? exp2_fast(sv[e] - m_new) : 0.f;
         psum += p;
         const float ps = p * kPScale;
         const f16 hi = (f16)ps;
@@ -244,7 +244,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
     float O = 0.f, L = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float wt = expf(oml[w][h][0] - M);
+      const float wt = exp2_fast(oml[w][h][0] - M);
       O = fmaf(om[w][h][d], wt, O);
       L = fmaf(oml[w][h][1], wt, L);
     }
@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
       store_shared(dst + d, O);
       if (d == 0) {
-        store_shared(dst + HD, M);
+        store_shared(dst + HD, M * kLn2);  // the slice merge works in natural units
         store_shared(dst + HD + 1, L);
       }
     }

@@ -23,6 +23,14 @@ constexpr int kWave = 64;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kKvSinks = 2;  // reference src/model.h:12
 constexpr float kNegBig = -3.402823466e38f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 2^x as the hardware's v_exp_f32 (about 1 ulp on the range the softmaxes use, x <= 0; results
+// below 2^-126 flush to zero, which is nothing next to the running maximum's own term of 1). The
+// attention kernels keep scores in log2 units (scaled by log2 e) so that every exponential is this
+// one instruction instead of the ~13 of expf.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Per-token parameters, resident on the device so that a captured graph stays static.
 struct StepParams {

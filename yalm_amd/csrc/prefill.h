@@ -643,7 +643,7 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
-  const float scale = 1.0f / sqrtf((float)HD);
+  const float scale = kLog2e / sqrtf((float)HD);  // scores in log2 units (exp2_fast)
 
   // staging of a key tile: K (32 keys x HD dims, 16-byte pieces) and V (HD dims x 32 keys)
   constexpr int KPIECES = 32 * HD / 8, VPIECES = HD * 32 / 8;
@@ -699,12 +699,12 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = k0 + acc_row(r, lane);
-      s[r] = key <= q_pos ? s[r] * scale : kNegBig;
+      s[r] = key <= q_pos ? s[r] * scale : kNegBig;  // log2 units
       mt = fmaxf(mt, s[r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
-    const float corr = expf(m_run - m_new);
+    const float corr = exp2_fast(m_run - m_new);
     float ps = 0.f;
     u32x4 pf[2];
 #pragma unroll
@@ -713,7 +713,7 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * kk + e;
-        const float p = s[r] > kNegBig ? expf(s[r] - m_new) : 0.f;
+        const float p = s[r] > kNegBig ? exp2_fast(s[r] - m_new) : 0.f;
         ps += p;
         p8[e] = (f16)p;
       }
