@@ -181,11 +181,12 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       }
       l_run = l_run * corr + psum;
       const u32x4 pb = __builtin_bit_cast(u32x4, pf);
+      // rescale only when some column's running maximum moved
+      if (__any(corr != 1.f))
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        acc[dt] *= corr;
-        acc[dt] = mfma_16x16x32(f.v[dt], pb, acc[dt]);
-      }
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= corr;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma_16x16x32(f.v[dt], pb, acc[dt]);
     };
     // Two register buffers used alternately (unrolled by two, no copies between them): while one
     // tile is used the next one's loads are in flight, and the scheduling barrier keeps them at the

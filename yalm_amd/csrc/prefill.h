@@ -696,11 +696,19 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     for (int ks = 0; ks < KS; ++ks) s = mfma32(*reinterpret_cast<const u32x4*>(krow + 16 * ks), qf[ks], s);
     // mask (key position > query position), scale, tile max of this query
     float mt = kNegBig;
+    if (k0 + 31 <= a.start + q0) {  // every key of the tile precedes the wave's first query
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = k0 + acc_row(r, lane);
-      s[r] = key <= q_pos ? s[r] * scale : kNegBig;  // log2 units
-      mt = fmaxf(mt, s[r]);
+      for (int r = 0; r < 16; ++r) {
+        s[r] *= scale;  // log2 units
+        mt = fmaxf(mt, s[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + acc_row(r, lane);
+        s[r] = key <= q_pos ? s[r] * scale : kNegBig;
+        mt = fmaxf(mt, s[r]);
+      }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
@@ -723,10 +731,13 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     l_run = l_run * corr + ps;
     m_run = m_new;
     // O^T += V^T P^T; k order of step kk: keys 16 kk + {0..3, 8..11} + 4 half of the tile
+    // rescale only when some query's running maximum moved (after the first tiles it rarely does)
+    const bool rescale = __any(corr != 1.f);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
+      if (rescale)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
       const uint16_t* vrow = &Vs[buf][(t * 32 + (lane & 31)) * VLD + 4 * half];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
