@@ -552,7 +552,15 @@ __global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, co
 __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int head_dim,
                                                           float qkv_clip, const float* inv_freq, int start, int msl,
                                                           uint16_t* Q, uint16_t* kcache, uint16_t* vcache) {
+  // (cos, sin) of pos * freq_k once per rotary pair k of the row, shared by all q and k heads
+  __shared__ float rope[128];  // head_dim <= 128 on the batched path (prefill_supported)
   const int t = blockIdx.x, pos = start + t;
+  for (int k = threadIdx.x; k < head_dim / 2; k += kBlock) {
+    const float ang = (float)pos * inv_freq[k];
+    rope[2 * k] = cosf(ang);
+    rope[2 * k + 1] = sinf(ang);
+  }
+  __syncthreads();
   const float* c = C + (long)t * ldc;
   const int pairs = (q_dim + 2 * kv_dim) / 2;
   for (int p = threadIdx.x; p < pairs; p += kBlock) {
@@ -560,8 +568,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
     float v0 = clipf(c[i], qkv_clip), v1 = clipf(c[i + 1], qkv_clip);
     if (i < q_dim + kv_dim) {
       const int j = i % head_dim;
-      const float ang = (float)pos * inv_freq[j / 2];
-      const float cs = cosf(ang), sn = sinf(ang);
+      const float cs = rope[j], sn = rope[j + 1];
       const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
       v0 = r0;
       v1 = r1;
