@@ -534,15 +534,46 @@ __global__ void __launch_bounds__(kBlock) embed_rows_kernel(const uint16_t* emb,
 }
 
 // Xn[t] = fp16(X[t] * inv * g), inv = 1/sqrt(mean(X[t]^2) + eps) (reference src/infer.cpp:136-146)
+// Rows up to 8192 long (dim % 4 == 0) stay in registers as float4 between the sum and the output
+// (one read of X, 16-byte loads and 8-byte stores); longer rows take the two-pass loop.
 __global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, const float* gain, float eps, int dim,
                                                               uint16_t* Xn) {
   __shared__ float red[kWavesPerBlock];
   const float* x = X + (long)blockIdx.x * dim;
+  uint16_t* o = Xn + (long)blockIdx.x * dim;
+  constexpr int kMax4 = 8;  // float4 per thread: 8192 / (4 * 256)
+  const int n4 = dim / 4;
+  if (dim % 4 == 0 && n4 <= kMax4 * kBlock) {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    f32x4 v[kMax4];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMax4; ++k) {
+      const int i = threadIdx.x + kBlock * k;
+      v[k] = i < n4 ? x4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+      ss += v[k][0] * v[k][0] + v[k][1] * v[k][1] + v[k][2] * v[k][2] + v[k][3] * v[k][3];
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(gain);
+#pragma unroll
+    for (int k = 0; k < kMax4; ++k) {
+      const int i = threadIdx.x + kBlock * k;
+      if (i < n4) {
+        const f32x4 g = g4[i];
+        unsigned long long h = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h |= (unsigned long long)__builtin_bit_cast(uint16_t, (f16)(v[k][e] * inv * g[e])) << (16 * e);
+        reinterpret_cast<unsigned long long*>(o)[i] = h;
+      }
+    }
+    return;
+  }
   float ss = 0.f;
   for (int i = threadIdx.x; i < dim; i += kBlock) ss += x[i] * x[i];
   ss = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-  uint16_t* o = Xn + (long)blockIdx.x * dim;
   for (int i = threadIdx.x; i < dim; i += kBlock) o[i] = __builtin_bit_cast(uint16_t, (f16)(x[i] * inv * gain[i]));
 }
 
@@ -574,17 +605,16 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
       v1 = r1;
     }
     const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0), h1 = __builtin_bit_cast(uint16_t, (f16)v1);
+    const uint32_t h01 = (uint32_t)h0 | ((uint32_t)h1 << 16);
     if (i < q_dim) {
-      Q[(long)t * q_dim + i] = h0;
-      Q[(long)t * q_dim + i + 1] = h1;
+      *reinterpret_cast<uint32_t*>(Q + (long)t * q_dim + i) = h01;  // i even: one 4-byte store
     } else {
       const bool is_k = i < q_dim + kv_dim;
       const int ik = i - q_dim - (is_k ? 0 : kv_dim);
       const int g = ik / head_dim, j = ik % head_dim;
       const long head = (long)g * head_dim * msl;
-      if (is_k) {
-        kcache[head + k_cache_idx(j, pos, msl)] = h0;
-        kcache[head + k_cache_idx(j + 1, pos, msl)] = h1;
+      if (is_k) {  // dims j, j+1 (j even) are adjacent in a 16-dim chunk of the K layout
+        *reinterpret_cast<uint32_t*>(kcache + head + k_cache_idx(j, pos, msl)) = h01;
       } else {
         vcache[head + (long)j * msl + pos] = h0;
         vcache[head + (long)(j + 1) * msl + pos] = h1;
