@@ -578,11 +578,11 @@ __global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, co
 }
 
 // Row t of the QKV GEMM output (position start + t): clip, RoPE on q and k pairs
-// (reference src/infer.cpp:197-215, 284-305), q as fp16 into Q, k and v as fp16 into the caches at
-// the row's position (no ring: start + n <= max_seq_len).
+// (reference src/infer.cpp:197-215, 284-305), q as fp16 into Q, k as fp16 into the cache at the
+// row's position (no ring: start + n <= max_seq_len). The v columns go to v_rows_kernel.
 __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int head_dim,
                                                           float qkv_clip, const float* inv_freq, int start, int msl,
-                                                          uint16_t* Q, uint16_t* kcache, uint16_t* vcache) {
+                                                          uint16_t* Q, uint16_t* kcache) {
   // (cos, sin) of pos * freq_k once per rotary pair k of the row, shared by all q and k heads
   __shared__ float rope[128];  // head_dim <= 128 on the batched path (prefill_supported)
   const int t = blockIdx.x, pos = start + t;
@@ -593,7 +593,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
   }
   __syncthreads();
   const float* c = C + (long)t * ldc;
-  const int pairs = (q_dim + 2 * kv_dim) / 2;
+  const int pairs = (q_dim + kv_dim) / 2;  // q and k; v goes through v_rows_kernel
   for (int p = threadIdx.x; p < pairs; p += kBlock) {
     const int i = 2 * p;
     float v0 = clipf(c[i], qkv_clip), v1 = clipf(c[i + 1], qkv_clip);
@@ -608,18 +608,33 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
     const uint32_t h01 = (uint32_t)h0 | ((uint32_t)h1 << 16);
     if (i < q_dim) {
       *reinterpret_cast<uint32_t*>(Q + (long)t * q_dim + i) = h01;  // i even: one 4-byte store
-    } else {
-      const bool is_k = i < q_dim + kv_dim;
-      const int ik = i - q_dim - (is_k ? 0 : kv_dim);
+    } else {  // k: dims j, j+1 (j even) are adjacent in a 16-dim chunk of the K layout
+      const int ik = i - q_dim;
       const int g = ik / head_dim, j = ik % head_dim;
-      const long head = (long)g * head_dim * msl;
-      if (is_k) {  // dims j, j+1 (j even) are adjacent in a 16-dim chunk of the K layout
-        *reinterpret_cast<uint32_t*>(kcache + head + k_cache_idx(j, pos, msl)) = h01;
-      } else {
-        vcache[head + (long)j * msl + pos] = h0;
-        vcache[head + (long)(j + 1) * msl + pos] = h1;
-      }
+      *reinterpret_cast<uint32_t*>(kcache + (long)g * head_dim * msl + k_cache_idx(j, pos, msl)) = h01;
     }
+  }
+}
+
+// The v columns of the QKV GEMM output into the V cache (clip, fp16 RNE; reference
+// src/infer.cpp:284-305): V[g][d][pos] is position-contiguous, so a workgroup transposes a tile of
+// 64 positions x 64 value dims through LDS and writes 128 contiguous bytes per dim instead of one
+// 2-byte store per (position, dim).
+__global__ void __launch_bounds__(kBlock) v_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int n,
+                                                        float qkv_clip, int start, int msl, uint16_t* vcache) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int p0 = blockIdx.x * 64, d0 = blockIdx.y * 64;  // positions (rows of C), value dims
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += kBlock / 64) {  // read: a row's 64 dims, coalesced
+    const int t = p0 + r, d = d0 + tx;
+    float v = 0.f;
+    if (t < n && d < kv_dim) v = clipf(C[(long)t * ldc + q_dim + kv_dim + d], qkv_clip);
+    tile[tx][r] = __builtin_bit_cast(uint16_t, (f16)v);
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += kBlock / 64) {  // write: a dim's 64 positions, coalesced
+    const int d = d0 + r, t = p0 + tx;
+    if (t < n && d < kv_dim) vcache[(long)d * msl + start + t] = tile[r][tx];
   }
 }
 

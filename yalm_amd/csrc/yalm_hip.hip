@@ -806,7 +806,10 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     if ((rc = launch_gemm<kGemmStore>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(qkv_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_C, qd + 2 * kvd, qd, kvd,
                        c.head_dim, c.qkv_clip, (const float*)ctx->inv_freq, start, c.max_seq_len, ctx->pf_Q,
-                       ctx->kcache(l), ctx->vcache(l));
+                       ctx->kcache(l));
+    // the V cache of kv head g at (g * head_dim + d) * msl: one [kv_dim][msl] matrix
+    hipLaunchKernelGGL(v_rows_kernel, dim3((n + 63) / 64, (kvd + 63) / 64), dim3(kBlock), 0, s, (const float*)ctx->pf_C,
+                       qd + 2 * kvd, qd, kvd, n, c.qkv_clip, start, c.max_seq_len, ctx->vcache(l));
     PrefillAttnArgs pa;
     pa.Q = ctx->pf_Q;
     pa.kcache = ctx->kcache(l);
