@@ -673,8 +673,10 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][HD * VLD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int gh = wave % G, qs = wave / G;
-  const int qb = a.n_blocks - 1 - blockIdx.x;  // latest (longest) query tiles first
-  const int g = blockIdx.y;
+  // latest (longest) query tiles first, of every kv head: the dispatcher starts the workgroups in
+  // order, so the long ones of all heads start in the first round and the short ones fill in
+  const int qb = a.n_blocks - 1 - (int)blockIdx.x / a.n_kv_heads;
+  const int g = (int)blockIdx.x % a.n_kv_heads;
   const int h = g * G + gh;
   const int q0 = (qb * QT + qs) * 32;
   const int qd = a.n_heads * HD;

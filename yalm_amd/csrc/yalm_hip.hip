@@ -728,7 +728,7 @@ template <int HD>
 bool launch_prefill_attn_hd(PrefillAttnArgs p, int G, int n_qtiles, hipStream_t s) {
   auto go = [&](auto kernel, int qt, int threads) {
     p.n_blocks = (n_qtiles + qt - 1) / qt;
-    hipLaunchKernelGGL(kernel, dim3(p.n_blocks, p.n_kv_heads), dim3(threads), 0, s, p);
+    hipLaunchKernelGGL(kernel, dim3(p.n_blocks * p.n_kv_heads), dim3(threads), 0, s, p);
   };
   switch (G) {
     case 1: go(prefill_attn_kernel<HD, 1, 4>, 4, 256); return true;
