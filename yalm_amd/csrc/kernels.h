@@ -1013,16 +1013,16 @@ __device__ __forceinline__ void attn_merge_slices(const AttnArgs& a, int g, int 
     }
   }
   __syncthreads();
-  if (tid < G) {
-    float M = kNegBig;
-    for (int sp = 0; sp < active; ++sp) M = fmaxf(M, mrg[tid][sp][0]);
-    float L = 0.f;
-    for (int sp = 0; sp < active; ++sp) {
-      const float w = expf(mrg[tid][sp][0] - M);
-      mrg[tid][sp][0] = w;
-      L = fmaf(mrg[tid][sp][1], w, L);
-    }
-    Ls[tid] = L;
+  // per head: wave h, lane sp (active <= 64 slices), reduced across the wave instead of a serial
+  // loop over the slices on one lane
+  for (int h = tid / kWave; h < G; h += NT / kWave) {
+    const int sp = tid & (kWave - 1);
+    const float m = sp < active ? mrg[h][sp][0] : kNegBig;
+    const float M = wave_max(m);
+    const float w = sp < active ? expf(m - M) : 0.f;
+    const float L = wave_sum(sp < active ? mrg[h][sp][1] * w : 0.f);
+    if (sp < active) mrg[h][sp][0] = w;
+    if (sp == 0) Ls[h] = L;
   }
   __syncthreads();
   float Ov[OPT];
