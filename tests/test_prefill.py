@@ -141,6 +141,33 @@ def test_prefill_matches_sequential_hydrate(cfg_name, n):
     hm.close()
 
 
+# Batched-path shapes beyond tiny: one kv head of 32 dims (the V-cache transpose covers half a
+# 64-dim tile), 2 and 8 query heads per kv head, head_dim 64 and partial rotary; prompt lengths
+# that are not multiples of the 64-position transpose tile, after a few decode steps.
+PREFILL_SHAPES = {
+    "hd32_kv1_g4": dict(TINY, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, n_layers=2),
+    "hd64_g2": dict(TINY, dim=256, head_dim=64, n_heads=4, n_kv_heads=2, rotary_dim=32, n_layers=2),
+    "hd32_g8": dict(TINY, dim=256, head_dim=32, n_heads=8, n_kv_heads=1, rotary_dim=32, n_layers=2),
+}
+
+
+@pytest.mark.parametrize("shape", list(PREFILL_SHAPES))
+def test_prefill_shapes_match_sequential_hydrate(shape):
+    cfg = PREFILL_SHAPES[shape]
+    t = np_tensors(cfg, seed=46, std=0.05)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    toks = np.random.default_rng(47).integers(0, cfg["vocab_size"], 3 + 131)
+    for i in range(3):
+        om.forward(int(toks[i]), i, 0)
+        hm.forward(int(toks[i]), i, 0)
+    lh = hm.prefill(toks[3:], start_pos=3)
+    lo = _sequential(om, toks[3:], start=3)
+    assert npref.rel_l2(lh, lo) < PREFILL_LOGIT_TOL
+    _check_kv_close(om, hm, cfg["n_layers"], len(toks))
+    hm.close()
+
+
 def test_prefill_in_chunks_and_after_decode_steps():
     cfg = dict(TINY)
     t = np_tensors(cfg, seed=43)
