@@ -36,7 +36,10 @@ def bpc(request):
     hip().set_test_bpc(0)
 
 
-@pytest.mark.parametrize("d,n", [(32, 64), (100, 256), (384, 768), (6144, 4096), (4096, 14336), (1000, 4096)])
+# (1002, 4096) and (6, 14336): more waves than row groups on the unrolled paths (the idle waves'
+# first loads go through zero-length descriptors)
+@pytest.mark.parametrize("d,n", [(32, 64), (100, 256), (384, 768), (6144, 4096), (4096, 14336), (1000, 4096),
+                                 (1002, 4096), (6, 14336)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_matvec_parity(d, n, norm, bpc):
     rng = np.random.default_rng(d * 7 + n)
