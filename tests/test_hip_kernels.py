@@ -192,6 +192,44 @@ def test_attention_known_answer_one_hot_softmax(attn_impl):
     assert np.allclose(got, want, atol=1e-4)
 
 
+@pytest.mark.parametrize("hd,nh,nkv,msl,kv_len", [(32, 8, 2, 512, 300), (128, 32, 8, 4096, 3201),
+                                                   (128, 32, 8, 4096, 93)])
+@pytest.mark.parametrize("qmag", [1e5, 1e-4])
+def test_attention_query_magnitude_beyond_fp16(hd, nh, nkv, msl, kv_len, qmag, attn_impl):
+    # The reference keeps q in fp32 (src/infer.cpp:218-250), and with qkv_clip = FLT_MAX nothing
+    # bounds it. Queries of 1e5 (past the fp16 range) and 1e-4 (fp16 subnormal territory) must give
+    # the oracle's result on both kernels; the matrix-core one scales each head into range.
+    rng = np.random.default_rng(hd + kv_len + int(qmag > 1))
+    # keys scaled so that the scores stay O(10): the softmax is not one-hot and q's precision counts
+    kb = f16(rng.standard_normal(nkv * hd * msl) * (1e-4 if qmag > 1 else 1.0))
+    vb = f16(rng.standard_normal(nkv * hd * msl))
+    q = (rng.standard_normal(nh * hd) * qmag).astype(np.float32)
+    got, _ = hip().attention(q, kb, vb, hd, kv_len - 1, msl, nh, nkv)
+    want, _ = O.mha(q, kb, vb, hd, kv_len, msl, nh, nkv)
+    assert np.all(np.isfinite(got))
+    assert npref.rel_l2(got, want) < RTOL
+
+
+@pytest.mark.parametrize("hd", [32, 128])
+def test_attention_known_answer_query_1e5(hd, attn_impl):
+    # The reference's known-answer construction (src/test.cpp:67-125) with query entries of 1e5:
+    # each head's softmax is one-hot on a chosen key, and the output is that key's V column.
+    nh, nkv, msl, kv_len = 4, 1, 64, 40
+    kb = np.zeros(nkv * hd * msl, np.uint16)
+    V = np.zeros((hd, msl), np.float32)
+    targets = [3, 17, 30, 39]  # key position chosen by head h
+    for h, tpos in enumerate(targets):
+        kb[O.k_cache_idx(h, tpos, msl)] = f16([1.0])[0]  # key tpos points along dim h
+        V[:, tpos] = np.arange(hd) * 0.01 + h
+    vb = f16(V.reshape(-1))
+    q = np.zeros(nh * hd, np.float32)
+    for h in range(nh):
+        q[h * hd + h] = 1e5
+    got, _ = hip().attention(q, kb, vb, hd, kv_len - 1, msl, nh, nkv)
+    want = np.concatenate([h2f(vb).reshape(hd, msl)[:, t] for t in targets])
+    assert np.allclose(got, want, atol=1e-4)
+
+
 def _oracle_qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc, theta=1e6, clip=3.4028234663852886e38):
     xb = O.rmsnorm(x, g, 1e-5) if g is not None else x.astype(np.float32)
     q = np.clip(O.matmul_f16(xb, wq), -clip, clip)
@@ -257,6 +295,39 @@ def test_qkv_rope_parity(pos, shape, bpc):
     vmask[vidx] = True
     assert np.array_equal(v2[~vmask], vc[~vmask])
     assert npref.rel_l2(h2f(v2[vidx]), h2f(vo[vidx])) < 2e-3
+
+
+@pytest.mark.parametrize("pos", [5, 4095])
+@pytest.mark.parametrize("shape,clip", [((256, 8, 2, 32, 512), 0.05), ((256, 8, 2, 32, 512), 0.2),
+                                        ((4096, 32, 8, 128, 4096), 0.05), ((4096, 32, 8, 128, 4096), 1.0)])
+def test_qkv_finite_clip_before_rope(pos, shape, clip):
+    # A finite qkv_clip (metadata key, reference src/model.cpp:59) clamps q, k and v before RoPE
+    # (src/infer.cpp:284-294). With q ~ N(0, 1.3) at the Mistral shape most entries saturate, so a
+    # clip applied after RoPE (rotated pairs reach clip * sqrt(2)) or not at all shows at once.
+    dim, nh, nkv, hd, msl = shape
+    rng = np.random.default_rng(pos + dim + 7)
+    wq = f16(rng.standard_normal((nh * hd, dim)) * 0.02)
+    wk = f16(rng.standard_normal((nkv * hd, dim)) * 0.02)
+    wv = f16(rng.standard_normal((nkv * hd, dim)) * 0.02)
+    x = rng.standard_normal(dim).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    kc = np.zeros(nkv * hd * msl, np.uint16)
+    vc = np.zeros(nkv * hd * msl, np.uint16)
+    q, k2, v2 = hip().qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc, qkv_clip=clip)
+    qo, ko, vo = _oracle_qkv(x, g, wq, wk, wv, nh, nkv, hd, msl, pos, kc, vc, clip=clip)
+    raw = O.matmul_f16(O.rmsnorm(x, g, 1e-5), wq)
+    assert np.mean(np.abs(raw) >= clip) > 0.2  # the clip is active on many entries
+    assert npref.rel_l2(q, qo) < 1e-5 + 3e-7 * pos
+    # rotated clipped pairs leave the [-clip, clip] box: the clip ran before RoPE
+    assert np.max(np.abs(q)) > 1.2 * clip
+    assert np.max(np.abs(q)) <= clip * np.sqrt(2) * (1 + 1e-5)
+    kv_pos = O.positions(pos, msl)[1]
+    idx = np.array([gi * hd * msl + O.k_cache_idx(j, kv_pos, msl) for gi in range(nkv) for j in range(hd)])
+    vidx = np.array([gi * hd * msl + j * msl + kv_pos for gi in range(nkv) for j in range(hd)])
+    assert npref.rel_l2(h2f(k2[idx]), h2f(ko[idx])) < 2e-3
+    # V is clipped and not rotated: every entry within the box, equal to the oracle's to an ulp
+    assert np.max(np.abs(h2f(v2[vidx]))) <= clip * (1 + 2 ** -10)
+    assert np.max(np.abs(h2f(v2[vidx]) - h2f(vo[vidx]))) <= 2 ** -10 * clip
 
 
 def test_argmax_tie_rule():

@@ -8,9 +8,11 @@
 //     loads are in flight while the current one is used; a wave with no tile issues no loads;
 //   - scores S^T = K Q^T with v_mfma_f32_16x16x32_f16, two 16-key groups per tile: A = 16 keys x
 //     32 dims of K straight from the 16-tiled cache (16 bytes per lane), B = the G query heads as
-//     columns. fp32 q is split into q_hi = fp16(q) and q_lo = fp16(q - q_hi) in columns h and
-//     G + h, so the sum of the two columns carries ~22 bits of q (fp16 products are exact in the
-//     fp32 accumulate);
+//     columns. Each head's fp32 q is first scaled by a power of two that maps its largest |q| into
+//     [2^14, 2^15) (undone exactly in the score scale), then split into q_hi = fp16(q) and
+//     q_lo = fp16(q - q_hi) in columns h and G + h, so the sum of the two columns carries ~22 bits
+//     of q relative to the head's largest entry, for any finite fp32 q (fp16 products are exact in
+//     the fp32 accumulate);
 //   - the keys of group j are ordered so that row 4 i + r is key 8 i + 4 j + r of the tile: the
 //     accumulators then leave lane l (column l % 16) with keys 8 (l / 16) .. +7 of the tile, which
 //     is exactly the B operand layout of O^T += V^T P^T on v_mfma_f32_16x16x32_f16, and the A
@@ -19,7 +21,7 @@
 //     range and split into hi/lo columns like q (undone at the end);
 //   - the waves' (m, l, o) are merged in LDS; slices of one kv head are merged by the last one
 //     to finish (attn_merge_slices).
-// Needs head_dim % 32 == 0 and max_seq_len % 32 == 0. |q| must stay below the fp16 range (65504).
+// Needs head_dim % 32 == 0 and max_seq_len % 32 == 0.
 #pragma once
 
 #include "kernels.h"
@@ -121,6 +123,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
 
     // q as the B operand: column col is head col (hi part) or head col - G (lo part); others zero
     u32x4 qf[KS];
+    float smul;  // score scale of this lane's head: 1/sqrt(hd) in log2 units, times 2^-e of the head
     {
       const bool used = col < 2 * G;
       const bool lo = col >= G;
@@ -132,12 +135,23 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
         q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
         q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
       }
+      // the head's largest |q| over the four lanes of the column (each holds 8 of every 32 dims)
+      float amax = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(q4[ks][e >> 2][e & 3]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      const int qe = q_range_exp(amax);
+      const float qmul = __builtin_ldexpf(1.0f, qe);
+      smul = __builtin_ldexpf(kLog2e / sqrtf((float)HD), -qe);  // scores in log2 units (exp2_fast)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         f16x8 v;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float x = q4[ks][e >> 2][e & 3];
+          const float x = q4[ks][e >> 2][e & 3] * qmul;
           const f16 hi = (f16)x;
           v[e] = !used ? (f16)0.f : (lo ? (f16)(x - (float)hi) : hi);
         }
@@ -145,7 +159,6 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       }
     }
 
-    const float scale = kLog2e / sqrtf((float)HD);  // scores in log2 units (exp2_fast)
     // one 32-key tile: scores, online softmax (per column = head), values
     auto tile = [&](const KvFrag<HD>& f, int t0) {
       f32x4 s[2];
@@ -161,7 +174,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       for (int e = 0; e < 8; ++e) {
         const float raw = s[e >> 2][e & 3];
         const float v = raw + __shfl_xor(raw, G, 16);  // hi + lo columns (both partners get the sum)
-        sv[e] = (t0 + 8 * grp + e < t_end) ? v * scale : kNegBig;
+        sv[e] = (t0 + 8 * grp + e < t_end) ? v * smul : kNegBig;
         mt = fmaxf(mt, sv[e]);
       }
       mt = fmaxf(mt, __shfl_xor(mt, 16));

@@ -98,6 +98,16 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// Power-of-two exponent that brings a head's largest |q| (amax) into [2^14, 2^15): q * 2^e is then
+// finite in fp16 (also as hi/lo parts) for any finite fp32 q, and the head's scores are multiplied
+// by 2^-e. Clamped so that neither factor leaves the normal fp32 range; amax 0, inf or NaN leaves q
+// as it is.
+__device__ __forceinline__ int q_range_exp(float amax) {
+  if (!(amax > 0.f) || !(amax < 3.402823466e38f)) return 0;
+  const int e = 15 - __builtin_amdgcn_frexp_expf(amax);  // amax = m 2^E, m in [0.5, 1)
+  return e < -60 ? -60 : (e > 100 ? 100 : e);
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float gelu(float x) {
   return 0.5f * x * (1.0f + tanhf(0.797885f * (x + 0.044715f * x * x * x)));

@@ -580,9 +580,12 @@ __global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, co
 // Row t of the QKV GEMM output (position start + t): clip, RoPE on q and k pairs
 // (reference src/infer.cpp:197-215, 284-305), q as fp16 into Q, k as fp16 into the cache at the
 // row's position (no ring: start + n <= max_seq_len). The v columns go to v_rows_kernel.
+// Each query head of the row is stored scaled by the power of two that maps its largest |q| into
+// [2^14, 2^15) (q_range_exp), so any finite fp32 q fits fp16 with the same relative precision;
+// qscale[t][h] receives the inverse factor, which the attention applies to the head's scores.
 __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int head_dim,
                                                           float qkv_clip, const float* inv_freq, int start, int msl,
-                                                          uint16_t* Q, uint16_t* kcache) {
+                                                          uint16_t* Q, float* qscale, uint16_t* kcache) {
   // (cos, sin) of pos * freq_k once per rotary pair k of the row, shared by all q and k heads
   __shared__ float rope[128];  // head_dim <= 128 on the batched path (prefill_supported)
   const int t = blockIdx.x, pos = start + t;
@@ -594,15 +597,32 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
   __syncthreads();
   const float* c = C + (long)t * ldc;
   const int pairs = (q_dim + kv_dim) / 2;  // q and k; v goes through v_rows_kernel
-  for (int p = threadIdx.x; p < pairs; p += kBlock) {
+  const int hp = head_dim / 2;             // pairs per head: aligned groups of hp lanes (hp <= 64)
+  // every thread runs the same number of iterations, so the head-wide maximum below can use
+  // cross-lane shuffles; heads are whole groups of lanes, and a group is all live or all dead
+  for (int p0 = 0; p0 < pairs; p0 += kBlock) {
+    const int p = p0 + threadIdx.x;
+    const bool live = p < pairs;
     const int i = 2 * p;
-    float v0 = clipf(c[i], qkv_clip), v1 = clipf(c[i + 1], qkv_clip);
-    if (i < q_dim + kv_dim) {
+    float v0 = 0.f, v1 = 0.f;
+    if (live) {
+      v0 = clipf(c[i], qkv_clip);
+      v1 = clipf(c[i + 1], qkv_clip);
       const int j = i % head_dim;
       const float cs = rope[j], sn = rope[j + 1];
       const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
       v0 = r0;
       v1 = r1;
+    }
+    float amax = fmaxf(fabsf(v0), fabsf(v1));
+    for (int o = 1; o < hp; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if (!live) continue;
+    if (i < q_dim) {
+      const int qe = q_range_exp(amax);
+      const float qmul = __builtin_ldexpf(1.0f, qe);
+      v0 *= qmul;
+      v1 *= qmul;
+      if (p % hp == 0) qscale[(long)t * (q_dim / head_dim) + i / head_dim] = __builtin_ldexpf(1.0f, -qe);
     }
     const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0), h1 = __builtin_bit_cast(uint16_t, (f16)v1);
     const uint32_t h01 = (uint32_t)h0 | ((uint32_t)h1 << 16);
@@ -654,7 +674,8 @@ __global__ void __launch_bounds__(kBlock) v_rows_kernel(const float* C, int ldc,
 // Requires HD % 32 == 0, max_seq_len % 32 == 0 and 64 * G * QT threads <= 1024.
 // ------------------------------------------------------------------------------------------
 struct PrefillAttnArgs {
-  const uint16_t* Q;   // [n][n_heads * HD] fp16
+  const uint16_t* Q;   // [n][n_heads * HD] fp16, each (row, head) scaled by a power of two
+  const float* qscale; // [n][n_heads]: the factor that undoes it, applied to the scores
   const uint16_t* kcache;
   const uint16_t* vcache;
   uint16_t* out;       // [n][n_heads * HD] fp16
@@ -697,7 +718,8 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
 #pragma unroll
   for (int t = 0; t < DT; ++t) o[t] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
-  const float scale = kLog2e / sqrtf((float)HD);  // scores in log2 units (exp2_fast)
+  // scores in log2 units (exp2_fast), with this query's q scale undone
+  const float scale = kLog2e / sqrtf((float)HD) * a.qscale[(long)min(my_q, a.n - 1) * a.n_heads + h];
 
   // staging of a key tile: K (32 keys x HD dims, 16-byte pieces) and V (HD dims x 32 keys)
   constexpr int KPIECES = 32 * HD / 8, VPIECES = HD * 32 / 8;

@@ -138,6 +138,7 @@ struct yhip_ctx {
   uint16_t* pf_H = nullptr;  // [n][hidden] fp16 SwiGLU output
   float* pf_C = nullptr;     // [n][q + 2kv]
   uint16_t* pf_Q = nullptr;  // [n][q]
+  float* pf_qs = nullptr;    // [n][n_heads] score factors of the scaled query heads
   uint16_t* pf_A = nullptr;  // [n][q]
   int* pf_tok = nullptr;     // [n]
   float* pf_P = nullptr;     // split-K partials of the prefill GEMMs
@@ -637,6 +638,30 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 }
 
 // ---- batched prefill ---------------------------------------------------------------------------
+// The prefill GEMM variant for an epilogue and shape (stages 1 = the 256 x 256 kernel, 2..4 the
+// LDS pipeline's depth, 0 the register-staged kernel), or the forced process-wide one.
+void gemm_choice(int epi, int M, int K, int& stages, int& bk, int& bm) {
+  stages = g_gemm_stages;
+  bk = g_gemm_bk;
+  bm = g_gemm_bm;
+  if (!g_gemm_auto) return;
+  // Variant per shape, from a sweep of the Mistral-7B shapes over M = 64..3200 on MI355X: the
+  // 256 x 256 tiles win only from ~3K rows (W1/W3, and W2 with its 14336-long rows); below that the
+  // 128-row LDS pipeline wins (up to 2.9x for W2 at a few hundred rows), with 256-row workgroups
+  // in between for W1/W3 and W2.
+  const bool big_rows = epi == kGemmSwiGLU || K >= 8192;
+  stages = K % 64 == 0 ? 2 : 4;
+  bk = K % 64 == 0 ? 64 : 32;
+  bm = 128;
+  if (big_rows && K % 64 == 0) {
+    if (M >= 3072) {
+      stages = 1;
+    } else if (M >= (epi == kGemmSwiGLU ? 192 : 1536)) {
+      bm = 256;
+    }
+  }
+}
+
 // Prefill GEMM launch. The variant is chosen per shape unless forced with the process-wide
 // options: the 256 x 256 large-tile kernel for the W1/W3 + SwiGLU GEMM and for long K (W2), the
 // 128 x 128 two-stage 64-deep pipeline otherwise (QKV, O), the four-stage 32-deep one when
@@ -644,24 +669,8 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 template <int EPI>
 int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
-  // Variant per shape, from a sweep of the Mistral-7B shapes over M = 64..3200 on MI355X: the
-  // 256 x 256 tiles win only from ~3K rows (W1/W3, and W2 with its 14336-long rows); below that the
-  // 128-row LDS pipeline wins (up to 2.9x for W2 at a few hundred rows), with 256-row workgroups
-  // in between for W1/W3 and W2.
-  int stages = g_gemm_stages, bk = g_gemm_bk, bm = g_gemm_bm;
-  if (g_gemm_auto) {
-    const bool big_rows = EPI == kGemmSwiGLU || g.K >= 8192;
-    stages = g.K % 64 == 0 ? 2 : 4;
-    bk = g.K % 64 == 0 ? 64 : 32;
-    bm = 128;
-    if (big_rows && g.K % 64 == 0) {
-      if (g.M >= 3072) {
-        stages = 1;
-      } else if (g.M >= (EPI == kGemmSwiGLU ? 192 : 1536)) {
-        bm = 256;
-      }
-    }
-  }
+  int stages, bk, bm;
+  gemm_choice(EPI, g.M, g.K, stages, bk, bm);
   // one-dimensional grids of 8 * ceil(tiles / 8) workgroups (gemm_tile)
   auto tiles8 = [&](int tm, int nc) {
     const int t = ((g.M + tm - 1) / tm) * ((g.N + nc - 1) / nc);
@@ -758,7 +767,8 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
     return o;
   };
   const size_t oX = take(N * c.dim * 4), oXn = take(N * c.dim * 2), oH = take(N * c.hidden_dim * 2),
-               oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oA = take(N * qd * 2), oT = take(N * 4),
+               oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oQs = take(N * c.n_heads * 4),
+               oA = take(N * qd * 2), oT = take(N * 4),
                oP = take((size_t)splitk_ws_floats(ctx->num_cus) * 4);
   if (ctx->pf_base) hipFree(ctx->pf_base);
   ctx->pf_base = nullptr;
@@ -769,6 +779,7 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
   ctx->pf_H = (uint16_t*)(ctx->pf_base + oH);
   ctx->pf_C = (float*)(ctx->pf_base + oC);
   ctx->pf_Q = (uint16_t*)(ctx->pf_base + oQ);
+  ctx->pf_qs = (float*)(ctx->pf_base + oQs);
   ctx->pf_A = (uint16_t*)(ctx->pf_base + oA);
   ctx->pf_tok = (int*)(ctx->pf_base + oT);
   ctx->pf_P = (float*)(ctx->pf_base + oP);
@@ -806,12 +817,13 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     if ((rc = launch_gemm<kGemmStore>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(qkv_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_C, qd + 2 * kvd, qd, kvd,
                        c.head_dim, c.qkv_clip, (const float*)ctx->inv_freq, start, c.max_seq_len, ctx->pf_Q,
-                       ctx->kcache(l));
+                       ctx->pf_qs, ctx->kcache(l));
     // the V cache of kv head g at (g * head_dim + d) * msl: one [kv_dim][msl] matrix
     hipLaunchKernelGGL(v_rows_kernel, dim3((n + 63) / 64, (kvd + 63) / 64), dim3(kBlock), 0, s, (const float*)ctx->pf_C,
                        qd + 2 * kvd, qd, kvd, n, c.qkv_clip, start, c.max_seq_len, ctx->vcache(l));
     PrefillAttnArgs pa;
     pa.Q = ctx->pf_Q;
+    pa.qscale = ctx->pf_qs;
     pa.kcache = ctx->kcache(l);
     pa.vcache = ctx->vcache(l);
     pa.out = ctx->pf_A;
@@ -1631,6 +1643,21 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   HIP_TRY(nullptr, hipDeviceSynchronize());
   if (mode == kGemmSwiGLU) HIP_TRY(nullptr, hipMemcpy(h, dh, (size_t)M * N * 2, hipMemcpyDeviceToHost));
   else HIP_TRY(nullptr, hipMemcpy(c, dc, (size_t)M * N * 4, hipMemcpyDeviceToHost));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int* bk, int* bm) {
+  if (!stages || !bk || !bm || M <= 0 || N <= 0 || K <= 0 || mode < 0 || mode > 2)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  int s = 0, k = 0, m = 0;
+  gemm_choice(mode, M, K, s, k, m);
+  if (s != 1) {  // the LDS pipeline's own limits (launch_gemm)
+    if (K % 64 != 0) k = 32;
+    if (k != 64) m = 128;
+  }
+  *stages = s;
+  *bk = k;
+  *bm = s == 1 ? kBigM : m;
   return YHIP_OK;
 }
 

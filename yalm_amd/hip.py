@@ -26,7 +26,7 @@ EXPORTS = (
     "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
-    "yhip_bench_gemm",
+    "yhip_bench_gemm", "yhip_gemm_variant",
 )
 
 
@@ -80,6 +80,7 @@ def lib():
                           + [ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p, _u16p, _u16p]),
         "yhip_test_gemm": (ctypes.c_int, [_u16p, _u16p, _u16p] + [ctypes.c_int] * 5 + [_f32p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
+        "yhip_gemm_variant": (ctypes.c_int, [ctypes.c_int] * 4 + [_ip] * 3),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
         "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
         "yhip_bench_gemm": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
@@ -246,6 +247,14 @@ def set_gemm_ksplit(n=0):
     """Prefill GEMM K splits on the LDS-pipeline kernel: 0 = chosen per shape (split when the output
     has too few tiles to fill the GPU), n >= 1 = forced (must divide the k-steps)."""
     _check(lib().yhip_set_option(None, b"gemm_ksplit", int(n)))
+
+
+def gemm_variant(M, N, K, mode):
+    """(stages, k-step, workgroup rows) of the prefill GEMM yhip_prefill runs for this shape and mode
+    under the current process-wide options (stages 1 = the 256 x 256 large-tile kernel)."""
+    out = [ctypes.c_int() for _ in range(3)]
+    _check(lib().yhip_gemm_variant(M, N, K, mode, *[ctypes.byref(o) for o in out]))
+    return tuple(o.value for o in out)
 
 
 def set_upload(stage_mb=64, threads=8):
