@@ -150,6 +150,19 @@ int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* 
 int yhip_test_attention(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
                         int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
                         int rotary_dim, float* att_out);
+/* yhip_test_attention without any allocation, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. q, kcache, vcache and att_out are DEVICE pointers (layouts as in
+ * yhip_test_attention; kcache is rewritten in sink mode, pos >= max_seq_len); the work is enqueued
+ * on `stream` (a hipStream_t, NULL = the default stream) and the call returns without waiting.
+ * The split-KV partials, tickets, step parameters and rotary frequencies live in a fixed device
+ * array of the library (1 MiB of partials + 4 KiB, one per GPU, held until the process ends): the
+ * call fails with YHIP_EINVAL when n_heads * nsplit * (head_dim + 2) floats exceed 1 MiB (nsplit 0 =
+ * the default, as yhip_test_attention). Every call on a GPU shares that array, so calls that
+ * overlap on one GPU (other streams, other threads) race; calls in order on one stream do not. */
+int yhip_attention_noalloc(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
+                           int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
+                           int rotary_dim, float* att_out, void* stream);
 /* Fused pre-norm + QKV matvec + clip + RoPE + KV-cache write (src/infer.cpp:267-305).
  * q_out [nh*hd]; kcache/vcache [n_kv*hd*msl] updated in place at kv_pos(pos). */
 int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* wq, const uint16_t* wk,

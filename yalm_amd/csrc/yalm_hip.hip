@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -178,12 +179,15 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Rotary inverse frequencies, one per pair: 1 / powf(theta, j / rotary_dim) for even j < rotary_dim,
 // 0 beyond it (reference src/infer.cpp:205), computed once on the host in fp32.
-std::vector<float> make_inv_freq(int head_dim, int rotary_dim, float theta) {
-  std::vector<float> f(head_dim / 2);
+void fill_inv_freq(float* f, int head_dim, int rotary_dim, float theta) {
   for (int k = 0; k < head_dim / 2; ++k) {
     const int j = 2 * k;
     f[k] = j >= rotary_dim ? 0.f : 1.0f / powf(theta, (float)j / (float)rotary_dim);
   }
+}
+std::vector<float> make_inv_freq(int head_dim, int rotary_dim, float theta) {
+  std::vector<float> f(head_dim / 2);
+  fill_inv_freq(f.data(), head_dim, rotary_dim, theta);
   return f;
 }
 
@@ -1533,6 +1537,106 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   HIP_TRY(nullptr, hipMemcpy(att_out, dout, (size_t)n_heads * head_dim * 4, hipMemcpyDeviceToHost));
   HIP_TRY(nullptr, hipMemcpy(kcache, dk, kv * 2, hipMemcpyDeviceToHost));
   return YHIP_OK;
+}
+
+// ---- attention without allocation ----------------------------------------------------------
+// The split-KV attention's working memory (per-slice partials, per-kv-head tickets, the step
+// parameters and the rotary frequencies) in one file-scope device array: each GPU the library runs
+// on holds its own copy until the process ends. Header: tickets at 0 (64 words), StepParams at
+// 256, rotary frequencies at 512 (64 floats); partials from 4096.
+namespace {
+constexpr size_t kNaHeaderBytes = 4096;
+constexpr size_t kNaPartialBytes = (size_t)1 << 20;
+constexpr size_t kNaScratchBytes = kNaHeaderBytes + kNaPartialBytes;
+constexpr int kNaMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNaScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_dev[kNaMaxDevices] = {};  // device address of `scratch` on each GPU
+
+// The scratch array's address on the current device, looked up once per device. In host code the
+// array's name is only a stand-in: kernels and copies take this address.
+unsigned char* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNaMaxDevices) {
+    fail(nullptr, YHIP_EDEVICE, "no current HIP device (or device index above 63)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(nullptr, YHIP_EDEVICE, std::string("scratch symbol lookup: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_dev[dev] = static_cast<unsigned char*>(p);
+  }
+  return g_scratch_dev[dev];
+}
+
+struct NaSetup {
+  int pos, n_freq;
+  float inv_freq[64];
+};
+
+// Clears the tickets (the merge expects zero) and writes the step parameters and frequencies: a
+// kernel rather than memsets or copies, so the sequence also records cleanly into a graph.
+__global__ void noalloc_setup_kernel(unsigned char* base, NaSetup su) {
+  unsigned* tickets = reinterpret_cast<unsigned*>(base);
+  StepParams* params = reinterpret_cast<StepParams*>(base + 256);
+  float* freq = reinterpret_cast<float*>(base + 512);
+  const int t = threadIdx.x;
+  tickets[t] = 0u;
+  if (t < su.n_freq) freq[t] = su.inv_freq[t];
+  if (t == 0) {
+    params->token = 0;
+    params->pos = su.pos;
+    params->pad[0] = params->pad[1] = 0;
+  }
+}
+}  // namespace
+
+extern "C" int yhip_attention_noalloc(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
+                                      int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
+                                      int rotary_dim, float* att_out, void* stream) {
+  if (!q || !kcache || !vcache || !att_out || pos < 0 || max_seq_len <= kKvSinks || rotary_dim < 0 ||
+      rotary_dim > head_dim)
+    return fail(nullptr, YHIP_EINVAL, "bad argument");
+  if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
+  if (nsplit <= 0) nsplit = std::max(1, std::min(64, 256 / n_kv_heads));  // as yhip_test_attention
+  if (nsplit > 64) return fail(nullptr, YHIP_EINVAL, "nsplit must be at most 64");
+  const size_t part_bytes = (size_t)n_heads * nsplit * (head_dim + 2) * sizeof(float);
+  if (part_bytes > kNaPartialBytes)
+    return fail(nullptr, YHIP_EINVAL, "n_heads * nsplit * (head_dim + 2) floats exceed the 1 MiB attention scratch");
+  unsigned char* base = noalloc_scratch();
+  if (!base) return YHIP_EDEVICE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  NaSetup su;
+  su.pos = pos;
+  su.n_freq = head_dim / 2;
+  fill_inv_freq(su.inv_freq, head_dim, rotary_dim, rope_theta);
+  hipLaunchKernelGGL(noalloc_setup_kernel, dim3(1), dim3(64), 0, s, base, su);
+  HIP_TRY(nullptr, hipGetLastError());
+  AttnArgs t;
+  t.q = q;
+  t.kcache = kcache;
+  t.vcache = vcache;
+  t.partial = reinterpret_cast<float*>(base + kNaHeaderBytes);
+  t.tickets = reinterpret_cast<unsigned*>(base);
+  t.out = att_out;
+  t.head_dim = head_dim;
+  t.n_heads = n_heads;
+  t.n_kv_heads = n_kv_heads;
+  t.msl = max_seq_len;
+  t.nsplit = nsplit;
+  t.min_slice = 64;  // as yhip_test_attention
+  t.inv_freq = reinterpret_cast<const float*>(base + 512);
+  t.params = reinterpret_cast<const StepParams*>(base + 256);
+  return launch_attention(nullptr, t, s);
 }
 
 extern "C" int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* wq, const uint16_t* wk,

@@ -26,7 +26,7 @@ EXPORTS = (
     "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
-    "yhip_bench_gemm", "yhip_gemm_variant",
+    "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc",
 )
 
 
@@ -81,6 +81,8 @@ def lib():
         "yhip_test_gemm": (ctypes.c_int, [_u16p, _u16p, _u16p] + [ctypes.c_int] * 5 + [_f32p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
         "yhip_gemm_variant": (ctypes.c_int, [ctypes.c_int] * 4 + [_ip] * 3),
+        "yhip_attention_noalloc": (ctypes.c_int, [vp, vp, vp] + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int,
+                                                                                        vp, vp]),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
         "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
         "yhip_bench_gemm": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
