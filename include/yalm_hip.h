@@ -109,7 +109,9 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * default), "bpc_qkv" / "bpc_o" / "bpc_w13" / "bpc_w2" / "bpc_lm" (workgroups per CU of the decode
  * matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for W2; the
  * results do not depend on it), "stats" (1 = time every synchronised step on the device with HIP
- * events and reset the totals; 0 = off).
+ * events and reset the totals; 0 = off), "fuse_attn" (1 = run the decode attention inside the QKV
+ * launch for steps with at most "fuse_attn_max" cached tokens (default 1024), below max_seq_len,
+ * on the matrix-core attention's shapes; 0 = its own launch, the default, measured faster).
  * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill

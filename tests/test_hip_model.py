@@ -307,6 +307,47 @@ def test_kv_write_then_decode_long_context(path):
     hm.close()
 
 
+FUSE_SHAPES = {
+    "tiny": dict(TINY),  # head_dim 32, 4 q heads per kv head, dim 256
+    "hd64_g2": dict(TINY, dim=256, head_dim=64, n_heads=4, n_kv_heads=2, rotary_dim=64, n_layers=2),
+    "hd128_g8": dict(TINY, dim=1024, head_dim=128, n_heads=8, n_kv_heads=1, rotary_dim=128, n_layers=2),
+    "hd32_g1": dict(TINY, dim=128, head_dim=32, n_heads=4, n_kv_heads=4, rotary_dim=32, n_layers=2),
+}
+
+
+@pytest.mark.parametrize("path", ["graph", "direct"])
+@pytest.mark.parametrize("shape", list(FUSE_SHAPES))
+def test_attention_fused_into_qkv_matches_oracle(path, shape):
+    # Short contexts run the attention inside the QKV launch (the first workgroups to finish take
+    # the attention items once every q/K/V row is written); longer ones launch it separately. With
+    # the threshold at 200 tokens and slices of 64 the sequence crosses it, after running 1 to 4
+    # slices per kv head fused (their merge included).
+    cfg = FUSE_SHAPES[shape]
+    t = np_tensors(cfg, seed=55, std=0.02)
+    om, hm = _models(cfg, t, path)
+    ref = hip().HipModel(cfg, t)  # attention always in its own launch
+    use_path(ref, path)
+    ref.set_option("fuse_attn", 0)
+    hm.set_option("fuse_attn", 1)
+    hm.set_option("fuse_attn_max", 200)
+    hm.set_option("attn_min_slice", 64)
+    ref.set_option("attn_min_slice", 64)
+    rng = np.random.default_rng(56)
+    toks = rng.integers(0, cfg["vocab_size"], 230)
+    for pos, tok in enumerate(toks):
+        mode = 1 if (pos % 7 == 0 or pos > 190) else 0
+        lo = om.forward(int(tok), pos, mode)
+        lh = hm.forward(int(tok), pos, mode)
+        lr = ref.forward(int(tok), pos, mode)
+        if mode == 1:
+            assert npref.rel_l2(lh, lo) < 1e-4, pos
+            assert npref.rel_l2(lr, lo) < 1e-4, pos
+            assert npref.rel_l2(lh, lr) < 1e-4, pos
+    _check_kv(om, hm, cfg["n_layers"])
+    hm.close()
+    ref.close()
+
+
 @pytest.mark.parametrize("path", ["graph", "direct"])
 def test_mfma_attention_slice_rule_across_lengths(path):
     # The MFMA attention picks its KV slice length from the context length (one slice up to 320

@@ -46,11 +46,13 @@ struct KvFrag {
 // Buffer loads: the K/V regions of the kv head are addressed by a descriptor in scalar registers,
 // so each load takes one 32-bit lane offset plus a wave-uniform scalar offset (the dims / k-step
 // strides) instead of a 64-bit address per load; reads past the region return zero.
+// CPOL kCpolSc1: agent-coherent reads, for entries written by other workgroups of the same launch.
+template <int CPOL = 0>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, CPOL));
 }
 
-template <int HD>
+template <int HD, int CPOL = 0>
 __device__ __forceinline__ void load_kv_frag(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int msl, int t0,
                                              int m, int q, KvFrag<HD>& f) {
   // K byte offset: (2 ks + q / 2) * 16 msl * 2 + key * 32 + 16 (q % 2)
@@ -59,37 +61,41 @@ __device__ __forceinline__ void load_kv_frag(__amdgpu_buffer_rsrc_t kr, __amdgpu
     const int tk = min(t0 + 8 * (m >> 2) + 4 * j + (m & 3), msl - 1);
     const int vo = (q >> 1) * 32 * msl + tk * 32 + 16 * (q & 1);
 #pragma unroll
-    for (int ks = 0; ks < HD / 32; ++ks) f.k[j][ks] = buffer_load16(kr, vo, ks * 64 * msl);
+    for (int ks = 0; ks < HD / 32; ++ks) f.k[j][ks] = buffer_load16<CPOL>(kr, vo, ks * 64 * msl);
   }
   // V byte offset: (16 dt + m) * msl * 2 + key * 2
   const int vo = m * 2 * msl + 2 * min(t0 + 8 * q, msl - 8);
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) f.v[dt] = buffer_load16(vr, vo, dt * 32 * msl);
+  for (int dt = 0; dt < HD / 16; ++dt) f.v[dt] = buffer_load16<CPOL>(vr, vo, dt * 32 * msl);
 }
 
 template <int HD, int G, int NW>
-__global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
+struct AttnMfmaSmem {
+  float om[NW][G][HD];  // per-wave unnormalised outputs
+  float oml[NW][G][2];  // per-wave (max, sum)
+  float mrg[G][kMaxSplits][2];
+  float Ls[G];
+  unsigned last_flag;
+};
+
+// One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g. COH: q and the
+// K/V entries are read with agent-coherent loads (they were written by other workgroups of the same
+// launch: the QKV kernel with the attention fused in). DB: two tile buffers per wave.
+template <int HD, int G, int NW, bool COH, bool DB = true>
+__device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int split, const Positions& pss,
+                                               AttnMfmaSmem<HD, G, NW>& sm) {
   static_assert(HD % 32 == 0 && G >= 1 && G <= 8, "head_dim % 32, 1..8 query heads per kv head");
   constexpr int NT = 64 * NW;
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int TS = 32;  // keys per wave tile
-  if ((int)blockIdx.y >= a.nsplit) {
-    const int j = ((int)blockIdx.y - a.nsplit) * (int)gridDim.x + (int)blockIdx.x;
-    if (j < a.pf.blocks) prefetch_worker<NT>(a.pf, j);
-    return;
-  }
-  __shared__ float om[NW][G][HD];  // per-wave unnormalised outputs
-  __shared__ float oml[NW][G][2];  // per-wave (max, sum)
-  __shared__ float mrg[G][kMaxSplits][2];
-  __shared__ float Ls[G];
-  __shared__ unsigned last_flag;
+  constexpr int CPOL = COH ? kCpolSc1 : 0;
+  auto& om = sm.om;
+  auto& oml = sm.oml;
 
   // the wave index in a scalar register: per-wave tile bounds and loop exits are then uniform
   // branches rather than exec-masked ones
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int g = blockIdx.x, split = blockIdx.y;
-  const Positions pss = positions(a.params->pos, a.msl);
   const int kv_len = pss.kv_len;
   const int chunk = attn_mfma_chunk(kv_len, a.nsplit, a.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
@@ -118,8 +124,9 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
   int t0 = t_begin + TS * wave;
   if (t0 < t_end) {
     // first tile in flight before q is read
-    KvFrag<HD> cur, nxt;
-    load_kv_frag<HD>(kr, vr, a.msl, t0, col, grp, cur);
+    KvFrag<HD> cur;
+    [[maybe_unused]] KvFrag<HD> nxt;
+    load_kv_frag<HD, CPOL>(kr, vr, a.msl, t0, col, grp, cur);
 
     // q as the B operand: column col is head col (hi part) or head col - G (lo part); others zero
     u32x4 qf[KS];
@@ -130,10 +137,22 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
       const int h = used ? (lo ? col - G : col) : 0;
       const float* qp = a.q + (long)(g * G + h) * HD + 8 * grp;
       f32x4 q4[KS][2];
+      if constexpr (COH) {
+        // descriptor on the kv head's q block (wave-uniform), per-lane byte offsets
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.q + (long)g * G * HD), 0, G * HD * (int)sizeof(float), kBufferConfig);
+        const int qoff = (h * HD + 8 * grp) * (int)sizeof(float);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
-        q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
+        for (int ks = 0; ks < KS; ++ks) {
+          q4[ks][0] = load_shared4(qr, qoff + 128 * ks);
+          q4[ks][1] = load_shared4(qr, qoff + 128 * ks + 16);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
+          q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
+        }
       }
       // the head's largest |q| over the four lanes of the column (each holds 8 of every 32 dims)
       float amax = 0.f;
@@ -204,15 +223,23 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
     // Two register buffers used alternately (unrolled by two, no copies between them): while one
     // tile is used the next one's loads are in flight, and the scheduling barrier keeps them at the
     // top. The explicit wait for the current tile is free in the steady state and keeps the
-    // compiler from waiting on the in-flight tile inside the current one.
-    for (;;) {
+    // compiler from waiting on the in-flight tile inside the current one. DB false: one buffer,
+    // each tile loaded after the previous one is used (fewer registers, for short slices).
+    if constexpr (!DB) {
+      for (;;) {
+        tile(cur, t0);
+        t0 += TS * NW;
+        if (t0 >= t_end) break;
+        load_kv_frag<HD, CPOL>(kr, vr, a.msl, t0, col, grp, cur);
+      }
+    } else for (;;) {
       int tn = t0 + TS * NW;
       if (tn >= t_end) {
         tile(cur, t0);
         break;
       }
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
-      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, nxt);
+      load_kv_frag<HD, CPOL>(kr, vr, a.msl, tn, col, grp, nxt);
       __builtin_amdgcn_sched_barrier(0);
       tile(cur, t0);
       t0 = tn;
@@ -222,7 +249,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
         break;
       }
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, cur);
+      load_kv_frag<HD, CPOL>(kr, vr, a.msl, tn, col, grp, cur);
       __builtin_amdgcn_sched_barrier(0);
       tile(nxt, t0);
       t0 = tn;
@@ -274,7 +301,72 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
     }
   }
   if (active == 1) return;
-  attn_merge_slices<HD, G, NT, false>(a, g, active, tid, mrg, Ls, last_flag);
+  attn_merge_slices<HD, G, NT, false>(a, g, active, tid, sm.mrg, sm.Ls, sm.last_flag);
 }
 
+template <int HD, int G, int NW>
+__global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
+  if ((int)blockIdx.y >= a.nsplit) {
+    const int j = ((int)blockIdx.y - a.nsplit) * (int)gridDim.x + (int)blockIdx.x;
+    if (j < a.pf.blocks) prefetch_worker<64 * NW>(a.pf, j);
+    return;
+  }
+  __shared__ AttnMfmaSmem<HD, G, NW> sm;
+  attn_mfma_body<HD, G, NW, false>(a, blockIdx.x, blockIdx.y, positions(a.params->pos, a.msl), sm);
+}
+
+// ------------------------------------------------------------------------------------------
+// QKV matvec with the decode attention fused in (short contexts, no sink rotation). Every
+// workgroup first streams its rows of [Wq;Wk;Wv] (RMSNorm, clip, RoPE, fp16 K/V at kv_pos;
+// q and the K/V entries written through to memory), waits until its stores are complete and counts
+// itself done. The attention items -- kv head i % n_kv_heads, slice i / n_kv_heads -- belong to the
+// last workgroups of the grid (item i to workgroup nblk - 1 - i): with the rows dealt round-robin
+// those hold one row group per wave and finish first. They wait until every workgroup has counted
+// itself done (bounded wait: a time-out sets *abort_flag and the host reports an error), then run
+// their item. This removes the attention launch, its boundary and its start-up latency.
+// done: kQkvDoneParts zeroed counters kQkvDoneStride words apart; workgroup b counts itself on
+// counter b % kQkvDoneParts (its XCD), so the completions do not queue behind one address.
+// ------------------------------------------------------------------------------------------
+constexpr int kQkvDoneParts = 8, kQkvDoneStride = 64;
+
+// Thread 0 polls until the parts of a split counter sum to `target` (bounded, as wait_count).
+__device__ __forceinline__ void wait_split_count(const unsigned* c, unsigned target, unsigned* abort_flag) {
+  if (threadIdx.x == 0) {
+    unsigned spins = 0;
+    for (;;) {
+      unsigned sum = 0;
+#pragma unroll
+      for (int k = 0; k < kQkvDoneParts; ++k)
+        sum += __hip_atomic_load(const_cast<unsigned*>(c + k * kQkvDoneStride), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (sum >= target) break;
+      __builtin_amdgcn_s_sleep(1);
+      if ((++spins & 255u) == 0 &&
+          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <int KC, int HD, int G>
+__global__ void __launch_bounds__(kBlock) qkv_attn_kernel(MatvecArgs m, AttnArgs a, unsigned* done,
+                                                          unsigned* abort_flag) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ AttnMfmaSmem<HD, G, kWavesPerBlock> sm;
+  matvec_body<KC, 2, kEpiQkvRope, false>(m, blockIdx.x, gridDim.x, lds, [] {});
+  publish();  // this thread's q / K / V stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(done + (blockIdx.x % kQkvDoneParts) * kQkvDoneStride, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  const Positions pss = positions(a.params->pos, a.msl);
+  const int chunk = attn_mfma_chunk(pss.kv_len, a.nsplit, a.min_slice);
+  const int items = a.n_kv_heads * ((pss.kv_len + chunk - 1) / chunk);
+  const int item = (int)gridDim.x - 1 - (int)blockIdx.x;
+  if (item >= items) return;
+  wait_split_count(done, gridDim.x, abort_flag);  // every row of q, K and V is written
+  attn_mfma_body<HD, G, kWavesPerBlock, true, false>(a, item % a.n_kv_heads, item / a.n_kv_heads, pss, sm);
+}
 }  // namespace yk

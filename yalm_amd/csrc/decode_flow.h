@@ -30,8 +30,6 @@
 
 namespace yk {
 
-constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait gives up (about a second)
-
 // All layers share one layout: layer l's weights start at wbase + l * stride, its K cache at
 // kv + 2 l kv_elems and its V cache right after.
 struct LayerLayout {
@@ -78,23 +76,6 @@ struct FlowArgs {
   unsigned launch;
   int nb[6];  // workgroups per phase: QKV, ATT, O, W13, W2, lm_head
 };
-
-// Thread 0 polls until *c >= target (bounded; a time-out sets the abort flag, after which every
-// wait returns at once and the host reports the error); the workgroup waits at the barrier.
-__device__ __forceinline__ void wait_count(const unsigned* c, unsigned target, unsigned* abort_flag) {
-  if (threadIdx.x == 0) {
-    unsigned spins = 0;
-    while (__hip_atomic_load(const_cast<unsigned*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if ((++spins & 255u) == 0 &&
-          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
 
 // Matvec phase with the row-length specialisations the model shapes use.
 template <int R, EpiKind EPI, class Wait>

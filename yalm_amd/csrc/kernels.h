@@ -150,6 +150,25 @@ __device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait gives up (about a second)
+
+// Thread 0 polls until *c >= target (bounded; a time-out sets the abort flag, after which every
+// wait returns at once and the host reports the error); the workgroup waits at the barrier.
+__device__ __forceinline__ void wait_count(const unsigned* c, unsigned target, unsigned* abort_flag) {
+  if (threadIdx.x == 0) {
+    unsigned spins = 0;
+    while (__hip_atomic_load(const_cast<unsigned*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if ((++spins & 255u) == 0 &&
+          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 constexpr int kBufferConfig = 0x00020000;  // raw buffer descriptor word 3 on gfx9-family GPUs
 constexpr int kCpolSc1 = 16;               // cache-policy operand: sc1, the agent-scope coherent load
 
@@ -214,6 +233,9 @@ struct MatvecArgs {
   // row-loop statistics for the lm_head: running (max, index) of the outputs, tie rule of
   // src/sampler.cpp:27-38, kept per wave (argmax fused into the last matvec)
   int track_max;
+  // QKV epilogue: 1 = q and the K/V of this position are written through to memory (agent-scope
+  // stores), for a later workgroup of the same launch that reads them (the fused attention)
+  int coh_store;
 };
 
 // Loads of one row segment for this lane: chunk c = lane + 64*u, u < KC (KC = K/512 when > 0).
@@ -305,8 +327,13 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
     }
     if (!store) return;
     if (i < a.q_dim) {
-      st_act<COH>(a.out + i, v0);
-      st_act<COH>(a.out + i + 1, v1);
+      if (COH || a.coh_store) {
+        store_shared(a.out + i, v0);
+        store_shared(a.out + i + 1, v1);
+      } else {
+        a.out[i] = v0;
+        a.out[i + 1] = v1;
+      }
     } else {
       const Positions ps = positions(pos, a.msl);
       const bool is_k = i < a.q_dim + a.kv_dim;
@@ -317,7 +344,16 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
       const uint16_t h1 = __builtin_bit_cast(uint16_t, (f16)v1);
       if constexpr (COH)  // the same launch's attention reads this position from the side buffer
         store_shared_u32(a.kvcur + (is_k ? 0 : a.kv_dim / 2) + ik / 2, (uint32_t)h0 | ((uint32_t)h1 << 16));
-      if (is_k) {
+      if (a.coh_store) {  // dims j, j + 1 (j even) are adjacent in K's 16-dim chunk: one word
+        if (is_k)
+          store_shared_u32(reinterpret_cast<uint32_t*>(a.kcache + head + k_cache_idx(j, ps.kv_pos, a.msl)),
+                           (uint32_t)h0 | ((uint32_t)h1 << 16));
+        else {
+          __hip_atomic_store(a.vcache + head + (long)j * a.msl + ps.kv_pos, h0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.vcache + head + (long)(j + 1) * a.msl + ps.kv_pos, h1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else if (is_k) {
         a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = h0;
         a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = h1;
       } else {

@@ -54,12 +54,13 @@ struct LayerW {
 // reference src/infer.cpp:205-208), written before each step so that a captured graph stays static.
 // It also zeroes the packed key the fused lm_head argmax posts to.
 __global__ void set_params_kernel(StepParams* p, int token, int pos, const float* inv_freq, float* rope_cs, int half,
-                                  unsigned long long* argmax_key) {
+                                  unsigned long long* argmax_key, unsigned* qkv_done, int n_layers) {
   if (threadIdx.x == 0) {
     p->token = token;
     p->pos = pos;
     *argmax_key = 0ull;
   }
+  for (int i = threadIdx.x; i < n_layers * kQkvDoneParts; i += blockDim.x) qkv_done[kQkvDoneStride * i] = 0u;
   fill_rope_table(inv_freq, rope_cs, half, pos);
 }
 
@@ -117,7 +118,14 @@ struct yhip_ctx {
   int prefetch_o = 0, prefetch_w13_mb = 0, prefetch_blocks = 256;
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   unsigned* pf_sink = nullptr;
-  hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // hydrate, logits, argmax
+  // captured steps: [mode: hydrate, logits, argmax][attention: separate launch, fused into QKV]
+  hipGraphExec_t graph[3][2] = {};
+  // decode attention fused into the QKV launch for contexts up to fuse_attn_max tokens (opt-in:
+  // measured slower than the separate launch on MI355X, see the design notes)
+  bool fuse_attn = false;
+  int fuse_attn_max = 1024;
+  unsigned* qkv_done = nullptr;    // per layer: kQkvDoneParts counters of QKV workgroups done (zeroed every step)
+  unsigned* step_abort = nullptr;  // a bounded wait of a fused launch timed out
 
   // single-launch decode (decode_flow.h)
   const void* flow_fn = nullptr;  // instantiation for this shape, or null when the shape has none
@@ -330,9 +338,72 @@ int check_attn_shape(yhip_ctx* ctx, int hd, int nh, int nkv) {
   return YHIP_OK;
 }
 
+// ---- QKV with the attention fused in ----------------------------------------------------------
+// Attention items (kv head x KV slice) of a step at position pos, as the kernel counts them.
+int attn_items_at(const yhip_ctx* ctx, int pos) {
+  const int kv_len = std::min(pos + 1, ctx->c.max_seq_len);
+  const int chunk = attn_mfma_chunk(kv_len, ctx->attn_splits, attn_min_slice_for(ctx, true));
+  return ctx->c.n_kv_heads * ((kv_len + chunk - 1) / chunk);
+}
+
+int qkv_blocks(const yhip_ctx* ctx) {
+  const int groups = (ctx->q_dim() + 2 * ctx->kv_dim()) / 2;
+  const int bpc = ctx->mv_bpc[0] > 0 ? ctx->mv_bpc[0] : default_bpc(ctx->c.dim, kEpiQkvRope);
+  return std::max(1, std::min((groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * bpc));
+}
+
+bool fused_attention_shape(const yhip_config& c) {
+  const int G = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
+  return (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+         (16 + (size_t)c.dim + c.head_dim) * sizeof(float) <= 65536;
+}
+
+// The step at pos runs the fused launch when the option is on, the MFMA attention applies, there is
+// no sink rotation (pos < max_seq_len), the context is short, and every attention item finds a QKV
+// workgroup.
+bool fused_attention_at(const yhip_ctx* ctx, int pos) {
+  return ctx->fuse_attn && attn_uses_mfma(ctx) && fused_attention_shape(ctx->c) && pos < ctx->c.max_seq_len &&
+         pos + 1 <= ctx->fuse_attn_max && attn_items_at(ctx, pos) <= qkv_blocks(ctx);
+}
+
+template <int KC, int HD, int G>
+void go_qkv_attn(const MatvecArgs& a, const AttnArgs& t, unsigned* done, unsigned* abort_flag, int blocks,
+                 hipStream_t s) {
+  const size_t lds = (16 + (size_t)a.K + a.head_dim) * sizeof(float);
+  hipLaunchKernelGGL((qkv_attn_kernel<KC, HD, G>), dim3(blocks), dim3(kBlock), lds, s, a, t, done, abort_flag);
+}
+
+int launch_qkv_attn(yhip_ctx* ctx, const MatvecArgs& a, const AttnArgs& t, unsigned* done, hipStream_t s) {
+  const int blocks = qkv_blocks(ctx), G = t.n_heads / t.n_kv_heads;
+  unsigned* ab = ctx->step_abort;
+  if (a.K == 4096 && t.head_dim == 128 && G == 4) {
+    go_qkv_attn<8, 128, 4>(a, t, done, ab, blocks, s);
+  } else {
+    switch (t.head_dim * 16 + G) {
+      case 32 * 16 + 1: go_qkv_attn<0, 32, 1>(a, t, done, ab, blocks, s); break;
+      case 32 * 16 + 2: go_qkv_attn<0, 32, 2>(a, t, done, ab, blocks, s); break;
+      case 32 * 16 + 4: go_qkv_attn<0, 32, 4>(a, t, done, ab, blocks, s); break;
+      case 32 * 16 + 8: go_qkv_attn<0, 32, 8>(a, t, done, ab, blocks, s); break;
+      case 64 * 16 + 1: go_qkv_attn<0, 64, 1>(a, t, done, ab, blocks, s); break;
+      case 64 * 16 + 2: go_qkv_attn<0, 64, 2>(a, t, done, ab, blocks, s); break;
+      case 64 * 16 + 4: go_qkv_attn<0, 64, 4>(a, t, done, ab, blocks, s); break;
+      case 64 * 16 + 8: go_qkv_attn<0, 64, 8>(a, t, done, ab, blocks, s); break;
+      case 128 * 16 + 1: go_qkv_attn<0, 128, 1>(a, t, done, ab, blocks, s); break;
+      case 128 * 16 + 2: go_qkv_attn<0, 128, 2>(a, t, done, ab, blocks, s); break;
+      case 128 * 16 + 4: go_qkv_attn<0, 128, 4>(a, t, done, ab, blocks, s); break;
+      case 128 * 16 + 8: go_qkv_attn<0, 128, 8>(a, t, done, ab, blocks, s); break;
+      default: return fail(ctx, YHIP_EINVAL, "fused attention: unsupported shape");
+    }
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("fused QKV + attention launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
-int enqueue_step(yhip_ctx* ctx, int mode) {
+// fused: the attention runs inside the QKV launch (fused_attention_at).
+int enqueue_step(yhip_ctx* ctx, int mode, int fused) {
   const yhip_config& c = ctx->c;
   hipStream_t s = ctx->stream;
   const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
@@ -363,7 +434,6 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
       a.emb = ctx->embed;
       a.emb_out = ctx->x;
     }
-    if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
     // 2. attention
     AttnArgs t;
     t.q = ctx->q;
@@ -380,7 +450,13 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
     t.min_slice = attn_min_slice_for(ctx, attn_uses_mfma(ctx));
     t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
-    if (ctx->prefetch_o || ctx->prefetch_w13_mb) {
+    if (fused) {
+      a.coh_store = 1;
+      if ((rc = launch_qkv_attn(ctx, a, t, ctx->qkv_done + (size_t)l * kQkvDoneParts * kQkvDoneStride, s))) return rc;
+    } else {
+      if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
+    }
+    if (!fused && (ctx->prefetch_o || ctx->prefetch_w13_mb)) {
       // O is read by its matvec in 64 KB pieces (8 rows of q_dim halves per workgroup for q_dim
       // 4096), W1/W3 in 32 KB pieces per matrix; chunk i of a range feeds consumer workgroup i.
       const long o_units = (long)c.dim * qd * 2 / 16;
@@ -394,7 +470,7 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
       t.pf.magic = 0x9E3779B9u;
       t.pf.sink = ctx->pf_sink;
     }
-    if ((rc = launch_attention(ctx, t, s))) return rc;
+    if (!fused && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
     a = mv_base();
     a.w0 = L.wo;
@@ -462,6 +538,8 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
       hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     HIP_TRY(ctx, hipGetLastError());
   }
+  if (fused)  // the fused launches' wait time-out flag, checked after the caller's synchronisation
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (mode == 1) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
@@ -474,10 +552,11 @@ int enqueue_step(yhip_ctx* ctx, int mode) {
 }
 
 void drop_graphs(yhip_ctx* ctx) {
-  for (auto& g : ctx->graph) {
-    if (g) hipGraphExecDestroy(g);
-    g = nullptr;
-  }
+  for (auto& per_mode : ctx->graph)
+    for (auto& g : per_mode) {
+      if (g) hipGraphExecDestroy(g);
+      g = nullptr;
+    }
 }
 
 // ---- single-launch decode ---------------------------------------------------------------------
@@ -573,6 +652,15 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   return YHIP_OK;
 }
 
+// After a synchronised step: a wait of a fused QKV + attention launch that timed out poisons it.
+int check_step_abort(yhip_ctx* ctx) {
+  if (ctx->argmax_host[4] == 0) return YHIP_OK;
+  ctx->argmax_host[4] = 0;
+  hipMemsetAsync(ctx->step_abort, 0, sizeof(unsigned), ctx->stream);
+  hipStreamSynchronize(ctx->stream);
+  return fail(ctx, YHIP_EDEVICE, "fused QKV + attention: a dependency wait timed out");
+}
+
 // After a synchronised single-launch step: a wait that timed out poisons the step.
 int check_flow_status(yhip_ctx* ctx) {
   if (!ctx->use_flow || ctx->argmax_host[1] == 0) return YHIP_OK;
@@ -617,27 +705,30 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   if (ctx->use_flow) return launch_flow_step(ctx, token, pos, mode);
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->params, token, pos,
-                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key);
+                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key, ctx->qkv_done,
+                     c.n_layers);
   HIP_TRY(ctx, hipGetLastError());
-  if (!ctx->use_graph) return enqueue_step(ctx, mode);
-  if (!ctx->graph[mode]) {
+  const int fused = fused_attention_at(ctx, pos) ? 1 : 0;
+  if (!ctx->use_graph) return enqueue_step(ctx, mode, fused);
+  hipGraphExec_t& ge = ctx->graph[mode][fused];
+  if (!ge) {
     hipGraph_t g = nullptr;
     HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(ctx, mode);
+    int rc = enqueue_step(ctx, mode, fused);
     hipError_t e = hipStreamEndCapture(ctx->stream, &g);
     if (rc) {
       if (g) hipGraphDestroy(g);
       return rc;
     }
     if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("graph capture: ") + hipGetErrorString(e));
-    e = hipGraphInstantiate(&ctx->graph[mode], g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e != hipSuccess) {
-      ctx->graph[mode] = nullptr;
+      ge = nullptr;
       return fail(ctx, YHIP_EDEVICE, std::string("graph instantiate: ") + hipGetErrorString(e));
     }
   }
-  HIP_TRY(ctx, hipGraphLaunch(ctx->graph[mode], ctx->stream));
+  HIP_TRY(ctx, hipGraphLaunch(ge, ctx->stream));
   return YHIP_OK;
 }
 
@@ -1000,7 +1091,9 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
                a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
                a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
                a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
-               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_pfs = atake(1024 * 4);
+               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_pfs = atake(1024 * 4),
+               a_qd = atake((size_t)std::max(1, c.n_layers) * kQkvDoneParts * kQkvDoneStride * sizeof(unsigned)),
+               a_sa = atake(256);
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -1020,6 +1113,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->best_v = (float*)(ctx->abase + a_bv);
   ctx->best_i = (int*)(ctx->abase + a_bi);
   ctx->pf_sink = (unsigned*)(ctx->abase + a_pfs);
+  ctx->qkv_done = (unsigned*)(ctx->abase + a_qd);
+  ctx->step_abort = (unsigned*)(ctx->abase + a_sa);
   {
     const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
     if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -1185,6 +1280,7 @@ extern "C" int yhip_forward(yhip_ctx* ctx, int token, int pos, int mode, float* 
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   collect_stats(ctx);
   if (int rc = check_flow_status(ctx)) return rc;
+  if (int rc = check_step_abort(ctx)) return rc;
   if (logits_host != ctx->logits_host) memcpy(logits_host, ctx->logits_host, (size_t)ctx->c.vocab_size * 4);
   return YHIP_OK;
 }
@@ -1196,6 +1292,7 @@ extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   collect_stats(ctx);
   if (int rc = check_flow_status(ctx)) return rc;
+  if (int rc = check_step_abort(ctx)) return rc;
   if (!ctx->use_flow && ctx->c.vocab_size % 2 == 0) {  // the fused lm_head's packed key (argmax_key)
     unsigned long long key;
     memcpy(&key, ctx->argmax_host + 2, sizeof(key));
@@ -1322,6 +1419,11 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     ctx->attn_splits = value;
   } else if (!strcmp(key, "attn_mfma")) {
     ctx->attn_mfma = value != 0;
+  } else if (!strcmp(key, "fuse_attn")) {
+    ctx->fuse_attn = value != 0;
+  } else if (!strcmp(key, "fuse_attn_max")) {
+    if (value < 0) return fail(ctx, YHIP_EINVAL, "fuse_attn_max must be >= 0");
+    ctx->fuse_attn_max = value;
   } else if (!strcmp(key, "prefetch_o")) {
     ctx->prefetch_o = value != 0;
   } else if (!strcmp(key, "prefetch_w13_mb")) {
