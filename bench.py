@@ -8,9 +8,11 @@ Workloads (synthetic, seeded; no checkpoint download):
           K greedy tokens (default 120). This is the headline line.
   long    same model; a 3200-token prompt prefilled in one batched call (MFMA GEMMs + causal MFMA
           attention; reported separately as prefill tok/s, TFLOP/s and matrix-core utilisation),
-          then K greedy tokens at kv ~3200.
-  attn    same model at ctx 16448 with the KV cache pre-filled ~N(0,1) to 16384 positions, then K
-          greedy tokens at kv ~16400.
+          then 30 greedy tokens at kv ~3200.
+  attn    same model at ctx 16448 with the KV cache pre-filled ~N(0,1) on the device to 16384
+          positions, then 64 greedy tokens at kv ~16400.
+Without --workload the run is the headline decode line with the long and attn workloads appended as
+extra keys ("long", "attn"), each with its own step_roofline.
 
 A step is one decode token: the reference loop's sample -> Model::forward (src/main.cpp:182-192),
 greedy, with the argmax taken on the device. W untimed warm-up steps run first on a throwaway
@@ -21,8 +23,10 @@ Printed JSON line extras:
   roofline      the dominant kernel (fused RMSNorm + W1/W3 + SwiGLU matvec, 234.9 MB of fp16 weights
                 per launch) timed live with HIP events on its launch stream over rotating weight copies
   step_roofline algorithmic bytes per token (all weights once + K/V read + K/V write) / step time
-  cpu_baseline  the CPU oracle (a restatement of the reference -d cpu path, OpenMP over all host
-                cores) on the same host weights, over a bounded sample of the same workload
+  cpu_baseline  the CPU oracle (a restatement of the reference -d cpu path, OpenMP over the host
+                cores given to this process) on the same host weights, over a bounded sample of the
+                decode workload: decode tok/s, and the reference's own figure (prompt + generated
+                tokens over hydrate + decode time, src/main.cpp:194-210)
 """
 from __future__ import annotations
 
@@ -32,7 +36,13 @@ import os
 import sys
 import time
 
-import numpy as np
+# OpenMP placement of the CPU baseline, read by the OpenMP runtime when it first loads (with the
+# native libraries below): threads on cores, packed. The thread count is the environment's own
+# (OMP_NUM_THREADS, else the runtime's default of one per logical CPU of this process).
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
+import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -62,11 +72,56 @@ def bytes_per_token(kv_len):
     return WEIGHT_BYTES + KV_BYTES_PER_POS * kv_len + KV_BYTES_PER_POS
 
 
+def step_roofline(kv_mean, tok_s):
+    b = bytes_per_token(kv_mean)
+    gbs = b * tok_s / 1e9
+    return {"bytes_per_token": int(b), "achieved_GBps": round(gbs, 1), "peak_GBps": PEAK_GBS,
+            "frac": round(gbs / PEAK_GBS, 4), "kv_len_mean": kv_mean}
+
+
+def host_cpu():
+    """CPU model, logical CPUs and physical cores this process may run on, and the OpenMP settings.
+    Called at start-up: once the OpenMP runtime binds the main thread, its affinity is one core."""
+    model = None
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not model:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            with open(base + "physical_package_id") as f1, open(base + "core_id") as f2:
+                cores.add((f1.read().strip(), f2.read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    return {"model": model, "logical_cpus": len(cpus), "physical_cores": len(cores),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+            "omp_places": os.environ.get("OMP_PLACES")}
+
+
+HOST_CPU = host_cpu()
+
+
 def cpu_baseline(session, cfg, prompt, gpu_tokens, budget_s):
     """The oracle on the host cores: hydrate the prompt, then greedy decode until the budget ends."""
     from oracle import binding as O  # the checker, timed here as the CPU baseline
-    ocfg = dict(cfg)
-    om = O.OracleModel(ocfg, session.tensors())
+    om = O.OracleModel(dict(cfg), session.tensors())
     t0 = time.perf_counter()
     lg = None
     for i, tok in enumerate(prompt):
@@ -89,17 +144,79 @@ def cpu_baseline(session, cfg, prompt, gpu_tokens, budget_s):
         if a != b:
             break
         match += 1
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    hc = HOST_CPU
+    threads = int(hc["omp_num_threads"] or hc["logical_cpus"])
     return {
         "value": round(steps / spent, 4) if spent > 0 else None,
         "unit": "tok/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
         "sample": f"{len(prompt)}-token prompt hydrated ({hydrate:.1f} s), then {steps} greedy decode steps "
                   f"timed ({spent:.1f} s) on the same weights; greedy tokens equal to the GPU's for the first "
                   f"{match} of {steps}",
+        "reference_style_tok_s": round((len(prompt) + steps) / (hydrate + spent), 4),
+        "host": hc,
+        "threads": threads,
         "greedy_match": match,
     }
+
+
+def timed_steps(view, first_tok, start_pos, n):
+    """n greedy steps on the device from start_pos; per-step wall time."""
+    toks, secs = [], []
+    tok = first_tok
+    for i in range(n):
+        s = time.perf_counter()
+        tok = view.forward_argmax(tok, start_pos + i)
+        secs.append(time.perf_counter() - s)
+        toks.append(tok)
+    return np.array(toks), np.array(secs)
+
+
+def run_long(hip, host, ctxp, cfg, steps=30, n_prompt=3200):
+    """3200-token batched prefill, then greedy decode at kv ~3200 (the long-context workload)."""
+    view = hip.HipModel.attach(ctxp, cfg)
+    prompt = host.uniform_ids(n_prompt, 3200, cfg["vocab_size"])
+    view.prefill(prompt[:256])  # warm-up (kernels loaded, workspace sized)
+    view.prefill(prompt)
+    t0 = time.perf_counter()
+    lg = view.prefill(prompt)
+    pf_s = time.perf_counter() - t0
+    fl = prefill_flops(cfg, n_prompt)
+    prefill = {"tokens": n_prompt, "ms": round(pf_s * 1e3, 3), "tok_s": round(n_prompt / pf_s, 1),
+               "tflops": round(fl / pf_s / 1e12, 1), "mfma_frac": round(fl / pf_s / 1e12 / PEAK_FP16_TFLOPS, 4),
+               "flops": fl, "peak_tflops": PEAK_FP16_TFLOPS}
+    log(f"[bench] long: prefill {n_prompt} tokens {pf_s * 1e3:.1f} ms = {n_prompt / pf_s:.0f} tok/s, "
+        f"{fl / pf_s / 1e12:.0f} TFLOP/s ({100 * fl / pf_s / 1e12 / PEAK_FP16_TFLOPS:.1f}% of the fp16 peak)")
+    first = int(np.argmax(lg))
+    timed_steps(view, first, n_prompt, 3)  # warm-up at this context length
+    lg = view.prefill(prompt)  # the cache as the timed decode expects it
+    toks, secs = timed_steps(view, int(np.argmax(lg)), n_prompt, steps)
+    tok_s = steps / float(np.sum(secs))
+    kv_mean = n_prompt + (steps - 1) / 2.0 + 1
+    log(f"[bench] long: decode {tok_s:.1f} tok/s at kv ~{kv_mean:.0f}")
+    return {"workload": "Mistral-7B-shape fp16: 3200-token batched prefill, then greedy decode, ctx 4096",
+            "prefill": prefill, "decode_steps": steps, "decode_tok_s": round(tok_s, 2),
+            "decode_ms_per_step": round(1e3 / tok_s, 4), "step_roofline": step_roofline(kv_mean, tok_s)}
+
+
+def run_attn(hip, host, sess, cfg, steps=64, fill=16384, ctx_len=16448):
+    """KV cache pre-filled on the device to 16384 positions, greedy decode at kv ~16400."""
+    c16 = dict(cfg, max_seq_len=ctx_len)
+    t0 = time.perf_counter()
+    m = hip.HipModel(c16, sess.tensors())
+    m.kv_fill_normal(fill, 16384)
+    log(f"[bench] attn: context {ctx_len} set up, KV pre-filled to {fill} in {time.perf_counter() - t0:.1f} s")
+    first = int(host.uniform_ids(1, 16385, cfg["vocab_size"])[0])
+    timed_steps(m, first, fill, 3)  # warm-up (rewrites the same positions as the timed run)
+    toks, secs = timed_steps(m, first, fill, steps)
+    m.close()
+    tok_s = steps / float(np.sum(secs))
+    kv_mean = fill + (steps - 1) / 2.0 + 1
+    log(f"[bench] attn: decode {tok_s:.1f} tok/s at kv ~{kv_mean:.0f}")
+    return {"workload": "Mistral-7B-shape fp16 decode over a KV cache pre-filled to 16384, ctx 16448",
+            "decode_steps": steps, "decode_tok_s": round(tok_s, 2), "decode_ms_per_step": round(1e3 / tok_s, 4),
+            "step_roofline": step_roofline(kv_mean, tok_s)}
 
 
 def main():
@@ -107,7 +224,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", choices=["decode", "long", "attn"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "long", "attn"], default=None,
+                    help="one workload only (default: the decode headline with long and attn as extra keys)")
     ap.add_argument("--path", choices=["graph", "single", "direct"], default="graph",
                     help="graph: per-op kernels replayed from a captured hipGraph; single: one launch per token "
                          "(dataflow of workgroups); direct: the per-op kernels launched one by one")
@@ -135,15 +253,13 @@ def main():
         print(json.dumps({"kernel": args.profile_kernel, "us_per_launch": round(us, 3), "reps": args.kernel_reps}))
         return
 
-    wl = args.workload
+    wl = args.workload or "decode"
+    extras = args.workload is None
     steps = args.steps if args.steps is not None else {"decode": 120, "long": 30, "attn": 64}[wl]
-    ctx_len = 16448 if wl == "attn" else 4096
-    n_prompt = {"decode": 32, "long": 3200, "attn": 1}[wl]
-    prompt_seed = {"decode": 32, "long": 3200, "attn": 16385}[wl]
     shape = dict(host.MISTRAL_7B)
 
     t0 = time.perf_counter()
-    sess = host.Session.synthetic(shape, context=ctx_len)
+    sess = host.Session.synthetic(shape, context=4096)
     cfg = sess.config()
     log(f"[bench] synthetic Mistral-7B-shape model built in {time.perf_counter() - t0:.1f} s")
     t0 = time.perf_counter()
@@ -160,89 +276,42 @@ def main():
         if hip.lib().yhip_set_option(ctxp, key, val) != 0:
             raise RuntimeError(hip.lib().yhip_last_error(ctxp).decode())
 
-    prompt = host.uniform_ids(n_prompt, prompt_seed, cfg["vocab_size"])
-    start_pos = 0
-    if wl == "attn":
-        # KV cache pre-filled ~N(0,1) fp16 at positions [0, 16384) for every layer, written into the
-        # reference layout through the C-ABI; decoding starts at position 16384.
-        n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-        fill_pos = 16384
-        rng = np.random.default_rng(16384)
-        for layer in range(cfg["n_layers"]):
-            k = rng.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
-            v = rng.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
-            hd, msl = cfg["head_dim"], cfg["max_seq_len"]
-            # zero the slots past the prefill in both layouts (positions >= fill_pos)
-            kk = k.reshape(cfg["n_kv_heads"], hd // 16, msl, 16)
-            kk[:, :, fill_pos:, :] = 0
-            vv = v.reshape(cfg["n_kv_heads"], hd, msl)
-            vv[:, :, fill_pos:] = 0
-            rc = hip.lib().yhip_kv_write(ctxp, layer, k.ctypes.data_as(hip._u16p), v.ctypes.data_as(hip._u16p))
-            if rc != 0:
-                raise RuntimeError(hip.lib().yhip_last_error(ctxp).decode())
-        start_pos = fill_pos
-        log(f"[bench] KV cache pre-filled to {fill_pos} positions")
-
-    prefill = None
     if wl == "long":
-        view = hip.HipModel.attach(ctxp, cfg)
-        view.prefill(prompt[:256])  # warm-up (kernels loaded, workspace sized)
-        view.prefill(prompt)
-        t0 = time.perf_counter()
-        lg = view.prefill(prompt)
-        pf_s = time.perf_counter() - t0
-        fl = prefill_flops(cfg, n_prompt)
-        prefill = {"tokens": n_prompt, "seconds": round(pf_s, 5), "tok_s": round(n_prompt / pf_s, 1),
-                   "tflops": round(fl / pf_s / 1e12, 1), "mfma_frac": round(fl / pf_s / 1e12 / PEAK_FP16_TFLOPS, 4),
-                   "flops": fl, "peak_tflops": PEAK_FP16_TFLOPS}
-        log(f"[bench] prefill {n_prompt} tokens: {pf_s * 1e3:.1f} ms = {n_prompt / pf_s:.0f} tok/s, "
-            f"{fl / pf_s / 1e12:.0f} TFLOP/s ({100 * fl / pf_s / 1e12 / PEAK_FP16_TFLOPS:.1f}% of fp16 peak)")
-        first_tok = int(np.argmax(lg))
+        res = run_long(hip, host, ctxp, cfg, steps)
+        print(json.dumps({"metric": METRIC, "value": res["decode_tok_s"], "unit": "tok/s", "n_gpus": 1,
+                          "steps": steps, "warmup": 3, "ms_per_step": res["decode_ms_per_step"],
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+                          "data": "synthetic", "config": {"workload": res["workload"], "path": args.path}, **res}))
+        sess.close()
+        return
+    if wl == "attn":
+        res = run_attn(hip, host, sess, cfg, steps)
+        print(json.dumps({"metric": METRIC, "value": res["decode_tok_s"], "unit": "tok/s", "n_gpus": 1,
+                          "steps": steps, "warmup": 3, "ms_per_step": res["decode_ms_per_step"],
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+                          "data": "synthetic", "config": {"workload": res["workload"], "path": args.path}, **res}))
+        sess.close()
+        return
 
-    def run(n_steps):
-        if wl == "long":
-            # greedy decode from the prefilled cache
-            toks, secs = [], []
-            tok = first_tok
-            view = hip.HipModel.attach(ctxp, cfg)
-            for i in range(n_steps):
-                s = time.perf_counter()
-                tok = view.forward_argmax(tok, n_prompt + i)
-                secs.append(time.perf_counter() - s)
-                toks.append(tok)
-            return np.array(toks), np.array(secs), 0.0
-        if wl != "attn":
-            return sess.generate(prompt, n_steps, temperature=0.0, device_argmax=True)
-        # decode directly from position 16384 with greedy argmax on the device
-        toks, secs = [], []
-        tok = int(prompt[0])
-        view = hip.HipModel.attach(ctxp, cfg)
-        for i in range(n_steps):
-            s = time.perf_counter()
-            tok = view.forward_argmax(tok, start_pos + i)
-            secs.append(time.perf_counter() - s)
-            toks.append(tok)
-        return np.array(toks), np.array(secs), 0.0
-
+    # ---- the headline: 32 prompt ids, then greedy decode at ctx 4096 ----
+    n_prompt = 32
+    prompt = host.uniform_ids(n_prompt, 32, cfg["vocab_size"])
     log(f"[bench] warm-up: {args.warmup} steps")
-    run(max(args.warmup, 1))
+    sess.generate(prompt, max(args.warmup, 1), temperature=0.0, device_argmax=True)
     log(f"[bench] timed: {steps} steps")
     view = hip.HipModel.attach(ctxp, cfg)
     view.set_option("stats", 1)  # HIP events around each step's kernels on the context's stream
-    toks, secs, hydrate_s = run(steps)
+    toks, secs, hydrate_s = sess.generate(prompt, steps, temperature=0.0, device_argmax=True)
     dev_us, dev_steps = view.step_stats()
     view.set_option("stats", 0)
     assert len(secs) == steps, "decode stopped early"
     total = float(np.sum(secs))
     tok_s = steps / total
-    first = start_pos + n_prompt
-    kv_mean = first + (steps - 1) / 2.0 + 1
-    step_bytes = bytes_per_token(kv_mean)
-    step_gbs = step_bytes * tok_s / 1e9
-    log(f"[bench] {tok_s:.1f} tok/s ({1e3 * total / steps:.3f} ms/step), {step_gbs:.0f} GB/s algorithmic")
-
-    # device time per timed step (HIP events on the decode stream)
+    kv_mean = n_prompt + (steps - 1) / 2.0 + 1
+    sr = step_roofline(kv_mean, tok_s)
+    log(f"[bench] {tok_s:.1f} tok/s ({1e3 * total / steps:.3f} ms/step), {sr['achieved_GBps']:.0f} GB/s algorithmic")
     step_us = dev_us / max(dev_steps, 1)
+    step_bytes = bytes_per_token(kv_mean)
     log(f"[bench] device time per step: {step_us:.1f} us over {dev_steps} steps "
         f"({step_bytes / (step_us * 1e-6) / 1e9:.0f} GB/s algorithmic)")
 
@@ -252,11 +321,16 @@ def main():
     w13_gbs = W13_BYTES / (us * 1e-6) / 1e9
     log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {w13_gbs:.0f} GB/s")
 
+    extra = {}
+    if extras:
+        extra["long"] = run_long(hip, host, ctxp, cfg)
+        extra["attn"] = run_attn(hip, host, sess, cfg)
+
     cpu = None
-    if args.cpu_seconds > 0 and wl == "decode":
+    if args.cpu_seconds > 0:
         log(f"[bench] CPU baseline (oracle, {args.cpu_seconds:.0f} s decode budget)")
         cpu = cpu_baseline(sess, cfg, prompt, [int(t) for t in toks], args.cpu_seconds)
-        log(f"[bench] CPU: {cpu['value']} tok/s on {cpu['cores']} cores; {cpu['sample']}")
+        log(f"[bench] CPU: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['host']['model']}); {cpu['sample']}")
 
     def traffic_of(name):
         tf = os.path.join(ROOT, "profiles", name)
@@ -293,24 +367,21 @@ def main():
         "dtype": "fp16",
         "data": "synthetic",
         "config": {
-            "workload": {"decode": "Mistral-7B-shape fp16 decode: 32 random prompt ids then greedy tokens, ctx 4096",
-                         "long": "Mistral-7B-shape fp16 decode after a 3200-token batched prefill, ctx 4096",
-                         "attn": "Mistral-7B-shape fp16 decode over a KV cache pre-filled to 16384, ctx 16448"}[wl],
+            "workload": "Mistral-7B-shape fp16 decode: 32 random prompt ids then greedy tokens, ctx 4096",
             "dim": 4096, "hidden_dim": 14336, "n_layers": 32, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128,
-            "vocab": 32000, "context": ctx_len, "prompt_tokens": n_prompt, "global_batch": 1,
+            "vocab": 32000, "context": 4096, "prompt_tokens": n_prompt, "global_batch": 1,
             "accumulate": "fp32", "activations": "fp32", "path": args.path, "parallelism": "none (1 GPU)",
         },
-        "step_roofline": {"bytes_per_token": int(step_bytes), "achieved_GBps": round(step_gbs, 1),
-                          "peak_GBps": PEAK_GBS, "frac": round(step_gbs / PEAK_GBS, 4), "kv_len_mean": kv_mean},
+        "step_roofline": sr,
+        "reference_style_tok_s": round((n_prompt + steps) / (hydrate_s + total), 2),
         "roofline": roofline,
         "w13_kernel": w13,
         "device_us_per_step": round(step_us, 2),
         "cpu_baseline": cpu,
+        **extra,
     }
     if args.option:
         out["config"]["options"] = dict(kv.partition("=")[::2] for kv in args.option)
-    if prefill is not None:
-        out["prefill"] = prefill
     print(json.dumps(out), flush=True)
     sess.close()
 

@@ -93,6 +93,11 @@ float* yhip_logits_host(yhip_ctx* ctx);
 int yhip_kv_read(yhip_ctx* ctx, int layer, uint16_t* k_host, uint16_t* v_host);
 int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16_t* v_host);
 
+/* Fills every layer's K and V cache with fp16 draws of N(0, 1) (a counter hash of `seed` and the
+ * element index) at positions below n_positions and zeros above, on the device: the set-up of the
+ * attention-heavy workload (a KV cache pre-filled to 16384 positions). No reference counterpart. */
+int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed);
+
 /* Options: "single_launch" (1 = the whole step as one launch, a dataflow of workgroups, where the
  * kernel has an instantiation: head_dim 128 with 4 q heads per kv head, and the test shapes;
  * 0 = per-op kernels, the default), "flow_bpc" / "flow_bpc_w2" (workgroups per CU of the single

@@ -1349,6 +1349,47 @@ extern "C" int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, c
   return YHIP_OK;
 }
 
+// ---- KV cache fill for the attention-heavy workload -------------------------------------------
+namespace {
+__device__ __forceinline__ unsigned long long mix64(unsigned long long z) {  // splitmix64 finaliser
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+// Every K and V entry of every layer: fp16 of N(0, 1) (Box-Muller on two 24-bit uniforms of a
+// counter hash) at positions below n_pos, zero above; positions follow the reference layouts
+// (K [g][d/16][t][16], V [g][d][t]).
+__global__ void kv_fill_normal_kernel(uint16_t* kv, size_t kv_elems, size_t total, int msl, int n_pos,
+                                      unsigned long long seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t within = i % kv_elems;        // element of this layer's K or V
+    const bool is_v = (i / kv_elems) % 2 == 1;  // layer l: K at 2 l, V at 2 l + 1
+    const int t = is_v ? (int)(within % msl) : (int)((within % (16 * (size_t)msl)) / 16);
+    uint16_t h = 0;
+    if (t < n_pos) {
+      const unsigned long long r = mix64(seed + 0x9E3779B97F4A7C15ull * (i + 1));
+      const float u1 = ((float)(r >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+      const float u2 = (float)((r >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+      const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+      h = __builtin_bit_cast(uint16_t, (f16)z);
+    }
+    kv[i] = h;
+  }
+}
+}  // namespace
+
+extern "C" int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (n_positions < 0 || n_positions > ctx->c.max_seq_len) return fail(ctx, YHIP_EINVAL, "n_positions out of range");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  const size_t total = ctx->kv_elems * 2 * (size_t)std::max(1, ctx->c.n_layers);
+  hipLaunchKernelGGL(kv_fill_normal_kernel, dim3(ctx->num_cus * 8), dim3(256), 0, ctx->stream, ctx->kv, ctx->kv_elems,
+                     total, ctx->c.max_seq_len, n_positions, seed);
+  HIP_TRY(ctx, hipGetLastError());
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
 extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   if (!key) return fail(ctx, YHIP_EINVAL, "null argument");
   if (!ctx) {

@@ -26,7 +26,7 @@ EXPORTS = (
     "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
-    "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc",
+    "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc", "yhip_kv_fill_normal",
 )
 
 
@@ -81,6 +81,7 @@ def lib():
         "yhip_test_gemm": (ctypes.c_int, [_u16p, _u16p, _u16p] + [ctypes.c_int] * 5 + [_f32p, _u16p]),
         "yhip_test_argmax": (ctypes.c_int, [_f32p, ctypes.c_int, _ip]),
         "yhip_gemm_variant": (ctypes.c_int, [ctypes.c_int] * 4 + [_ip] * 3),
+        "yhip_kv_fill_normal": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_ulonglong]),
         "yhip_attention_noalloc": (ctypes.c_int, [vp, vp, vp] + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int,
                                                                                         vp, vp]),
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
@@ -197,6 +198,10 @@ class HipModel:
         k, kp = _u16(k)
         v, vp = _u16(v)
         _check(lib().yhip_kv_write(self.h, layer, kp, vp), self.h)
+
+    def kv_fill_normal(self, n_positions, seed):
+        """Every layer's K/V = fp16 N(0, 1) draws below n_positions, zeros above (on the device)."""
+        _check(lib().yhip_kv_fill_normal(self.h, int(n_positions), int(seed)), self.h)
 
     def set_option(self, key, value):
         _check(lib().yhip_set_option(self.h, key.encode(), int(value)), self.h)
