@@ -25,7 +25,8 @@ def hip():
 
 # (LDS stages, k-step, workgroup rows); 0 stages = the register-staged kernel
 GEMM_VARIANTS = [(-1, 32, 128), (4, 32, 128), (2, 64, 128), (3, 64, 128), (2, 64, 256), (3, 64, 256),
-                 (1, 64, 256), (1, 32, 256), (0, 32, 128)]  # -1: chosen per shape; 1: the 256 x 256 kernel
+                 (1, 64, 256), (1, 32, 256), (0, 32, 128),
+                 (5, 64, 256)]  # -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K
 
 
 @pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}" for s, k, m in GEMM_VARIANTS])
@@ -240,18 +241,25 @@ def test_gemm_variants_chosen_at_3200_rows():
     assert H.gemm_variant(3200, 4096, 4096, 1) == (2, 64, 128)
 
 
+@pytest.mark.parametrize("variant", ["auto", "stream_k"])
 @pytest.mark.parametrize("mode,N,K", [(2, 14336, 4096), (1, 4096, 14336), (0, 6144, 4096), (1, 4096, 4096)])
-def test_gemm_production_shapes_at_3200_rows(mode, N, K):
-    # The Mistral-7B prefill GEMMs at M = 3200 with the auto-selected variants, against a float64
-    # product on sampled rows and columns (tile edges of both tile sizes included).
+def test_gemm_production_shapes_at_3200_rows(mode, N, K, variant):
+    # The Mistral-7B prefill GEMMs at M = 3200 with the auto-selected variants (and forced stream-K
+    # large tiles), against a float64 product on sampled rows and columns (tile edges of both tile
+    # sizes included).
     H = hip()
+    if variant == "stream_k":
+        H.set_gemm_stages(5, 64, 256)
     M = 3200
     rng = np.random.default_rng(N + K + mode)
     a = f16(rng.standard_normal((M, K), dtype=np.float32))
     b = f16(rng.standard_normal((N, K), dtype=np.float32) * 0.02)
     b3 = f16(rng.standard_normal((N, K), dtype=np.float32) * 0.02) if mode == 2 else None
     c0 = rng.standard_normal((M, N), dtype=np.float32) if mode == 1 else None
-    got = H.gemm(a, b, mode=mode, b3=b3, c=c0)
+    try:
+        got = H.gemm(a, b, mode=mode, b3=b3, c=c0)
+    finally:
+        H.set_gemm_stages(-1)
     edges = [0, 1, 127, 128, 255, 256, 3071, 3072, 3199]
     rows = np.unique(np.concatenate([edges, rng.choice(M, 40, replace=False)]))
     cedges = [0, 63, 64, 127, 128, 255, 256, N - 129, N - 128, N - 1]

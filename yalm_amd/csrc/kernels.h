@@ -169,6 +169,22 @@ __device__ __forceinline__ void wait_count(const unsigned* c, unsigned target, u
   __syncthreads();
 }
 
+// Thread 0 polls until *f == value (bounded, as wait_count); the workgroup waits at the barrier.
+__device__ __forceinline__ void wait_flag(const unsigned* f, unsigned value, unsigned* abort_flag) {
+  if (threadIdx.x == 0) {
+    unsigned spins = 0;
+    while (__hip_atomic_load(const_cast<unsigned*>(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != value) {
+      __builtin_amdgcn_s_sleep(1);
+      if ((++spins & 255u) == 0 &&
+          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 constexpr int kBufferConfig = 0x00020000;  // raw buffer descriptor word 3 on gfx9-family GPUs
 constexpr int kCpolSc1 = 16;               // cache-policy operand: sc1, the agent-scope coherent load
 

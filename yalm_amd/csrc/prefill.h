@@ -58,6 +58,10 @@ struct GemmArgs {
   float* P;
   long p_floats;  // capacity of P
   int ksplit;     // 0 or 1: no split
+  // Stream-K large tiles: one flag per workgroup slot (kSkFlagStride words apart, zeroed once) and
+  // the word a timed-out wait sets.
+  unsigned* sk_flags;
+  unsigned* abort_flag;
 };
 
 constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
@@ -406,95 +410,99 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs g) {
 // ------------------------------------------------------------------------------------------
 constexpr int kBigM = 256, kBigN = 256;
 
+// One 256 x 256 output tile of the large-tile GEMM, shared by the data-parallel kernel (one tile per
+// workgroup) and the stream-K kernel (ranges of k-steps over tiles).
 template <int EPI, int S, int BK>
-__global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
-  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
-  constexpr int CPR = BK / 8, RPI = 1024 / (2 * BK), RPW = 256 / (2 * BK);
-  constexpr int ATILE = kBigM * BK, BTILE = kBigN * BK;
-  constexpr int IA = kBigM / RPI / 4, IB = kBigN / RPI / 4;  // load instructions per wave per stage
-  constexpr int LPS = IA + IB;
-  constexpr int KK = BK / 16;
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[S][ATILE + BTILE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  constexpr int NC = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;  // output columns per tile
-  int tm, tn;
-  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + NC - 1) / NC, tm, tn)) return;
-  const int m0 = tm * kBigM, n0 = tn * NC;
-  auto swz = [](int r) { return (r / RPW) % CPR; };
+struct BigTile {
+  static constexpr int CPR = BK / 8, RPI = 1024 / (2 * BK), RPW = 256 / (2 * BK);
+  static constexpr int ATILE = kBigM * BK, BTILE = kBigN * BK;
+  static constexpr int IA = kBigM / RPI / 4, IB = kBigN / RPI / 4;  // load instructions per wave per stage
+  static constexpr int LPS = IA + IB;
+  static constexpr int KK = BK / 16;
+  static constexpr int NC = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;  // output columns per tile
+  static constexpr int STAGE = ATILE + BTILE;                        // halves per LDS stage
+  static __device__ __forceinline__ int swz(int r) { return (r / RPW) % CPR; }
 
-  const uint16_t* arow[IA];
-  const uint16_t* brow[IB];
+  // acc += A[m0 .. m0 + 256) . B[n0 ...]^T over k-steps [kt0, kt1), through the S-stage LDS
+  // pipeline; every wave of the workgroup takes part (the LDS stages are reused afterwards).
+  // tid = threadIdx.x (a persistent caller passes an opaque copy so its per-lane indexing is not
+  // hoisted out of the tile loop and kept live across it).
+  static __device__ __forceinline__ void mainloop(const GemmArgs& g, uint16_t* smem, int m0, int n0, int kt0, int kt1,
+                                                  f32x16 (&acc)[4][4], int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint16_t* arow[IA];
+    const uint16_t* brow[IB];
 #pragma unroll
-  for (int j = 0; j < IA; ++j) {
-    const int r = RPI * (wave + 4 * j) + lane / CPR;
-    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * ((lane % CPR) ^ swz(r));
-  }
-#pragma unroll
-  for (int j = 0; j < IB; ++j) {
-    const int r = RPI * (wave + 4 * j) + lane / CPR;
-    const int c = (lane % CPR) ^ swz(r);
-    if constexpr (EPI == kGemmSwiGLU) {
-      const int col = n0 + (r >> 6) * 32 + (r & 31);
-      const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
-      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
-    } else {
-      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+    for (int j = 0; j < IA; ++j) {
+      const int r = RPI * (wave + 4 * j) + lane / CPR;
+      arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * ((lane % CPR) ^ swz(r));
     }
-  }
-  auto issue = [&](int kt) {
-    uint16_t* st = smem[kt % S];
-    const int k0 = kt * BK;
 #pragma unroll
-    for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
-#pragma unroll
-    for (int j = 0; j < IB; ++j) load_lds16(brow[j] + k0, st + ATILE + (wave + 4 * j) * 512);
-  };
-  auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const int c = 2 * kk + (lane >> 5);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int ra = wm * 128 + t * 32 + (lane & 31);
-      const int rb = wn * 128 + t * 32 + (lane & 31);
-      fa[t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ swz(ra)));
-      fb[t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ swz(rb)));
+    for (int j = 0; j < IB; ++j) {
+      const int r = RPI * (wave + 4 * j) + lane / CPR;
+      const int c = (lane % CPR) ^ swz(r);
+      if constexpr (EPI == kGemmSwiGLU) {
+        const int col = n0 + (r >> 6) * 32 + (r & 31);
+        const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
+        brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+      } else {
+        brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+      }
     }
-  };
-
-  f32x16 acc[4][4];
+    auto issue = [&](int kt) {
+      uint16_t* st = smem + ((kt - kt0) % S) * STAGE;
+      const int k0 = kt * BK;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  const int nk = g.K / BK;
+      for (int j = 0; j < IB; ++j) load_lds16(brow[j] + k0, st + ATILE + (wave + 4 * j) * 512);
+    };
+    auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+      const int c = 2 * kk + (lane >> 5);
 #pragma unroll
-  for (int kt = 0; kt < S - 1; ++kt)
-    if (kt < nk) issue(kt);
-  for (int kt = 0; kt < nk; ++kt) {
-    // k-step kt has landed once at most S - 2 later stages are outstanding
-    if (kt + S - 2 < nk) wait_vmcnt<LPS * (S - 2)>();
-    else wait_vmcnt<0>();
+      for (int t = 0; t < 4; ++t) {
+        const int ra = wm * 128 + t * 32 + (lane & 31);
+        const int rb = wn * 128 + t * 32 + (lane & 31);
+        fa[t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ swz(ra)));
+        fb[t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ swz(rb)));
+      }
+    };
+#pragma unroll
+    for (int kt = kt0; kt < kt0 + S - 1; ++kt)
+      if (kt < kt1) issue(kt);
+    for (int kt = kt0; kt < kt1; ++kt) {
+      // k-step kt has landed once at most S - 2 later stages are outstanding
+      if (kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
+      else wait_vmcnt<0>();
+      __asm__ volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
+      __asm__ volatile("" ::: "memory");
+      if (kt + S - 1 < kt1) issue(kt + S - 1);
+      const uint16_t* As = smem + ((kt - kt0) % S) * STAGE;
+      const uint16_t* Bs = As + ATILE;
+      u32x4 fa[2][4], fb[2][4];
+      read_frags(As, Bs, 0, fa[0], fb[0]);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+      }
+    }
+    // the next tile's loads reuse the stages: every wave is done reading them
     __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
+    __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    if (kt + S - 1 < nk) issue(kt + S - 1);
-    const uint16_t* As = smem[kt % S];
-    const uint16_t* Bs = smem[kt % S] + ATILE;
-    u32x4 fa[2][4], fb[2][4];
-    read_frags(As, Bs, 0, fa[0], fb[0]);
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
-    }
   }
 
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  // The epilogue of row block i (32 rows of this wave): v[j] = its four 32 x 32 accumulator tiles.
+  static __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, int m0, int n0, int i, const f32x16 (&v)[4],
+                                                       int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = m0 + wm * 128 + i * 32 + acc_row(r, lane);
@@ -504,7 +512,7 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
         for (int q = 0; q < 2; ++q) {
           const int j = n0 + wn * 64 + q * 32 + (lane & 31);
           if (j < g.N) {
-            const float a1 = acc[i][2 * q][r], a3 = acc[i][2 * q + 1][r];
+            const float a1 = v[2 * q][r], a3 = v[2 * q + 1][r];
             const float h = g.act == 1 ? silu(a1) : gelu(a1);
             g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
           }
@@ -515,10 +523,143 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
           const int n = n0 + wn * 128 + j * 32 + (lane & 31);
           if (n >= g.N) continue;
           float* cp = g.C + (long)m * g.ldc + n;
-          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
-          else *cp = acc[i][j][r];
+          if constexpr (EPI == kGemmResid) *cp += v[j][r];
+          else *cp = v[j][r];
         }
       }
+    }
+  }
+
+  static __device__ __forceinline__ void epilogue(const GemmArgs& g, int m0, int n0, const f32x16 (&acc)[4][4],
+                                                  int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) epilogue_rows(g, m0, n0, i, acc[i], tid);
+  }
+};
+
+// Large-tile GEMM: 256 x 256 per workgroup, four waves in 2 x 2 each computing 128 x 128 (4 x 4
+// tiles of 32 x 32; the 256 fp32 accumulators live in the accumulation registers), BK-deep
+// k-steps in an S-stage LDS pipeline (S x BK x 1 KB) filled by direct-to-LDS loads with the same
+// swizzle as gemm_lds_kernel, one workgroup per CU. A wave issues 2 MFMAs per fragment read; the
+// loads are latency-bound, so the pipeline keeps S - 1 stages in flight (measured: with one
+// 64 KB stage in flight the loads alone take 70% of the GEMM's time).
+// SwiGLU: the 256 B rows are 128 rows of W1 and the same 128 rows of W3 interleaved by 32, so a
+// wave's tiles 2q and 2q + 1 hold W1 and W3 of the same 32 output columns.
+template <int EPI, int S, int BK>
+__global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
+  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
+  using T = BigTile<EPI, S, BK>;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * T::STAGE];
+  int tm, tn;
+  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + T::NC - 1) / T::NC, tm, tn)) return;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  T::mainloop(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
+  T::epilogue(g, tm * kBigM, tn * T::NC, acc, threadIdx.x);
+}
+
+// ------------------------------------------------------------------------------------------
+// Stream-K variant of the large-tile GEMM: one workgroup per CU, and the grid's k-steps (tiles x
+// K / BK, tiles M-fastest) dealt out evenly as contiguous ranges, so no CU idles when the tile
+// count is not a multiple of the CU count (a 3200 x 4096 output has 208 tiles of 256 x 256). The
+// ranges of XCD x (workgroups b with b % 8 == x) are contiguous, so each XCD walks its own run of
+// tiles and reuses the weight panels from its L2.
+// A workgroup walks the tiles of its range from the last to the first. When its range ends inside
+// a tile, that part comes first and is stored as an fp32 partial (written through to memory, in
+// the accumulators' own lane order) to the workgroup's slot, then the slot's flag is set to this
+// launch's epoch. The workgroup that holds a tile's last k-step handles that tile last: it adds the
+// partials of the earlier ranges (in range order: deterministic) once their flags show the epoch,
+// and applies the epilogue. Waits are bounded: a time-out sets *abort_flag (the host reports an
+// error) and the tile's result is then wrong, never hung.
+// P: gridDim.x slots of 65536 floats; flags: gridDim.x words, 64 apart, below the epoch on entry.
+// ------------------------------------------------------------------------------------------
+constexpr int kSkSlotFloats = kBigM * kBigN;
+constexpr int kSkFlagStride = 64;
+
+template <int EPI, int S, int BK>
+__global__ void __launch_bounds__(256) gemm_sk_kernel(GemmArgs g, unsigned* flags, unsigned epoch,
+                                                      unsigned* abort_flag) {
+  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
+  using T = BigTile<EPI, S, BK>;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * T::STAGE];
+  const int mt = (g.M + kBigM - 1) / kBigM, nt = (g.N + T::NC - 1) / T::NC;
+  const int KI = g.K / BK;
+  const long total = (long)mt * nt * KI;
+  const int P = gridDim.x;
+  // range index: XCD-contiguous (workgroup b runs on XCD b % 8)
+  const int per_x = P / 8;
+  const int ri = (P % 8 == 0) ? ((int)blockIdx.x % 8) * per_x + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  auto range_begin = [&](int r) { return (long)r * total / P; };
+  const long b = range_begin(ri), e = range_begin(ri + 1);
+  if (b >= e) return;
+  // accumulator tile (i, j) of this thread <-> slot floats ((wave * 16 + 4 i + j) * 64 + lane) * 16 + [0, 16):
+  // 64 contiguous bytes per lane, moved as four 16-byte agent-coherent accesses
+
+  long it = e;
+  while (it > b) {
+    // the last tile of [b, it): its k-steps [k0, k1) within this range
+    const long t = (it - 1) / KI;
+    const long tile_start = t * KI;
+    const int k0 = (int)(max(b, tile_start) - tile_start), k1 = (int)(it - tile_start);
+    it = max(b, tile_start);
+    const int m0 = (int)(t % mt) * kBigM, n0 = (int)(t / mt) * T::NC;
+    // per-lane indexing is recomputed for every tile rather than held across the loop
+    int tid = threadIdx.x;
+    __asm__ volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6;
+    auto slot_byte = [&](int i, int j) { return (((wave * 16 + 4 * i + j) * 64 + lane) * 16) * (int)sizeof(float); };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    if (k0 > 0 && k1 == KI) {
+      // this workgroup finishes a tile that earlier ranges started: their partials seed the
+      // accumulators, added in range order. The tile is the last one of this reverse walk and the
+      // first of theirs, so the partials are normally published long before.
+      int first = ri;  // the first range that reaches into this tile
+      while (first > 0 && range_begin(first) > tile_start) --first;
+      for (int q = first; q < ri; ++q) {
+        if (range_begin(q) == range_begin(q + 1)) continue;  // an empty range (fewer k-steps than workgroups)
+        wait_flag(flags + (long)q * kSkFlagStride, epoch, abort_flag);
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+            g.P + (long)q * kSkSlotFloats, 0, kSkSlotFloats * (int)sizeof(float), kBufferConfig);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const f32x4 v = load_shared4(sr, slot_byte(i, j) + 16 * r4);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][4 * r4 + r] += v[r];
+            }
+      }
+    }
+    T::mainloop(g, smem, m0, n0, k0, k1, acc, tid);
+    if (k1 < KI) {
+      // a partial: a later range finishes this tile
+      const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+          g.P + (long)ri * kSkSlotFloats, 0, kSkSlotFloats * (int)sizeof(float), kBufferConfig);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4 v = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), sr, slot_byte(i, j) + 16 * r4, 0,
+                                                   kCpolSc1);
+          }
+      publish();
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(flags + (long)ri * kSkFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      T::epilogue(g, m0, n0, acc, tid);
     }
   }
 }

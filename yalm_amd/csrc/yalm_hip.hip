@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -36,6 +37,7 @@ int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
 bool g_gemm_auto = true;  // prefill GEMM variant chosen per shape (cleared by forcing one)
 int g_gemm_ksplit = 0;    // prefill GEMM K splits on the LDS-pipeline kernel (0 = chosen per shape)
+std::atomic<unsigned> g_sk_epoch{0};  // stream-K GEMM launches so far (each launch's flag value)
 int g_upload_stage_mb = 64;  // weight upload: pinned staging chunk in MB (0 = direct pageable copies)
 int g_upload_threads = 8;    // weight upload: host threads filling a staging chunk
 
@@ -150,8 +152,9 @@ struct yhip_ctx {
   float* pf_qs = nullptr;    // [n][n_heads] score factors of the scaled query heads
   uint16_t* pf_A = nullptr;  // [n][q]
   int* pf_tok = nullptr;     // [n]
-  float* pf_P = nullptr;     // split-K partials of the prefill GEMMs
+  float* pf_P = nullptr;     // split-K / stream-K partials of the prefill GEMMs
   long pf_Pn = 0;            // its capacity in floats
+  unsigned* pf_flags = nullptr;  // stream-K flags (zeroed when the workspace is allocated)
 
   // device timing of synchronised steps ("stats" option)
   bool stats = false;
@@ -234,8 +237,11 @@ void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
 int device_cus();  // compute units of the current device (defined with the test hooks)
 
 // Split-K workspace bound: tiles x splits never exceed one workgroup per CU, and a 128 x 128 tile
-// (or 128 x 64 of W1 and of W3) holds 16384 partial sums.
-long splitk_ws_floats(int cus) { return (long)cus * 16384; }
+// (or 128 x 64 of W1 and of W3) holds 16384 partial sums; the stream-K GEMM keeps one 256 x 256
+// fp32 slot per CU.
+long splitk_ws_floats(int cus) { return (long)cus * kSkSlotFloats; }
+// Stream-K flags: one word per CU slot, kSkFlagStride words apart.
+size_t sk_flag_bytes(int cus) { return (size_t)cus * kSkFlagStride * sizeof(unsigned); }
 
 // Chooses the instantiation for row length K, rows-per-group R and epilogue kind.
 int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hipStream_t s, int bpc = 0) {
@@ -771,6 +777,19 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     const int t = ((g.M + tm - 1) / tm) * ((g.N + nc - 1) / nc);
     return dim3(8 * ((t + 7) / 8));
   };
+  if (stages == 5) {  // 256 x 256 tiles, stream-K over all CUs
+    const int P = ctx ? ctx->num_cus : device_cus();
+    if (!g.P || !g.sk_flags || !g.abort_flag || g.p_floats < (long)P * kSkSlotFloats)
+      return fail(ctx, YHIP_EINVAL, "gemm: stream-K needs a partial slot and a flag per CU");
+    const unsigned epoch = ++g_sk_epoch;
+    if (g.K % 64 == 0)
+      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 2, 64>), dim3(P), dim3(256), 0, s, g, g.sk_flags, epoch, g.abort_flag);
+    else
+      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 4, 32>), dim3(P), dim3(256), 0, s, g, g.sk_flags, epoch, g.abort_flag);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
+    return YHIP_OK;
+  }
   if (stages == 1) {  // 256 x 256 tiles
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
     if (bk == 64 && g.K % 64 == 0)
@@ -864,7 +883,7 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
   const size_t oX = take(N * c.dim * 4), oXn = take(N * c.dim * 2), oH = take(N * c.hidden_dim * 2),
                oC = take(N * (qd + 2 * kvd) * 4), oQ = take(N * qd * 2), oQs = take(N * c.n_heads * 4),
                oA = take(N * qd * 2), oT = take(N * 4),
-               oP = take((size_t)splitk_ws_floats(ctx->num_cus) * 4);
+               oP = take((size_t)splitk_ws_floats(ctx->num_cus) * 4), oF = take(sk_flag_bytes(ctx->num_cus));
   if (ctx->pf_base) hipFree(ctx->pf_base);
   ctx->pf_base = nullptr;
   ctx->pf_cap = 0;
@@ -879,6 +898,9 @@ int ensure_prefill_ws(yhip_ctx* ctx, int n) {
   ctx->pf_tok = (int*)(ctx->pf_base + oT);
   ctx->pf_P = (float*)(ctx->pf_base + oP);
   ctx->pf_Pn = splitk_ws_floats(ctx->num_cus);
+  ctx->pf_flags = (unsigned*)(ctx->pf_base + oF);
+  if (hipMemset(ctx->pf_flags, 0, sk_flag_bytes(ctx->num_cus)) != hipSuccess)
+    return fail(ctx, YHIP_EDEVICE, "prefill workspace: flag reset failed");
   ctx->pf_cap = n;
   return YHIP_OK;
 }
@@ -909,6 +931,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.K = c.dim;
     g.P = ctx->pf_P;
     g.p_floats = ctx->pf_Pn;
+    g.sk_flags = ctx->pf_flags;
+    g.abort_flag = ctx->step_abort;
     if ((rc = launch_gemm<kGemmStore>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(qkv_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_C, qd + 2 * kvd, qd, kvd,
                        c.head_dim, c.qkv_clip, (const float*)ctx->inv_freq, start, c.max_seq_len, ctx->pf_Q,
@@ -948,6 +972,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.K = qd;
     g.P = ctx->pf_P;
     g.p_floats = ctx->pf_Pn;
+    g.sk_flags = ctx->pf_flags;
+    g.abort_flag = ctx->step_abort;
     if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(kBlock), 0, s, (const float*)ctx->pf_X,
                        (const float*)L.rms_ffn, c.norm_eps, c.dim, ctx->pf_Xn);
@@ -965,6 +991,8 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.act = c.act;
     g.P = ctx->pf_P;
     g.p_floats = ctx->pf_Pn;
+    g.sk_flags = ctx->pf_flags;
+    g.abort_flag = ctx->step_abort;
     if ((rc = launch_gemm<kGemmSwiGLU>(ctx, g, s))) return rc;
     memset(&g, 0, sizeof(g));
     g.A = ctx->pf_H;
@@ -978,9 +1006,13 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     g.K = c.hidden_dim;
     g.P = ctx->pf_P;
     g.p_floats = ctx->pf_Pn;
+    g.sk_flags = ctx->pf_flags;
+    g.abort_flag = ctx->step_abort;
     if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
   }
   HIP_TRY(ctx, hipGetLastError());
+  // a timed-out wait of a stream-K GEMM, checked after the next synchronisation
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (!logits_host) return YHIP_OK;
   // last token: final rmsnorm + lm_head (reference src/infer.cpp:501-527)
   const int Rc = (c.vocab_size % 2 == 0) ? 2 : 1;
@@ -998,6 +1030,7 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
   HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                               hipMemcpyDeviceToHost, s));
   HIP_TRY(ctx, hipStreamSynchronize(s));
+  if (int rc = check_step_abort(ctx)) return rc;
   if (logits_host != ctx->logits_host) memcpy(logits_host, ctx->logits_host, (size_t)c.vocab_size * 4);
   return YHIP_OK;
 }
@@ -1402,8 +1435,9 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       g_attn_mfma = value != 0;
       return YHIP_OK;
     }
-    if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 0 register-staged; 1 large tile; 2..4 LDS stages
-      if (value < -1 || value > 4) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 4]");
+    if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 0 register-staged; 1 large tile; 2..4 LDS stages;
+                                        // 5 large tiles, stream-K
+      if (value < -1 || value > 5) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 5]");
       g_gemm_auto = value < 0;
       if (value >= 0) g_gemm_stages = value;
       return YHIP_OK;
@@ -1857,9 +1891,13 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   uint16_t* dh = mode == kGemmSwiGLU ? d.alloc<uint16_t>((size_t)M * N) : nullptr;
   const long pf = splitk_ws_floats(device_cus());
   float* dp = d.alloc<float>((size_t)pf);
+  unsigned* dflags = d.alloc<unsigned>(sk_flag_bytes(device_cus()) / sizeof(unsigned));  // zeroed
+  unsigned* dabort = d.alloc<unsigned>(1);
   TRY_ALLOC(da);
   TRY_ALLOC(db);
   TRY_ALLOC(dp);
+  TRY_ALLOC(dflags);
+  TRY_ALLOC(dabort);
   if (mode == kGemmSwiGLU) {
     TRY_ALLOC(db3);
     TRY_ALLOC(dh);
@@ -1883,11 +1921,16 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   g.act = act;
   g.P = dp;
   g.p_floats = pf;
+  g.sk_flags = dflags;
+  g.abort_flag = dabort;
   int rc = mode == kGemmStore ? launch_gemm<kGemmStore>(nullptr, g, nullptr)
            : mode == kGemmResid ? launch_gemm<kGemmResid>(nullptr, g, nullptr)
                                 : launch_gemm<kGemmSwiGLU>(nullptr, g, nullptr);
   if (rc) return rc;
   HIP_TRY(nullptr, hipDeviceSynchronize());
+  unsigned aborted = 0;
+  HIP_TRY(nullptr, hipMemcpy(&aborted, dabort, sizeof(aborted), hipMemcpyDeviceToHost));
+  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm: a stream-K wait timed out");
   if (mode == kGemmSwiGLU) HIP_TRY(nullptr, hipMemcpy(h, dh, (size_t)M * N * 2, hipMemcpyDeviceToHost));
   else HIP_TRY(nullptr, hipMemcpy(c, dc, (size_t)M * N * 4, hipMemcpyDeviceToHost));
   return YHIP_OK;
@@ -1898,13 +1941,13 @@ extern "C" int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   int s = 0, k = 0, m = 0;
   gemm_choice(mode, M, K, s, k, m);
-  if (s != 1) {  // the LDS pipeline's own limits (launch_gemm)
+  if (s != 1 && s != 5) {  // the LDS pipeline's own limits (launch_gemm)
     if (K % 64 != 0) k = 32;
     if (k != 64) m = 128;
   }
   *stages = s;
   *bk = k;
-  *bm = s == 1 ? kBigM : m;
+  *bm = (s == 1 || s == 5) ? kBigM : m;
   return YHIP_OK;
 }
 
@@ -2127,12 +2170,16 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   uint16_t* dh = d.alloc<uint16_t>((size_t)M * N);
   const long pf = splitk_ws_floats(device_cus());
   float* dp = d.alloc<float>((size_t)pf);
+  unsigned* dflags = d.alloc<unsigned>(sk_flag_bytes(device_cus()) / sizeof(unsigned));  // zeroed
+  unsigned* dabort = d.alloc<unsigned>(1);
   TRY_ALLOC(da);
   TRY_ALLOC(db);
   TRY_ALLOC(db3);
   TRY_ALLOC(dc);
   TRY_ALLOC(dh);
   TRY_ALLOC(dp);
+  TRY_ALLOC(dflags);
+  TRY_ALLOC(dabort);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, da, (size_t)M * K, 11u);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db, (size_t)N * K, 12u);
   hipLaunchKernelGGL(fill_weights_kernel, dim3(1024), dim3(256), 0, nullptr, db3, (size_t)N * K, 13u);
@@ -2155,6 +2202,8 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   g.act = 1;
   g.P = dp;
   g.p_floats = pf;
+  g.sk_flags = dflags;
+  g.abort_flag = dabort;
   hipStream_t s;
   HIP_TRY(nullptr, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   auto launch = [&] {
@@ -2178,6 +2227,9 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   hipStreamDestroy(s);
   if (rc) return rc;
   if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, std::string("gemm bench: ") + hipGetErrorString(e));
+  unsigned aborted = 0;
+  HIP_TRY(nullptr, hipMemcpy(&aborted, dabort, sizeof(aborted), hipMemcpyDeviceToHost));
+  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm bench: a stream-K wait timed out");
   *us_per_launch = 1000.f * ms / reps;
   return YHIP_OK;
 }

@@ -244,7 +244,8 @@ def set_test_bpc(n):
 
 def set_gemm_stages(n, bk=32, bm=128):
     """Prefill GEMM variant: -1 = chosen per shape (default); 0 = register-staged kernel; 1 = large
-    tiles (k-step bk); 2..4 = LDS pipeline stages with k-step bk and workgroup rows bm."""
+    tiles (k-step bk); 2..4 = LDS pipeline stages with k-step bk and workgroup rows bm; 5 = large
+    tiles, stream-K over all CUs."""
     _check(lib().yhip_set_option(None, b"gemm_stages", int(n)))
     _check(lib().yhip_set_option(None, b"gemm_bk", int(bk)))
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
