@@ -78,14 +78,18 @@ struct AttnMfmaSmem {
   unsigned last_flag;
 };
 
-// One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g. COH: q and the
-// K/V entries are read with agent-coherent loads (they were written by other workgroups of the same
-// launch: the QKV kernel with the attention fused in). DB: two tile buffers per wave.
-template <int HD, int G, int NW, bool COH, bool DB = true>
-__device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int split, const Positions& pss,
-                                               AttnMfmaSmem<HD, G, NW>& sm) {
+// The per-wave part of the MFMA attention over keys [t_begin, t_end) of kv head g, for all G
+// query heads of g, in a workgroup of NW waves: every wave's (m, l, o) lands in sm.om / sm.oml,
+// then a workgroup barrier. COH: q and the K/V entries are read with agent-coherent loads (they
+// were written by other workgroups of the same launch: the QKV kernel with the attention fused in).
+// DB: two tile buffers per wave. `issue()` runs once in every wave, right after the wave's first
+// K/V tile and its q loads are issued (at once in a wave without a tile): loads it issues are
+// younger than those, and loads retire in issue order, so waiting for the tile and q does not wait
+// for them.
+template <int HD, int G, int NW, bool COH, bool DB, class Issue>
+__device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_begin, int t_end,
+                                                AttnMfmaSmem<HD, G, NW>& sm, Issue issue) {
   static_assert(HD % 32 == 0 && G >= 1 && G <= 8, "head_dim % 32, 1..8 query heads per kv head");
-  constexpr int NT = 64 * NW;
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int TS = 32;  // keys per wave tile
   constexpr int CPOL = COH ? kCpolSc1 : 0;
@@ -96,23 +100,11 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
   // branches rather than exec-masked ones
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int kv_len = pss.kv_len;
-  const int chunk = attn_mfma_chunk(kv_len, a.nsplit, a.min_slice);
-  const int active = (kv_len + chunk - 1) / chunk;
-  if (split >= active) return;
-  const int t_begin = split * chunk;
-  const int t_end = min(kv_len, t_begin + chunk);
   const long head_off = (long)g * HD * a.msl;
-  uint16_t* kh = a.kcache + head_off;
-  const uint16_t* vh = a.vcache + head_off;
   const int head_bytes = HD * a.msl * 2;
-  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(kh, 0, head_bytes, kBufferConfig);
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(a.kcache + head_off, 0, head_bytes, kBufferConfig);
   const __amdgpu_buffer_rsrc_t vr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vh), 0, head_bytes, kBufferConfig);
-  if (pss.kv_sink > 0 && split == 0) {
-    rotate_sinks<HD, NT>(a, kh, pss.kv_sink, tid);
-    __syncthreads();
-  }
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vcache + head_off), 0, head_bytes, kBufferConfig);
 
   float m_run = kNegBig, l_run = 0.f;
   f32x4 acc[DT];
@@ -154,6 +146,9 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
           q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
       // the head's largest |q| over the four lanes of the column (each holds 8 of every 32 dims)
       float amax = 0.f;
 #pragma unroll
@@ -254,6 +249,8 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
       tile(nxt, t0);
       t0 = tn;
     }
+  } else {
+    issue();
   }
 
   // this wave's (m, l, o): l summed over the four lane groups, o over the hi/lo columns
@@ -274,6 +271,28 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
     }
   }
   __syncthreads();
+}
+
+// One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g (COH, DB as
+// attn_mfma_waves).
+template <int HD, int G, int NW, bool COH, bool DB = true>
+__device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int split, const Positions& pss,
+                                               AttnMfmaSmem<HD, G, NW>& sm) {
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x;
+  const int kv_len = pss.kv_len;
+  const int chunk = attn_mfma_chunk(kv_len, a.nsplit, a.min_slice);
+  const int active = (kv_len + chunk - 1) / chunk;
+  if (split >= active) return;
+  const int t_begin = split * chunk;
+  const int t_end = min(kv_len, t_begin + chunk);
+  if (pss.kv_sink > 0 && split == 0) {
+    rotate_sinks<HD, NT>(a, a.kcache + (long)g * HD * a.msl, pss.kv_sink, tid);
+    __syncthreads();
+  }
+  attn_mfma_waves<HD, G, NW, COH, DB>(a, g, t_begin, t_end, sm, [] {});
+  auto& om = sm.om;
+  auto& oml = sm.oml;
 
   // the workgroup's (m, l, o) per head: final output, or this slice's partial for the merge
   const int stride = HD + 2;
@@ -368,5 +387,152 @@ __global__ void __launch_bounds__(kBlock) qkv_attn_kernel(MatvecArgs m, AttnArgs
   if (item >= items) return;
   wait_split_count(done, gridDim.x, abort_flag);  // every row of q, K and V is written
   attn_mfma_body<HD, G, kWavesPerBlock, true, false>(a, item % a.n_kv_heads, item / a.n_kv_heads, pss, sm);
+}
+
+// ------------------------------------------------------------------------------------------
+// Decode attention and the O projection in one launch (short contexts, no sink rotation),
+// reference src/infer.cpp:327-344: x += Wo . concat_h attn_h.
+//
+// The product splits over kv heads: Wo . attn = sum_g Wo[:, cols(g)] . attn(g), where cols(g) are
+// the G * HD columns of the G query heads of kv head g. Workgroup b takes kv head g = b % nkv and
+// the RB output rows starting at rb * RB (rb = b / nkv); with nkv = 8 every workgroup of kv head g
+// runs on the same XCD (b mod 8), so that head's K/V lines are fetched into one L2 only. Each
+// workgroup
+//   1. issues its K/V tile and q loads, then its Wo block (RB rows x G*HD columns, 16 bytes per
+//      lane per row segment, streaming loads) while the attention runs;
+//   2. runs the whole-context MFMA attention of kv head g for its G query heads (every workgroup of
+//      g repeats it: a few hundred keys are a few hundred KB from L2, against the separate launch's
+//      boundary and start-up);
+//   3. multiplies its Wo block by that attention output (LDS) and combines each row's sum with the
+//      other kv heads' in a 64-bit word per row (below); the workgroup that completes a row writes
+//      x[row] once.
+// Wo loads: chunk c = lane + 64 u (u < U) of the wave's block is row c / CPR, column chunk c % CPR
+// (CPR = G*HD/8 16-byte chunks per row segment); a wave covers U * 64 / CPR rows.
+//
+// The per-row word: bits 0..59 hold the sum of the terms 2^55 + round(p 2^32) added so far (p: one
+// workgroup's fp32 partial product for that row, clamped to |p| < 2^23; each term is below 2^56, so
+// up to 15 of them never carry into bit 60), bits 60..63 count the additions. Every workgroup adds
+// its term plus 2^60 with one returning 64-bit atomic; the one whose addition brings the count to
+// nkv holds all terms in (returned value + its own), writes x[row] += (sum - nkv 2^55) 2^-32 and
+// clears the word for the next launch. Integer addition is associative, so x does not depend on the
+// order in which the workgroups' atomics land: the step is bit-reproducible. The fixed-point
+// resolution is 2^-32 (2.3e-10) per partial, absolute.
+// ------------------------------------------------------------------------------------------
+struct AttnOArgs {
+  const uint16_t* wo;        // [dim][q_dim]
+  float* x;                  // [dim], x += Wo . attn
+  unsigned long long* rowacc;  // [dim] combining words, zero between launches
+  int dim, q_dim;
+};
+
+constexpr int kRowAccCountShift = 60;
+constexpr unsigned long long kRowAccMask = (1ull << kRowAccCountShift) - 1;
+constexpr unsigned long long kRowAccBias = 1ull << 55;
+constexpr float kRowAccScale = 4294967296.0f;  // 2^32
+constexpr int kRowAccMaxTerms = 15;
+
+// This workgroup's term for one row: 2^60 (the count) + 2^55 + round(p 2^32), |p 2^32| < 2^55.
+__device__ __forceinline__ unsigned long long rowacc_term(float p) {
+  float v = rintf(p * kRowAccScale);
+  v = fminf(fmaxf(v, -36028797018963960.0f), 36028797018963960.0f);  // 2^55 - 2^31 (float-representable)
+  return (1ull << kRowAccCountShift) + kRowAccBias + (unsigned long long)(long long)v;
+}
+// The row's fp32 sum from a completed word (count n): (value bits - n 2^55) 2^-32.
+__device__ __forceinline__ float rowacc_sum(unsigned long long w, int n) {
+  const long long v = (long long)(w & kRowAccMask) - (long long)n * (long long)kRowAccBias;
+  return (float)v * (1.0f / kRowAccScale);
+}
+
+template <int HD, int G, int NW, int U>
+struct AttnOGeom {
+  static constexpr int CPR = G * HD / 8;
+  static constexpr int UPR = CPR >= 64 ? CPR / 64 : 1;   // loads per row (CPR >= 64)
+  static constexpr int RPL = CPR >= 64 ? 1 : 64 / CPR;   // rows per load (CPR < 64)
+  static constexpr int RW = CPR >= 64 ? U / UPR : U * RPL;  // rows per wave
+  static constexpr int RB = RW * NW;                     // rows per workgroup
+  static_assert(RW >= 1 && RW <= 64 && (CPR >= 64 ? U % UPR == 0 : true), "attention + O row layout");
+};
+
+template <int HD, int G, int NW, int U>
+__global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o) {
+  using Geo = AttnOGeom<HD, G, NW, U>;
+  constexpr int CPR = Geo::CPR, RW = Geo::RW;
+  __shared__ AttnMfmaSmem<HD, G, NW> sm;
+  __shared__ __attribute__((aligned(16))) float ao[G * HD];
+  __shared__ float rs[NW][RW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = (int)blockIdx.x % a.n_kv_heads, rb = (int)blockIdx.x / a.n_kv_heads;
+  const int row0 = rb * Geo::RB + wave * RW;
+  const int kv_len = min(a.params->pos + 1, a.msl);  // the host runs this kernel only for pos < msl
+
+  // this wave's Wo rows, columns of kv head g; rows past dim read as zero (descriptor bound)
+  const long row_bytes = (long)o.q_dim * 2;
+  const int valid_bytes = row0 < o.dim ? (int)min((long)(o.dim - row0) * row_bytes, (long)0x7fffffff) : 0;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(o.wo + (long)(row0 < o.dim ? row0 : 0) * o.q_dim + (long)g * G * HD), 0, valid_bytes,
+      kBufferConfig);
+  u32x4 wv[U];
+  auto issue = [&] {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = lane + 64 * u;
+      const int voff = (c / CPR) * (int)row_bytes + (c % CPR) * 16;
+      wv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, 0, kCpolNt));
+    }
+  };
+  attn_mfma_waves<HD, G, NW, false, false>(a, g, 0, kv_len, sm, issue);
+
+  // the workgroup's attention output for the G heads of g, normalised, into LDS
+  for (int e = tid; e < G * HD; e += 64 * NW) {
+    const int h = e / HD, d = e % HD;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.oml[w][h][0]);
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = exp2_fast(sm.oml[w][h][0] - M);
+      O = fmaf(sm.om[w][h][d], wt, O);
+      L = fmaf(sm.oml[w][h][1], wt, L);
+    }
+    ao[e] = O / L;
+  }
+  __syncthreads();
+
+  // Wo block . attention output; row sums to lanes 0 .. RW-1, then one atomic per row
+  float mine = 0.f;
+  if constexpr (CPR >= 64) {
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < Geo::UPR; ++k) {
+        const int c = lane + 64 * (j * Geo::UPR + k);
+        acc = dot8(wv[j * Geo::UPR + k], ao + 8 * (c % CPR), acc);
+      }
+      const float s = wave_sum(acc);
+      if (lane == j) mine = s;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float s = lane_group_sum<CPR>(dot8(wv[u], ao + 8 * (lane % CPR), 0.f));
+      if (lane % CPR == 0) rs[wave][u * Geo::RPL + lane / CPR] = s;
+    }
+    __syncthreads();
+    mine = lane < RW ? rs[wave][lane] : 0.f;
+  }
+  const int row = row0 + lane;
+  if (lane < RW && row < o.dim) {
+    const float xr = o.x[row];
+    const unsigned long long term = rowacc_term(mine);
+    const unsigned long long old =
+        __hip_atomic_fetch_add(o.rowacc + row, term, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long w = old + term;
+    if ((int)(w >> kRowAccCountShift) == a.n_kv_heads) {  // the last of the row's nkv terms
+      o.x[row] = xr + rowacc_sum(w, a.n_kv_heads);
+      __hip_atomic_store(o.rowacc + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 }  // namespace yk

@@ -120,14 +120,21 @@ struct yhip_ctx {
   int prefetch_o = 0, prefetch_w13_mb = 0, prefetch_blocks = 256;
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   unsigned* pf_sink = nullptr;
-  // captured steps: [mode: hydrate, logits, argmax][attention: separate launch, fused into QKV]
-  hipGraphExec_t graph[3][2] = {};
+  // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepQkvAttn,
+  // kStepAttnO]
+  hipGraphExec_t graph[3][3] = {};
+  // attention and the O projection in one launch (attn_o_kernel) for contexts up to attn_o_max
+  // tokens: 108-119 us less per token than the separate launches up to 350 keys, 60 at 500, 17 at
+  // 700, slower from ~800 on (Mistral-7B shape on MI355X)
+  bool attn_o = true;
+  int attn_o_max = 700;
   // decode attention fused into the QKV launch for contexts up to fuse_attn_max tokens (opt-in:
   // measured slower than the separate launch on MI355X, see the design notes)
   bool fuse_attn = false;
   int fuse_attn_max = 1024;
   unsigned* qkv_done = nullptr;    // per layer: kQkvDoneParts counters of QKV workgroups done (zeroed every step)
   unsigned* step_abort = nullptr;  // a bounded wait of a fused launch timed out
+  unsigned long long* rowacc = nullptr;  // [dim] attn_o_kernel's per-row combining words (zero between launches)
 
   // single-launch decode (decode_flow.h)
   const void* flow_fn = nullptr;  // instantiation for this shape, or null when the shape has none
@@ -406,10 +413,74 @@ int launch_qkv_attn(yhip_ctx* ctx, const MatvecArgs& a, const AttnArgs& t, unsig
   return YHIP_OK;
 }
 
+// ---- attention + O projection in one launch ------------------------------------------------------
+// Waves per attn_o_kernel workgroup, and its Wo loads per wave: 16 row segments of G*HD columns
+// (whole rows of 16-byte chunks), or CPR when a segment has fewer than 64 chunks, so that a wave's
+// rows fit its 64 lanes.
+constexpr int kAttnOWaves = 8;
+template <int HD, int G>
+constexpr int attn_o_loads() {
+  return G * HD / 8 >= 16 ? 16 : G * HD / 8;
+}
+template <int HD, int G>
+int attn_o_blocks(const yhip_config& c) {
+  constexpr int RB = AttnOGeom<HD, G, kAttnOWaves, attn_o_loads<HD, G>()>::RB;
+  return c.n_kv_heads * ((c.dim + RB - 1) / RB);
+}
+
+template <int HD, int G>
+void go_attn_o(const yhip_config& c, const AttnArgs& t, const AttnOArgs& o, hipStream_t s) {
+  hipLaunchKernelGGL((attn_o_kernel<HD, G, kAttnOWaves, attn_o_loads<HD, G>()>), dim3(attn_o_blocks<HD, G>(c)),
+                     dim3(64 * kAttnOWaves), 0, s, t, o);
+}
+
+bool attn_o_shape(const yhip_config& c) {
+  const int G = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
+  return (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+         c.n_kv_heads <= kRowAccMaxTerms;
+}
+
+// The step at pos runs attention and O in one launch when the option is on, the MFMA attention
+// applies, there is no sink rotation (pos < max_seq_len) and the context is at most attn_o_max.
+bool attn_o_at(const yhip_ctx* ctx, int pos) {
+  return ctx->attn_o && attn_uses_mfma(ctx) && attn_o_shape(ctx->c) && pos < ctx->c.max_seq_len &&
+         pos + 1 <= ctx->attn_o_max;
+}
+
+int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStream_t s) {
+  const yhip_config& c = ctx->c;
+  switch (t.head_dim * 16 + t.n_heads / t.n_kv_heads) {
+    case 32 * 16 + 1: go_attn_o<32, 1>(c, t, o, s); break;
+    case 32 * 16 + 2: go_attn_o<32, 2>(c, t, o, s); break;
+    case 32 * 16 + 4: go_attn_o<32, 4>(c, t, o, s); break;
+    case 32 * 16 + 8: go_attn_o<32, 8>(c, t, o, s); break;
+    case 64 * 16 + 1: go_attn_o<64, 1>(c, t, o, s); break;
+    case 64 * 16 + 2: go_attn_o<64, 2>(c, t, o, s); break;
+    case 64 * 16 + 4: go_attn_o<64, 4>(c, t, o, s); break;
+    case 64 * 16 + 8: go_attn_o<64, 8>(c, t, o, s); break;
+    case 128 * 16 + 1: go_attn_o<128, 1>(c, t, o, s); break;
+    case 128 * 16 + 2: go_attn_o<128, 2>(c, t, o, s); break;
+    case 128 * 16 + 4: go_attn_o<128, 4>(c, t, o, s); break;
+    case 128 * 16 + 8: go_attn_o<128, 8>(c, t, o, s); break;
+    default: return fail(ctx, YHIP_EINVAL, "attention + O: unsupported shape");
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention + O launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
-// fused: the attention runs inside the QKV launch (fused_attention_at).
-int enqueue_step(yhip_ctx* ctx, int mode, int fused) {
+// variant: kStepSeparate (every kernel its own launch), kStepQkvAttn (the attention runs inside
+// the QKV launch, fused_attention_at) or kStepAttnO (attention and O in one launch, attn_o_at).
+enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2 };
+int step_variant(const yhip_ctx* ctx, int pos) {
+  if (fused_attention_at(ctx, pos)) return kStepQkvAttn;  // opt-in, so it takes precedence
+  return attn_o_at(ctx, pos) ? kStepAttnO : kStepSeparate;
+}
+
+int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
+  const bool fused = variant == kStepQkvAttn;
   const yhip_config& c = ctx->c;
   hipStream_t s = ctx->stream;
   const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
@@ -462,7 +533,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int fused) {
     } else {
       if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
     }
-    if (!fused && (ctx->prefetch_o || ctx->prefetch_w13_mb)) {
+    if (variant == kStepSeparate && (ctx->prefetch_o || ctx->prefetch_w13_mb)) {
       // O is read by its matvec in 64 KB pieces (8 rows of q_dim halves per workgroup for q_dim
       // 4096), W1/W3 in 32 KB pieces per matrix; chunk i of a range feeds consumer workgroup i.
       const long o_units = (long)c.dim * qd * 2 / 16;
@@ -476,8 +547,19 @@ int enqueue_step(yhip_ctx* ctx, int mode, int fused) {
       t.pf.magic = 0x9E3779B9u;
       t.pf.sink = ctx->pf_sink;
     }
-    if (!fused && (rc = launch_attention(ctx, t, s))) return rc;
+    if (variant == kStepAttnO) {
+      // 2 + 3. attention and O-proj + residual in one launch
+      AttnOArgs o;
+      o.wo = L.wo;
+      o.x = ctx->x;
+      o.rowacc = ctx->rowacc;
+      o.dim = c.dim;
+      o.q_dim = qd;
+      if ((rc = launch_attn_o(ctx, t, o, s))) return rc;
+    }
+    if (variant == kStepSeparate && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
+    if (variant != kStepAttnO) {
     a = mv_base();
     a.w0 = L.wo;
     a.row_step = 2L * qd;
@@ -487,6 +569,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int fused) {
     a.x = ctx->att;
     a.out = ctx->x;
     if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s, ctx->mv_bpc[1]))) return rc;
+    }
     // 4. rmsnorm + W1/W3 + SwiGLU
     a = mv_base();
     a.w0 = L.w1;
@@ -714,13 +797,13 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
                      (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key, ctx->qkv_done,
                      c.n_layers);
   HIP_TRY(ctx, hipGetLastError());
-  const int fused = fused_attention_at(ctx, pos) ? 1 : 0;
-  if (!ctx->use_graph) return enqueue_step(ctx, mode, fused);
-  hipGraphExec_t& ge = ctx->graph[mode][fused];
+  const int variant = step_variant(ctx, pos);
+  if (!ctx->use_graph) return enqueue_step(ctx, mode, variant);
+  hipGraphExec_t& ge = ctx->graph[mode][variant];
   if (!ge) {
     hipGraph_t g = nullptr;
     HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(ctx, mode, fused);
+    int rc = enqueue_step(ctx, mode, variant);
     hipError_t e = hipStreamEndCapture(ctx->stream, &g);
     if (rc) {
       if (g) hipGraphDestroy(g);
@@ -1126,7 +1209,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
                a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
                a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_pfs = atake(1024 * 4),
                a_qd = atake((size_t)std::max(1, c.n_layers) * kQkvDoneParts * kQkvDoneStride * sizeof(unsigned)),
-               a_sa = atake(256);
+               a_sa = atake(256), a_racc = atake(dim * sizeof(unsigned long long));
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -1148,6 +1231,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->pf_sink = (unsigned*)(ctx->abase + a_pfs);
   ctx->qkv_done = (unsigned*)(ctx->abase + a_qd);
   ctx->step_abort = (unsigned*)(ctx->abase + a_sa);
+  ctx->rowacc = (unsigned long long*)(ctx->abase + a_racc);
   {
     const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
     if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -1494,6 +1578,11 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     ctx->attn_splits = value;
   } else if (!strcmp(key, "attn_mfma")) {
     ctx->attn_mfma = value != 0;
+  } else if (!strcmp(key, "attn_o")) {
+    ctx->attn_o = value != 0;
+  } else if (!strcmp(key, "attn_o_max")) {
+    if (value < 0) return fail(ctx, YHIP_EINVAL, "attn_o_max must be >= 0");
+    ctx->attn_o_max = value;
   } else if (!strcmp(key, "fuse_attn")) {
     ctx->fuse_attn = value != 0;
   } else if (!strcmp(key, "fuse_attn_max")) {
