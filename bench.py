@@ -200,11 +200,13 @@ def run_long(hip, host, ctxp, cfg, steps=30, n_prompt=3200):
             "decode_ms_per_step": round(1e3 / tok_s, 4), "step_roofline": step_roofline(kv_mean, tok_s)}
 
 
-def run_attn(hip, host, sess, cfg, steps=64, fill=16384, ctx_len=16448):
+def run_attn(hip, host, sess, cfg, steps=64, fill=16384, ctx_len=16448, opts=()):
     """KV cache pre-filled on the device to 16384 positions, greedy decode at kv ~16400."""
     c16 = dict(cfg, max_seq_len=ctx_len)
     t0 = time.perf_counter()
     m = hip.HipModel(c16, sess.tensors())
+    for key, val in opts:  # the same context options as the headline context
+        m.set_option(key.decode(), val)
     m.kv_fill_normal(fill, 16384)
     log(f"[bench] attn: context {ctx_len} set up, KV pre-filled to {fill} in {time.perf_counter() - t0:.1f} s")
     first = int(host.uniform_ids(1, 16385, cfg["vocab_size"])[0])
@@ -285,7 +287,7 @@ def main():
         sess.close()
         return
     if wl == "attn":
-        res = run_attn(hip, host, sess, cfg, steps)
+        res = run_attn(hip, host, sess, cfg, steps, opts=opts)
         print(json.dumps({"metric": METRIC, "value": res["decode_tok_s"], "unit": "tok/s", "n_gpus": 1,
                           "steps": steps, "warmup": 3, "ms_per_step": res["decode_ms_per_step"],
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
@@ -324,7 +326,7 @@ def main():
     extra = {}
     if extras:
         extra["long"] = run_long(hip, host, ctxp, cfg)
-        extra["attn"] = run_attn(hip, host, sess, cfg)
+        extra["attn"] = run_attn(hip, host, sess, cfg, opts=opts)
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -23,12 +23,12 @@ def hip():
 
 
 # The ways a step can run: one launch per token (a dataflow of workgroups), the captured hipGraph
-# of per-op kernels (the default; attention and O share a launch up to 700 keys), the same kernels
-# launched directly, the graph with the SIMT attention, and the graph with attention and O always
-# in separate launches.
+# of per-op kernels (the default: attention and O share a launch up to 700 keys, beyond that the
+# attention's slice merge moves into the O launch), the same kernels launched directly, the graph
+# with the SIMT attention, and the graph with attention (merge included) and O in separate launches.
 PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
          "direct": dict(single_launch=0, graph=0), "graph_simt": dict(single_launch=0, graph=1, attn_mfma=0),
-         "graph_sep": dict(single_launch=0, graph=1, attn_o=0)}
+         "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0)}
 
 
 def use_path(m, path):
@@ -395,6 +395,44 @@ def test_attention_and_o_in_one_launch_matches_oracle(path, shape):
     hm.close()
 
 
+SPLIT_O_SHAPES = {
+    "mistral": dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32, n_kv_heads=8,
+                    max_seq_len=4096, rotary_dim=128),
+    "hd32_g4": dict(TINY, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, n_layers=2, max_seq_len=4608),
+    "hd64_g8": dict(TINY, dim=512, head_dim=64, n_heads=16, n_kv_heads=2, rotary_dim=64, n_layers=2, max_seq_len=2048),
+}
+
+
+@pytest.mark.parametrize("path", ["graph", "direct"])
+@pytest.mark.parametrize("shape", list(SPLIT_O_SHAPES))
+def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
+    # Beyond 700 keys the split-KV attention stores every slice's partial and the O launch merges
+    # them (each workgroup its kv head's slices) before its Wo block: positions across the slice
+    # rules (64/128/256/384-key slices, 1 to 24 slices), at the end of the context, and past it (sink
+    # mode: the two sink keys re-rotated, the ring position), against the oracle on a cache
+    # pre-filled from the host.
+    cfg = SPLIT_O_SHAPES[shape]
+    t = np_tensors(cfg, seed=61, std=0.02)
+    om, hm = _models(cfg, t, path)
+    rng = np.random.default_rng(62)
+    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
+    for layer in range(cfg["n_layers"]):
+        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
+        om.set_kv(layer, k, v)
+        hm.set_kv(layer, k, v)
+    msl = cfg["max_seq_len"]
+    tok = 3
+    for pos in (700, 701, 1023, 1024, 1536, 1537, 2047, 3216, msl - 1, msl, msl + 1, msl + 5):
+        if pos > msl + 5:
+            continue
+        lo = om.forward(tok, pos)
+        lh = hm.forward(tok, pos)
+        assert npref.rel_l2(lh, lo) < 1e-4, pos
+        tok = O.argmax(lo)
+    hm.close()
+
+
 def test_attention_and_o_in_one_launch_is_bit_reproducible():
     # The kv heads' partial products meet in integer words per row (fixed point plus an arrival
     # count), so x does not depend on the order the workgroups finish in: two contexts running the
@@ -414,6 +452,21 @@ def test_attention_and_o_in_one_launch_is_bit_reproducible():
     for (ka, va), (kb, vb) in zip(kva, kvb):
         assert np.array_equal(ka, kb) and np.array_equal(va, vb)
     assert npref.rel_l2(la, ls) < 1e-5
+
+
+def test_slice_merge_in_the_o_launch_is_bit_reproducible():
+    # The same for the merge + O launch at 3000 keys (14 slices per kv head), against the
+    # separate attention (its own last-slice merge) and O launches.
+    cfg = SPLIT_O_SHAPES["mistral"]
+    t = np_tensors(cfg, seed=63, std=0.02)
+    outs = []
+    for so in (1, 1, 0):
+        with hip().HipModel(cfg, t) as m:
+            m.set_option("split_o", so)
+            m.kv_fill_normal(3000, 64)
+            outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
+    assert np.array_equal(outs[0], outs[1])
+    assert npref.rel_l2(outs[0], outs[2]) < 1e-5
 
 
 @pytest.mark.parametrize("path", ["graph", "direct"])

@@ -308,7 +308,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
       O = fmaf(om[w][h][d], wt, O);
       L = fmaf(oml[w][h][1], wt, L);
     }
-    if (active == 1) {
+    if (active == 1 && !a.defer_merge) {
       a.out[(long)(g * G + h) * HD + d] = O / L;
     } else {
       float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
@@ -319,7 +319,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
       }
     }
   }
-  if (active == 1) return;
+  if (active == 1 || a.defer_merge) return;
   attn_merge_slices<HD, G, NT, false>(a, g, active, tid, sm.mrg, sm.Ls, sm.last_flag);
 }
 
@@ -453,52 +453,14 @@ struct AttnOGeom {
   static_assert(RW >= 1 && RW <= 64 && (CPR >= 64 ? U % UPR == 0 : true), "attention + O row layout");
 };
 
+// The O part shared by attn_o_kernel and merge_o_kernel: this wave's Wo rows (wv, columns of kv
+// head g) times the G heads' attention output ao (LDS), each row's sum combined with the other kv
+// heads' in the row words; the workgroup completing a row writes x[row].
 template <int HD, int G, int NW, int U>
-__global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o) {
+__device__ __forceinline__ void attn_o_rows(const AttnOArgs& o, const float* ao, float (&rs)[NW][AttnOGeom<HD, G, NW, U>::RW],
+                                            const u32x4 (&wv)[U], int row0, int lane, int wave, int nkv) {
   using Geo = AttnOGeom<HD, G, NW, U>;
   constexpr int CPR = Geo::CPR, RW = Geo::RW;
-  __shared__ AttnMfmaSmem<HD, G, NW> sm;
-  __shared__ __attribute__((aligned(16))) float ao[G * HD];
-  __shared__ float rs[NW][RW];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = (int)blockIdx.x % a.n_kv_heads, rb = (int)blockIdx.x / a.n_kv_heads;
-  const int row0 = rb * Geo::RB + wave * RW;
-  const int kv_len = min(a.params->pos + 1, a.msl);  // the host runs this kernel only for pos < msl
-
-  // this wave's Wo rows, columns of kv head g; rows past dim read as zero (descriptor bound)
-  const long row_bytes = (long)o.q_dim * 2;
-  const int valid_bytes = row0 < o.dim ? (int)min((long)(o.dim - row0) * row_bytes, (long)0x7fffffff) : 0;
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(o.wo + (long)(row0 < o.dim ? row0 : 0) * o.q_dim + (long)g * G * HD), 0, valid_bytes,
-      kBufferConfig);
-  u32x4 wv[U];
-  auto issue = [&] {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = lane + 64 * u;
-      const int voff = (c / CPR) * (int)row_bytes + (c % CPR) * 16;
-      wv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, 0, kCpolNt));
-    }
-  };
-  attn_mfma_waves<HD, G, NW, false, false>(a, g, 0, kv_len, sm, issue);
-
-  // the workgroup's attention output for the G heads of g, normalised, into LDS
-  for (int e = tid; e < G * HD; e += 64 * NW) {
-    const int h = e / HD, d = e % HD;
-    float M = kNegBig;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.oml[w][h][0]);
-    float O = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float wt = exp2_fast(sm.oml[w][h][0] - M);
-      O = fmaf(sm.om[w][h][d], wt, O);
-      L = fmaf(sm.oml[w][h][1], wt, L);
-    }
-    ao[e] = O / L;
-  }
-  __syncthreads();
-
   // Wo block . attention output; row sums to lanes 0 .. RW-1, then one atomic per row
   float mine = 0.f;
   if constexpr (CPR >= 64) {
@@ -529,10 +491,132 @@ __global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o
     const unsigned long long old =
         __hip_atomic_fetch_add(o.rowacc + row, term, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned long long w = old + term;
-    if ((int)(w >> kRowAccCountShift) == a.n_kv_heads) {  // the last of the row's nkv terms
-      o.x[row] = xr + rowacc_sum(w, a.n_kv_heads);
+    if ((int)(w >> kRowAccCountShift) == nkv) {  // the last of the row's nkv terms
+      o.x[row] = xr + rowacc_sum(w, nkv);
       __hip_atomic_store(o.rowacc + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+// This wave's Wo rows, columns of kv head g, into registers (streaming loads); rows past dim read as
+// zero (descriptor bound).
+template <int HD, int G, int NW, int U>
+__device__ __forceinline__ void attn_o_issue(const AttnOArgs& o, int g, int row0, int lane, u32x4 (&wv)[U]) {
+  constexpr int CPR = AttnOGeom<HD, G, NW, U>::CPR;
+  const long row_bytes = (long)o.q_dim * 2;
+  const int valid_bytes = row0 < o.dim ? (int)min((long)(o.dim - row0) * row_bytes, (long)0x7fffffff) : 0;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(o.wo + (long)(row0 < o.dim ? row0 : 0) * o.q_dim + (long)g * G * HD), 0, valid_bytes,
+      kBufferConfig);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = lane + 64 * u;
+    const int voff = (c / CPR) * (int)row_bytes + (c % CPR) * 16;
+    wv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, 0, kCpolNt));
+  }
+}
+
+template <int HD, int G, int NW, int U>
+__global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o) {
+  using Geo = AttnOGeom<HD, G, NW, U>;
+  constexpr int RW = Geo::RW;
+  __shared__ AttnMfmaSmem<HD, G, NW> sm;
+  __shared__ __attribute__((aligned(16))) float ao[G * HD];
+  __shared__ float rs[NW][RW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = (int)blockIdx.x % a.n_kv_heads, rb = (int)blockIdx.x / a.n_kv_heads;
+  const int row0 = rb * Geo::RB + wave * RW;
+  const int kv_len = min(a.params->pos + 1, a.msl);  // the host runs this kernel only for pos < msl
+
+  u32x4 wv[U];
+  attn_mfma_waves<HD, G, NW, false, false>(a, g, 0, kv_len, sm, [&] { attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv); });
+
+  // the workgroup's attention output for the G heads of g, normalised, into LDS
+  for (int e = tid; e < G * HD; e += 64 * NW) {
+    const int h = e / HD, d = e % HD;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.oml[w][h][0]);
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = exp2_fast(sm.oml[w][h][0] - M);
+      O = fmaf(sm.om[w][h][d], wt, O);
+      L = fmaf(sm.oml[w][h][1], wt, L);
+    }
+    ao[e] = O / L;
+  }
+  __syncthreads();
+
+  attn_o_rows<HD, G, NW, U>(o, ao, rs, wv, row0, lane, wave, a.n_kv_heads);
+}
+
+// ------------------------------------------------------------------------------------------
+// Slice merge and the O projection in one launch (contexts beyond attn_o's): the split-KV attention
+// launch before it stores every slice's partial (unnormalised output o_s, running maximum m_s in
+// natural units, sum l_s; AttnArgs::defer_merge) and skips its own last-slice merge. Workgroup b
+// (kv head g = b % nkv, rows as attn_o_kernel) requests kv head g's partial block (G heads x nsplit
+// slices x (HD + 2) floats, at most kMergeOMaxSplits slices) before its Wo block, merges
+// out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s) in LDS while the Wo
+// stream is in flight (reference src/infer.cpp:172-187,218-250: one softmax over all keys,
+// restated over slices), then multiplies and combines rows as attn_o_kernel.
+// ------------------------------------------------------------------------------------------
+constexpr int kMergeOMaxSplits = 32;
+
+template <int HD, int G, int NW, int U>
+__global__ void __launch_bounds__(64 * NW) merge_o_kernel(AttnArgs a, AttnOArgs o) {
+  using Geo = AttnOGeom<HD, G, NW, U>;
+  constexpr int RW = Geo::RW, NT = 64 * NW;
+  constexpr int PB = G * kMergeOMaxSplits * (HD + 2);  // floats of the largest partial block
+  constexpr int PPT = (PB / 4 + NT - 1) / NT;             // float4 per thread
+  static_assert((HD + 2) % 2 == 0, "partial rows");
+  __shared__ __attribute__((aligned(16))) float pb[PB];
+  __shared__ float wts[G][kMergeOMaxSplits];
+  __shared__ float linv[G];
+  __shared__ __attribute__((aligned(16))) float ao[G * HD];
+  __shared__ float rs[NW][RW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = (int)blockIdx.x % a.n_kv_heads, rb = (int)blockIdx.x / a.n_kv_heads;
+  const int row0 = rb * Geo::RB + wave * RW;
+  const Positions pss = positions(a.params->pos, a.msl);
+  const int chunk = attn_mfma_chunk(pss.kv_len, a.nsplit, a.min_slice);
+  const int active = (pss.kv_len + chunk - 1) / chunk;  // as the attention launch counted them
+
+  // kv head g's partials: rows (g G + h) nsplit + s of HD + 2 floats, one contiguous block; the
+  // loads go out before the Wo loads, so waiting for them leaves the Wo stream in flight
+  const int nfl = G * a.nsplit * (HD + 2);
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      a.partial + (long)g * G * a.nsplit * (HD + 2), 0, nfl * (int)sizeof(float), kBufferConfig);
+  f32x4 pv[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k)
+    pv[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * (tid + NT * k), 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[U];
+  attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < PPT; ++k)
+    if (4 * (tid + NT * k) < nfl) *reinterpret_cast<f32x4*>(pb + 4 * (tid + NT * k)) = pv[k];
+  __syncthreads();
+  // per head: the slices' weights relative to the largest maximum, and 1 / sum_s w_s l_s
+  if (tid < G * 64) {
+    const int h = tid / 64, s = tid % 64;
+    const float* row = pb + (h * a.nsplit + s) * (HD + 2);
+    const float m = s < active ? row[HD] : kNegBig;
+    const float M = wave_max(m);
+    const float w = s < active ? expf(m - M) : 0.f;
+    const float L = wave_sum(s < active ? w * row[HD + 1] : 0.f);
+    if (s < kMergeOMaxSplits) wts[h][s] = w;
+    if (s == 0) linv[h] = 1.0f / L;
+  }
+  __syncthreads();
+  for (int e = tid; e < G * HD; e += NT) {
+    const int h = e / HD, d = e % HD;
+    float O = 0.f;
+    for (int s = 0; s < active; ++s) O = fmaf(wts[h][s], pb[(h * a.nsplit + s) * (HD + 2) + d], O);
+    ao[e] = O * linv[h];
+  }
+  __syncthreads();
+  attn_o_rows<HD, G, NW, U>(o, ao, rs, wv, row0, lane, wave, a.n_kv_heads);
 }
 }  // namespace yk

@@ -936,6 +936,8 @@ struct AttnArgs {
   float* out;            // [nh][hd]
   int head_dim, n_heads, n_kv_heads, msl, nsplit;
   int min_slice;          // smallest KV slice per workgroup (multiple of 64; MFMA kernel: 0 = by length)
+  int defer_merge = 0;    // MFMA kernel: every slice (one included) stores its partial and the slices are
+                          // merged by the next launch (merge_o_kernel) instead of the last slice
   const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
   AttnPrefetch pf;

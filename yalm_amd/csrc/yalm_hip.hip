@@ -121,13 +121,16 @@ struct yhip_ctx {
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   unsigned* pf_sink = nullptr;
   // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepQkvAttn,
-  // kStepAttnO]
-  hipGraphExec_t graph[3][3] = {};
+  // kStepAttnO, kStepSplitO]
+  hipGraphExec_t graph[3][4] = {};
   // attention and the O projection in one launch (attn_o_kernel) for contexts up to attn_o_max
   // tokens: 108-119 us less per token than the separate launches up to 350 keys, 60 at 500, 17 at
   // 700, slower from ~800 on (Mistral-7B shape on MI355X)
   bool attn_o = true;
   int attn_o_max = 700;
+  // beyond that, the split-KV attention leaves its slice merge to merge_o_kernel, which merges and
+  // runs the O projection in one launch
+  bool split_o = true;
   // decode attention fused into the QKV launch for contexts up to fuse_attn_max tokens (opt-in:
   // measured slower than the separate launch on MI355X, see the design notes)
   bool fuse_attn = false;
@@ -447,23 +450,40 @@ bool attn_o_at(const yhip_ctx* ctx, int pos) {
          pos + 1 <= ctx->attn_o_max;
 }
 
-int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStream_t s) {
+template <int HD, int G>
+void go_merge_o(const yhip_config& c, const AttnArgs& t, const AttnOArgs& o, hipStream_t s) {
+  hipLaunchKernelGGL((merge_o_kernel<HD, G, kAttnOWaves, attn_o_loads<HD, G>()>), dim3(attn_o_blocks<HD, G>(c)),
+                     dim3(64 * kAttnOWaves), 0, s, t, o);
+}
+
+// The step at pos leaves the split-KV attention's slice merge to merge_o_kernel when the option is on,
+// the MFMA attention applies and the slices fit the merge kernel's partial block.
+bool split_o_at(const yhip_ctx* ctx, int pos) {
+  return ctx->split_o && attn_uses_mfma(ctx) && attn_o_shape(ctx->c) && ctx->attn_splits <= kMergeOMaxSplits &&
+         !attn_o_at(ctx, pos);
+}
+
+// merge: false = attn_o_kernel (attention inside), true = merge_o_kernel (partials from the attention
+// launch)
+int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStream_t s, bool merge = false) {
   const yhip_config& c = ctx->c;
+#define YK_AO(HD, G) (merge ? go_merge_o<HD, G>(c, t, o, s) : go_attn_o<HD, G>(c, t, o, s))
   switch (t.head_dim * 16 + t.n_heads / t.n_kv_heads) {
-    case 32 * 16 + 1: go_attn_o<32, 1>(c, t, o, s); break;
-    case 32 * 16 + 2: go_attn_o<32, 2>(c, t, o, s); break;
-    case 32 * 16 + 4: go_attn_o<32, 4>(c, t, o, s); break;
-    case 32 * 16 + 8: go_attn_o<32, 8>(c, t, o, s); break;
-    case 64 * 16 + 1: go_attn_o<64, 1>(c, t, o, s); break;
-    case 64 * 16 + 2: go_attn_o<64, 2>(c, t, o, s); break;
-    case 64 * 16 + 4: go_attn_o<64, 4>(c, t, o, s); break;
-    case 64 * 16 + 8: go_attn_o<64, 8>(c, t, o, s); break;
-    case 128 * 16 + 1: go_attn_o<128, 1>(c, t, o, s); break;
-    case 128 * 16 + 2: go_attn_o<128, 2>(c, t, o, s); break;
-    case 128 * 16 + 4: go_attn_o<128, 4>(c, t, o, s); break;
-    case 128 * 16 + 8: go_attn_o<128, 8>(c, t, o, s); break;
+    case 32 * 16 + 1: YK_AO(32, 1); break;
+    case 32 * 16 + 2: YK_AO(32, 2); break;
+    case 32 * 16 + 4: YK_AO(32, 4); break;
+    case 32 * 16 + 8: YK_AO(32, 8); break;
+    case 64 * 16 + 1: YK_AO(64, 1); break;
+    case 64 * 16 + 2: YK_AO(64, 2); break;
+    case 64 * 16 + 4: YK_AO(64, 4); break;
+    case 64 * 16 + 8: YK_AO(64, 8); break;
+    case 128 * 16 + 1: YK_AO(128, 1); break;
+    case 128 * 16 + 2: YK_AO(128, 2); break;
+    case 128 * 16 + 4: YK_AO(128, 4); break;
+    case 128 * 16 + 8: YK_AO(128, 8); break;
     default: return fail(ctx, YHIP_EINVAL, "attention + O: unsupported shape");
   }
+#undef YK_AO
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention + O launch: ") + hipGetErrorString(e));
   return YHIP_OK;
@@ -472,11 +492,13 @@ int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStrea
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
 // variant: kStepSeparate (every kernel its own launch), kStepQkvAttn (the attention runs inside
-// the QKV launch, fused_attention_at) or kStepAttnO (attention and O in one launch, attn_o_at).
-enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2 };
+// the QKV launch, fused_attention_at), kStepAttnO (attention and O in one launch, attn_o_at) or
+// kStepSplitO (split-KV attention, then slice merge and O in one launch, split_o_at).
+enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3 };
 int step_variant(const yhip_ctx* ctx, int pos) {
   if (fused_attention_at(ctx, pos)) return kStepQkvAttn;  // opt-in, so it takes precedence
-  return attn_o_at(ctx, pos) ? kStepAttnO : kStepSeparate;
+  if (attn_o_at(ctx, pos)) return kStepAttnO;
+  return split_o_at(ctx, pos) ? kStepSplitO : kStepSeparate;
 }
 
 int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
@@ -547,19 +569,23 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       t.pf.magic = 0x9E3779B9u;
       t.pf.sink = ctx->pf_sink;
     }
-    if (variant == kStepAttnO) {
-      // 2 + 3. attention and O-proj + residual in one launch
+    if (variant == kStepSplitO) {  // 2. attention, its slices merged by the O launch
+      t.defer_merge = 1;
+      if ((rc = launch_attention(ctx, t, s))) return rc;
+    }
+    if (variant == kStepAttnO || variant == kStepSplitO) {
+      // 2 + 3. attention (or its slice merge) and O-proj + residual in one launch
       AttnOArgs o;
       o.wo = L.wo;
       o.x = ctx->x;
       o.rowacc = ctx->rowacc;
       o.dim = c.dim;
       o.q_dim = qd;
-      if ((rc = launch_attn_o(ctx, t, o, s))) return rc;
+      if ((rc = launch_attn_o(ctx, t, o, s, variant == kStepSplitO))) return rc;
     }
     if (variant == kStepSeparate && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
-    if (variant != kStepAttnO) {
+    if (variant != kStepAttnO && variant != kStepSplitO) {
     a = mv_base();
     a.w0 = L.wo;
     a.row_step = 2L * qd;
@@ -1578,6 +1604,8 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     ctx->attn_splits = value;
   } else if (!strcmp(key, "attn_mfma")) {
     ctx->attn_mfma = value != 0;
+  } else if (!strcmp(key, "split_o")) {
+    ctx->split_o = value != 0;
   } else if (!strcmp(key, "attn_o")) {
     ctx->attn_o = value != 0;
   } else if (!strcmp(key, "attn_o_max")) {
