@@ -82,14 +82,17 @@ struct AttnMfmaSmem {
 // query heads of g, in a workgroup of NW waves: every wave's (m, l, o) lands in sm.om / sm.oml,
 // then a workgroup barrier. COH: q and the K/V entries are read with agent-coherent loads (they
 // were written by other workgroups of the same launch: the QKV kernel with the attention fused in).
-// DB: two tile buffers per wave. `issue()` runs once in every wave, right after the wave's first
+// NB: tile buffers per wave -- 1 (each tile loaded after the previous one is used) or 2 (the next
+// tile's loads in flight while the current one is used). `issue()` runs once in every wave, right
+// after the wave's first
 // K/V tile and its q loads are issued (at once in a wave without a tile): loads it issues are
 // younger than those, and loads retire in issue order, so waiting for the tile and q does not wait
 // for them.
-template <int HD, int G, int NW, bool COH, bool DB, class Issue>
+template <int HD, int G, int NW, bool COH, int NB, class Issue>
 __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_begin, int t_end,
                                                 AttnMfmaSmem<HD, G, NW>& sm, Issue issue) {
   static_assert(HD % 32 == 0 && G >= 1 && G <= 8, "head_dim % 32, 1..8 query heads per kv head");
+  static_assert(NB == 1 || NB == 2, "tile buffers per wave");
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int TS = 32;  // keys per wave tile
   constexpr int CPOL = COH ? kCpolSc1 : 0;
@@ -215,12 +218,12 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma_16x16x32(f.v[dt], pb, acc[dt]);
     };
-    // Two register buffers used alternately (unrolled by two, no copies between them): while one
-    // tile is used the next one's loads are in flight, and the scheduling barrier keeps them at the
-    // top. The explicit wait for the current tile is free in the steady state and keeps the
-    // compiler from waiting on the in-flight tile inside the current one. DB false: one buffer,
+    // NB = 2: two register buffers used alternately (unrolled by two, no copies between them):
+    // while one tile is used the next one's loads are in flight, and the scheduling barrier keeps
+    // them at the top. The explicit wait for the current tile is free in the steady state and keeps
+    // the compiler from waiting on the in-flight tile inside the current one. NB = 1: one buffer,
     // each tile loaded after the previous one is used (fewer registers, for short slices).
-    if constexpr (!DB) {
+    if constexpr (NB == 1) {
       for (;;) {
         tile(cur, t0);
         t0 += TS * NW;
@@ -273,9 +276,9 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
   __syncthreads();
 }
 
-// One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g (COH, DB as
+// One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g (COH, NB as
 // attn_mfma_waves).
-template <int HD, int G, int NW, bool COH, bool DB = true>
+template <int HD, int G, int NW, bool COH, int NB = 2>
 __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int split, const Positions& pss,
                                                AttnMfmaSmem<HD, G, NW>& sm) {
   constexpr int NT = 64 * NW;
@@ -290,7 +293,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
     rotate_sinks<HD, NT>(a, a.kcache + (long)g * HD * a.msl, pss.kv_sink, tid);
     __syncthreads();
   }
-  attn_mfma_waves<HD, G, NW, COH, DB>(a, g, t_begin, t_end, sm, [] {});
+  attn_mfma_waves<HD, G, NW, COH, NB>(a, g, t_begin, t_end, sm, [] {});
   auto& om = sm.om;
   auto& oml = sm.oml;
 
@@ -323,7 +326,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
   attn_merge_slices<HD, G, NT, false>(a, g, active, tid, sm.mrg, sm.Ls, sm.last_flag);
 }
 
-template <int HD, int G, int NW>
+template <int HD, int G, int NW, int NB = 2>
 __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
   if ((int)blockIdx.y >= a.nsplit) {
     const int j = ((int)blockIdx.y - a.nsplit) * (int)gridDim.x + (int)blockIdx.x;
@@ -331,7 +334,7 @@ __global__ void __launch_bounds__(64 * NW) attn_mfma_kernel(AttnArgs a) {
     return;
   }
   __shared__ AttnMfmaSmem<HD, G, NW> sm;
-  attn_mfma_body<HD, G, NW, false>(a, blockIdx.x, blockIdx.y, positions(a.params->pos, a.msl), sm);
+  attn_mfma_body<HD, G, NW, false, NB>(a, blockIdx.x, blockIdx.y, positions(a.params->pos, a.msl), sm);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -386,7 +389,7 @@ __global__ void __launch_bounds__(kBlock) qkv_attn_kernel(MatvecArgs m, AttnArgs
   const int item = (int)gridDim.x - 1 - (int)blockIdx.x;
   if (item >= items) return;
   wait_split_count(done, gridDim.x, abort_flag);  // every row of q, K and V is written
-  attn_mfma_body<HD, G, kWavesPerBlock, true, false>(a, item % a.n_kv_heads, item / a.n_kv_heads, pss, sm);
+  attn_mfma_body<HD, G, kWavesPerBlock, true, 1>(a, item % a.n_kv_heads, item / a.n_kv_heads, pss, sm);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -528,7 +531,7 @@ __global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o
   const int kv_len = min(a.params->pos + 1, a.msl);  // the host runs this kernel only for pos < msl
 
   u32x4 wv[U];
-  attn_mfma_waves<HD, G, NW, false, false>(a, g, 0, kv_len, sm, [&] { attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv); });
+  attn_mfma_waves<HD, G, NW, false, 1>(a, g, 0, kv_len, sm, [&] { attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv); });
 
   // the workgroup's attention output for the G heads of g, normalised, into LDS
   for (int e = tid; e < G * HD; e += 64 * NW) {
