@@ -116,8 +116,15 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * results do not depend on it), "stats" (1 = time every synchronised step on the device with HIP
  * events and reset the totals; 0 = off), "fuse_attn" (1 = run the decode attention inside the QKV
  * launch for steps with at most "fuse_attn_max" cached tokens (default 1024), below max_seq_len,
- * on the matrix-core attention's shapes; 0 = its own launch, the default, measured faster).
- * With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
+ * on the matrix-core attention's shapes; 0 = its own launch, the default, measured faster),
+ * "attn_o" (1 = default: for steps with at most "attn_o_max" cached tokens (default 700), below
+ * max_seq_len, on the matrix-core attention's shapes with at most 15 kv heads, attention and the O
+ * projection run in one launch whose workgroups each repeat their kv head's attention and combine
+ * their rows of Wo . attention in per-row integer words, bit-reproducibly; 0 = separate launches),
+ * "split_o" (1 = default: beyond that, the split-KV attention stores every slice's partial and the
+ * O launch merges them, with at most 32 slices per kv head; 0 = the attention launch merges its
+ * own slices). The results of every option setting agree to fp32 rounding; each is tested against
+ * the CPU reference. With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
  * GEMM variant: stages -1 = chosen per shape (default), 0 = register-staged kernel, 1 = 256 x 256
