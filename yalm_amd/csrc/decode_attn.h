@@ -413,8 +413,9 @@ __global__ void __launch_bounds__(kBlock) qkv_attn_kernel(MatvecArgs m, AttnArgs
 // (CPR = G*HD/8 16-byte chunks per row segment); a wave covers U * 64 / CPR rows.
 //
 // The per-row word: bits 0..59 hold the sum of the terms 2^55 + round(p 2^32) added so far (p: one
-// workgroup's fp32 partial product for that row, clamped to |p| < 2^23; each term is below 2^56, so
-// up to 15 of them never carry into bit 60), bits 60..63 count the additions. Every workgroup adds
+// workgroup's fp32 partial product for that row, clamped to |p 2^32| <= 2^55 - 2^32, i.e. |p| just
+// under 2^23; each term is below 2^56, so up to 15 of them never carry into bit 60), bits 60..63
+// count the additions. Every workgroup adds
 // its term plus 2^60 with one returning 64-bit atomic; the one whose addition brings the count to
 // nkv holds all terms in (returned value + its own), writes x[row] += (sum - nkv 2^55) 2^-32 and
 // clears the word for the next launch. Integer addition is associative, so x does not depend on the
@@ -434,10 +435,11 @@ constexpr unsigned long long kRowAccBias = 1ull << 55;
 constexpr float kRowAccScale = 4294967296.0f;  // 2^32
 constexpr int kRowAccMaxTerms = 15;
 
-// This workgroup's term for one row: 2^60 (the count) + 2^55 + round(p 2^32), |p 2^32| < 2^55.
+// This workgroup's term for one row: 2^60 (the count) + 2^55 + round(p 2^32).
 __device__ __forceinline__ unsigned long long rowacc_term(float p) {
+  constexpr float kLim = 36028792723996672.0f;  // 2^55 - 2^32, the largest float below 2^55
   float v = rintf(p * kRowAccScale);
-  v = fminf(fmaxf(v, -36028797018963960.0f), 36028797018963960.0f);  // 2^55 - 2^31 (float-representable)
+  v = fminf(fmaxf(v, -kLim), kLim);
   return (1ull << kRowAccCountShift) + kRowAccBias + (unsigned long long)(long long)v;
 }
 // The row's fp32 sum from a completed word (count n): (value bits - n 2^55) 2^-32.
