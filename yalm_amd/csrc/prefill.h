@@ -62,6 +62,7 @@ struct GemmArgs {
   // the word a timed-out wait sets.
   unsigned* sk_flags;
   unsigned* abort_flag;
+  int interleave;  // large tiles: the interleaved k-step schedule (BigTile::mainloop<true>)
 };
 
 constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
@@ -267,8 +268,8 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
       brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + kbeg + 8 * c;
     }
   }
-  auto issue = [&](int kt) {
-    const int st = kt % S, k0 = kt * BK;
+  auto issue = [&](int kt, int kdata) {  // stage slot of k-step kt, filled with k-step kdata
+    const int st = kt % S, k0 = kdata * BK;
 #pragma unroll
     for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, &smem[st][(wave + NW * j) * 512]);
 #pragma unroll
@@ -294,7 +295,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
   const int nk = kspan / BK;
 #pragma unroll
   for (int kt = 0; kt < S - 1; ++kt)
-    if (kt < nk) issue(kt);
+    if (kt < nk) issue(kt, kt);
   for (int kt = 0; kt < nk; ++kt) {
     // k-step kt has landed once at most S - 2 later stages (LPS loads each) are outstanding
     if (kt + S - 2 < nk) wait_vmcnt<LPS * (S - 2)>();
@@ -305,7 +306,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
     __asm__ volatile("" ::: "memory");  // no LDS access moves across the barrier
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    if (kt + S - 1 < nk) issue(kt + S - 1);
+    if (kt + S - 1 < nk) issue(kt + S - 1, kt + S - 1);
     const uint16_t* As = smem[kt % S];
     const uint16_t* Bs = smem[kt % S] + ATILE;
     u32x4 fa[2][2], fb[2][2];
@@ -427,6 +428,11 @@ struct BigTile {
   // pipeline; every wave of the workgroup takes part (the LDS stages are reused afterwards).
   // tid = threadIdx.x (a persistent caller passes an opaque copy so its per-lane indexing is not
   // hoisted out of the tile loop and kept live across it).
+  // IL: every k-step issues its copy unconditionally (a stage past the end re-reads the last k-step
+  // into a slot nobody reads) so that the step is one basic block, and the copies and the next
+  // fragments' LDS reads are interleaved with the MFMAs (scheduling groups) instead of bunched
+  // after the barrier.
+  template <bool IL = false>
   static __device__ __forceinline__ void mainloop(const GemmArgs& g, uint16_t* smem, int m0, int n0, int kt0, int kt1,
                                                   f32x16 (&acc)[4][4], int tid) {
     const int lane = tid & 63, wave = tid >> 6;
@@ -450,9 +456,9 @@ struct BigTile {
         brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
       }
     }
-    auto issue = [&](int kt) {
+    auto issue = [&](int kt, int kdata) {
       uint16_t* st = smem + ((kt - kt0) % S) * STAGE;
-      const int k0 = kt * BK;
+      const int k0 = kdata * BK;
 #pragma unroll
       for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
 #pragma unroll
@@ -470,19 +476,25 @@ struct BigTile {
     };
 #pragma unroll
     for (int kt = kt0; kt < kt0 + S - 1; ++kt)
-      if (kt < kt1) issue(kt);
+      if (IL || kt < kt1) issue(kt, min(kt, kt1 - 1));
     for (int kt = kt0; kt < kt1; ++kt) {
       // k-step kt has landed once at most S - 2 later stages are outstanding
-      if (kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
+      if (IL || kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
       else wait_vmcnt<0>();
       __asm__ volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
       __asm__ volatile("" ::: "memory");
-      if (kt + S - 1 < kt1) issue(kt + S - 1);
       const uint16_t* As = smem + ((kt - kt0) % S) * STAGE;
       const uint16_t* Bs = As + ATILE;
       u32x4 fa[2][4], fb[2][4];
-      read_frags(As, Bs, 0, fa[0], fb[0]);
+      if constexpr (IL) {
+        read_frags(As, Bs, 0, fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(kt + S - 1, min(kt + S - 1, kt1 - 1));
+      } else {
+        if (kt + S - 1 < kt1) issue(kt + S - 1, kt + S - 1);
+        read_frags(As, Bs, 0, fa[0], fb[0]);
+      }
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
@@ -491,7 +503,22 @@ struct BigTile {
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
       }
+      if constexpr (IL) {
+        // per 16 MFMAs of a kk step: one LDS read of the next step's fragments after every other
+        // MFMA (8), one copy after every fourth (LPS over the k-step)
+        constexpr int VPK = (LPS + KK - 1) / KK;  // copies per kk step
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (kk + 1 < KK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < VPK) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          }
+      }
     }
+    if constexpr (IL) wait_vmcnt<0>();  // the copies past the end land before the stages are reused
     // the next tile's loads reuse the stages: every wave is done reading them
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -557,7 +584,10 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  T::mainloop(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
+  if (g.interleave)
+    T::template mainloop<true>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
+  else
+    T::mainloop(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
   T::epilogue(g, tm * kBigM, tn * T::NC, acc, threadIdx.x);
 }
 

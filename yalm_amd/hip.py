@@ -251,6 +251,12 @@ def set_gemm_stages(n, bk=32, bm=128):
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
 
 
+def set_gemm_interleave(on=True):
+    """Large-tile prefill GEMM: copies and fragment reads interleaved with the MFMAs (default) or the
+    compiler's own order."""
+    _check(lib().yhip_set_option(None, b"gemm_il", int(bool(on))))
+
+
 def set_gemm_ksplit(n=0):
     """Prefill GEMM K splits on the LDS-pipeline kernel: 0 = chosen per shape (split when the output
     has too few tiles to fill the GPU), n >= 1 = forced (must divide the k-steps)."""
