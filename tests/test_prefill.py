@@ -25,10 +25,10 @@ def hip():
 
 # (LDS stages, k-step, workgroup rows, large-tile k-step schedule interleaved); 0 stages = the
 # register-staged kernel
-GEMM_VARIANTS = [(-1, 32, 128, 1), (4, 32, 128, 1), (2, 64, 128, 1), (3, 64, 128, 1), (2, 64, 256, 1),
-                 (3, 64, 256, 1), (1, 64, 256, 1), (1, 32, 256, 1), (1, 64, 256, 0), (1, 32, 256, 0),
-                 (0, 32, 128, 1),
-                 (5, 64, 256, 1)]  # -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K
+GEMM_VARIANTS = [(-1, 32, 128, -1), (4, 32, 128, -1), (2, 64, 128, -1), (3, 64, 128, -1), (2, 64, 256, -1),
+                 (3, 64, 256, -1), (1, 64, 256, 1), (1, 32, 256, 1), (1, 64, 256, 2), (1, 32, 256, 2),
+                 (1, 64, 256, 0), (1, 32, 256, 0), (0, 32, 128, -1),
+                 (5, 64, 256, -1)]  # -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K
 
 
 @pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}i{i}" for s, k, m, i in GEMM_VARIANTS])
@@ -37,7 +37,7 @@ def gemm_variant(request):
     hip().set_gemm_interleave(request.param[3])
     yield request.param
     hip().set_gemm_stages(-1)
-    hip().set_gemm_interleave(True)
+    hip().set_gemm_interleave(-1)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096),

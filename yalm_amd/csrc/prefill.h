@@ -432,7 +432,7 @@ struct BigTile {
   // into a slot nobody reads) so that the step is one basic block, and the copies and the next
   // fragments' LDS reads are interleaved with the MFMAs (scheduling groups) instead of bunched
   // after the barrier.
-  template <bool IL = false>
+  template <int IL = 0>
   static __device__ __forceinline__ void mainloop(const GemmArgs& g, uint16_t* smem, int m0, int n0, int kt0, int kt1,
                                                   f32x16 (&acc)[4][4], int tid) {
     const int lane = tid & 63, wave = tid >> 6;
@@ -456,14 +456,18 @@ struct BigTile {
         brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
       }
     }
-    auto issue = [&](int kt, int kdata) {
+    // the stage's copies j0 .. j1 - 1 (A pieces first, then B)
+    auto issue_part = [&](int kt, int kdata, int j0, int j1) {
       uint16_t* st = smem + ((kt - kt0) % S) * STAGE;
       const int k0 = kdata * BK;
 #pragma unroll
-      for (int j = 0; j < IA; ++j) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
-#pragma unroll
-      for (int j = 0; j < IB; ++j) load_lds16(brow[j] + k0, st + ATILE + (wave + 4 * j) * 512);
+      for (int j = 0; j < IA + IB; ++j) {
+        if (j < j0 || j >= j1) continue;
+        if (j < IA) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
+        else load_lds16(brow[j - IA] + k0, st + ATILE + (wave + 4 * (j - IA)) * 512);
+      }
     };
+    auto issue = [&](int kt, int kdata) { issue_part(kt, kdata, 0, IA + IB); };
     auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
       const int c = 2 * kk + (lane >> 5);
 #pragma unroll
@@ -476,10 +480,10 @@ struct BigTile {
     };
 #pragma unroll
     for (int kt = kt0; kt < kt0 + S - 1; ++kt)
-      if (IL || kt < kt1) issue(kt, min(kt, kt1 - 1));
+      if (IL != 0 || kt < kt1) issue(kt, min(kt, kt1 - 1));
     for (int kt = kt0; kt < kt1; ++kt) {
       // k-step kt has landed once at most S - 2 later stages are outstanding
-      if (IL || kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
+      if (IL != 0 || kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
       else wait_vmcnt<0>();
       __asm__ volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
@@ -487,7 +491,28 @@ struct BigTile {
       const uint16_t* As = smem + ((kt - kt0) % S) * STAGE;
       const uint16_t* Bs = As + ATILE;
       u32x4 fa[2][4], fb[2][4];
-      if constexpr (IL) {
+      if constexpr (IL == 2) {
+        // fenced phases: phase kk issues the reads of kk + 1 and a quarter of the next stage's
+        // copies, then its 16 MFMAs; the fences keep each phase's reads ahead of its MFMAs, so the
+        // wait before phase kk + 1 finds them done
+        constexpr int VPK = (LPS + KK - 1) / KK;
+        const int kn = min(kt + S - 1, kt1 - 1);
+        read_frags(As, Bs, 0, fa[0], fb[0]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+          issue_part(kt + S - 1, kn, kk * VPK, (kk + 1) * VPK);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
+      if constexpr (IL == 1) {
         read_frags(As, Bs, 0, fa[0], fb[0]);
         __builtin_amdgcn_sched_barrier(0);
         issue(kt + S - 1, min(kt + S - 1, kt1 - 1));
@@ -503,7 +528,7 @@ struct BigTile {
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
       }
-      if constexpr (IL) {
+      if constexpr (IL == 1) {
         // per 16 MFMAs of a kk step: one LDS read of the next step's fragments after every other
         // MFMA (8), one copy after every fourth (LPS over the k-step)
         constexpr int VPK = (LPS + KK - 1) / KK;  // copies per kk step
@@ -518,7 +543,7 @@ struct BigTile {
           }
       }
     }
-    if constexpr (IL) wait_vmcnt<0>();  // the copies past the end land before the stages are reused
+    if constexpr (IL != 0) wait_vmcnt<0>();  // the copies past the end land before the stages are reused
     // the next tile's loads reuse the stages: every wave is done reading them
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -584,8 +609,10 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  if (g.interleave)
-    T::template mainloop<true>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
+  if (g.interleave == 2)
+    T::template mainloop<2>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
+  else if (g.interleave)
+    T::template mainloop<1>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
   else
     T::mainloop(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
   T::epilogue(g, tm * kBigM, tn * T::NC, acc, threadIdx.x);

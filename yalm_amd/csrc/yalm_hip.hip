@@ -32,10 +32,11 @@ thread_local std::string g_thread_err;
 // yhip_set_option(NULL, "test_bpc", n) so tests can force many row groups per wave.
 int g_test_bpc = 0;
 bool g_attn_mfma = true;  // attention kernel of the kernel-level entry points (process-wide option)
-// Large-tile prefill GEMM k-step schedule: 1 = copies and fragment reads interleaved with the MFMAs
-// (BigTile::mainloop<true>, default), 0 = the compiler's own order. Measured on MI355X at 3200
-// rows: W1/W3 962 -> 884 us, W2 517 -> 470-484 us.
-int g_gemm_il = 1;
+// Large-tile prefill GEMM k-step schedule (BigTile::mainloop<IL>): 0 = the compiler's own order,
+// 1 = copies and fragment reads placed between the MFMAs by scheduling groups, 2 = fenced phases;
+// -1 (default) = per shape: 2 for K >= 8192, else 1. Same box, 3200 rows (us): W1/W3 962 / 890 /
+// 905, W2 510 / 488 / 463.
+int g_gemm_il = -1;
 int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-staged kernel)
 int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
@@ -906,7 +907,7 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (stages == 1) {  // 256 x 256 tiles
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
     GemmArgs gi = g;
-    gi.interleave = g_gemm_il;
+    gi.interleave = g_gemm_il >= 0 ? g_gemm_il : (g.K >= 8192 ? 2 : 1);
     if (bk == 64 && g.K % 64 == 0)
       hipLaunchKernelGGL((gemm_big_kernel<EPI, 2, 64>), tiles8(kBigM, nc), dim3(256), 0, s, gi);
     else
@@ -1559,7 +1560,8 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_il")) {
-      g_gemm_il = value != 0;
+      if (value < -1 || value > 2) return fail(nullptr, YHIP_EINVAL, "gemm_il must be -1 (per shape), 0, 1 or 2");
+      g_gemm_il = value;
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_bk")) {

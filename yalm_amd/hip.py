@@ -251,10 +251,11 @@ def set_gemm_stages(n, bk=32, bm=128):
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
 
 
-def set_gemm_interleave(on=True):
-    """Large-tile prefill GEMM: copies and fragment reads interleaved with the MFMAs (default) or the
-    compiler's own order."""
-    _check(lib().yhip_set_option(None, b"gemm_il", int(bool(on))))
+def set_gemm_interleave(mode=-1):
+    """Large-tile prefill GEMM k-step schedule: -1 = per shape (default), 0 = the compiler's own
+    order, 1 = copies and fragment reads interleaved with the MFMAs by scheduling groups, 2 = fenced
+    phases."""
+    _check(lib().yhip_set_option(None, b"gemm_il", int(mode)))
 
 
 def set_gemm_ksplit(n=0):
