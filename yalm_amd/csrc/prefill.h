@@ -696,7 +696,12 @@ __global__ void __launch_bounds__(256) gemm_sk_kernel(GemmArgs g, unsigned* flag
             }
       }
     }
-    T::mainloop(g, smem, m0, n0, k0, k1, acc, tid);
+    if (g.interleave == 2)
+      T::template mainloop<2>(g, smem, m0, n0, k0, k1, acc, tid);
+    else if (g.interleave)
+      T::template mainloop<1>(g, smem, m0, n0, k0, k1, acc, tid);
+    else
+      T::mainloop(g, smem, m0, n0, k0, k1, acc, tid);
     if (k1 < KI) {
       // a partial: a later range finishes this tile
       const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(

@@ -896,10 +896,12 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     if (!g.P || !g.sk_flags || !g.abort_flag || g.p_floats < (long)P * kSkSlotFloats)
       return fail(ctx, YHIP_EINVAL, "gemm: stream-K needs a partial slot and a flag per CU");
     const unsigned epoch = ++g_sk_epoch;
+    GemmArgs gi = g;
+    gi.interleave = g_gemm_il >= 0 ? g_gemm_il : (g.K >= 8192 ? 2 : 1);
     if (g.K % 64 == 0)
-      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 2, 64>), dim3(P), dim3(256), 0, s, g, g.sk_flags, epoch, g.abort_flag);
+      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 2, 64>), dim3(P), dim3(256), 0, s, gi, g.sk_flags, epoch, g.abort_flag);
     else
-      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 4, 32>), dim3(P), dim3(256), 0, s, g, g.sk_flags, epoch, g.abort_flag);
+      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 4, 32>), dim3(P), dim3(256), 0, s, gi, g.sk_flags, epoch, g.abort_flag);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
     return YHIP_OK;
