@@ -53,6 +53,7 @@ WEIGHT_BYTES = 14_221_860_864       # all layer weights + lm_head + one embeddin
 KV_BYTES_PER_POS = 131_072          # 32 layers x 8 kv heads x 128 x (K + V) x 2 bytes
 W13_BYTES = 2 * 14336 * 4096 * 2 + 4096 * 4 * 2 + 14336 * 4  # weights + x + gain + hb out
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
+GREEDY_CHECK = 32  # generated tokens the CPU baseline compares with the GPU's, at least
 
 
 def prefill_flops(cfg, n, start=0):
@@ -331,7 +332,11 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         log(f"[bench] CPU baseline (oracle, {args.cpu_seconds:.0f} s decode budget)")
-        cpu = cpu_baseline(sess, cfg, prompt, [int(t) for t in toks], args.cpu_seconds)
+        gpu_toks = [int(t) for t in toks]
+        if len(gpu_toks) < GREEDY_CHECK:  # the greedy contract covers the first 32 generated tokens
+            more, _, _ = sess.generate(prompt, GREEDY_CHECK, temperature=0.0, device_argmax=True)
+            gpu_toks = [int(t) for t in more]
+        cpu = cpu_baseline(sess, cfg, prompt, gpu_toks, args.cpu_seconds)
         log(f"[bench] CPU: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['host']['model']}); {cpu['sample']}")
 
     def traffic_of(name):
