@@ -916,6 +916,10 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     const uint16_t* qrow = a.Q + (long)min(my_q, a.n - 1) * qd + h * HD + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks);
+    // kept in registers for the whole loop (left alone, the compiler reloads them from memory for
+    // every key tile and waits for each load in front of its MFMA)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) __asm__ volatile("" : "+v"(qf[ks]));
   }
   f32x16 o[DT];
 #pragma unroll
@@ -968,11 +972,15 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1, k0 = kt * 32;
     if (kt + 1 < nkt) gload(k0 + 32);
-    // S^T = K Q^T
+    // S^T = K Q^T; the tile's K fragments are all requested before the first MFMA
     f32x16 s = f32x16{};
     const uint16_t* krow = &Ks[buf][(lane & 31) * KLD + 8 * half];
+    u32x4 kf[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(*reinterpret_cast<const u32x4*>(krow + 16 * ks), qf[ks], s);
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(krow + 16 * ks);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(kf[ks], qf[ks], s);
     // mask (key position > query position), scale, tile max of this query
     float mt = kNegBig;
     if (k0 + 31 <= a.start + q0) {  // every key of the tile precedes the wave's first query
@@ -1012,18 +1020,25 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     // O^T += V^T P^T; k order of step kk: keys 16 kk + {0..3, 8..11} + 4 half of the tile
     // rescale only when some query's running maximum moved (after the first tiles it rarely does)
     const bool rescale = __any(corr != 1.f);
+    // the tile's V fragments, all requested before the first value MFMA
+    u32x4 vf[DT][2];
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      if (rescale)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
       const uint16_t* vrow = &Vs[buf][(t * 32 + (lane & 31)) * VLD + 4 * half];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * kk);
         const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * kk + 8);
-        o[t] = mfma32(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[kk], o[t]);
+        vf[t][kk] = u32x4{lo.x, lo.y, hi.x, hi.y};
       }
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      if (rescale)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) o[t] = mfma32(vf[t][kk], pf[kk], o[t]);
     }
     if (kt + 1 < nkt) lstore(buf ^ 1);
     __syncthreads();
