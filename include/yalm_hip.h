@@ -189,8 +189,9 @@ int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* 
 int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16_t* b3, int M, int N, int K, int mode, int act,
                    float* c, uint16_t* h);
 /* The prefill GEMM variant yhip_prefill runs for this shape and mode (as yhip_test_gemm), under the
- * current process-wide options: stages 1 = the 256 x 256 large-tile kernel, 2..4 = the LDS
- * pipeline's depth, 0 = the register-staged kernel; bk the k-step; bm the workgroup's rows. No
+ * current process-wide options: stages 6 = the eight-wave 256 x 256 kernel, 1 = the four-wave
+ * 256 x 256 kernel, 5 = the same with stream-K, 2..4 = the LDS pipeline's depth, 0 = the
+ * register-staged kernel; bk the k-step; bm the workgroup's rows. No
  * reference counterpart (the reference has no batched prefill). */
 int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int* bk, int* bm);
 /* Greedy argmax on the device with the reference tie rule. */

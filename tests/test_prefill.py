@@ -28,7 +28,9 @@ def hip():
 GEMM_VARIANTS = [(-1, 32, 128, -1), (4, 32, 128, -1), (2, 64, 128, -1), (3, 64, 128, -1), (2, 64, 256, -1),
                  (3, 64, 256, -1), (1, 64, 256, 1), (1, 32, 256, 1), (1, 64, 256, 2), (1, 32, 256, 2),
                  (1, 64, 256, 0), (1, 32, 256, 0), (0, 32, 128, -1),
-                 (5, 64, 256, -1)]  # -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K
+                 (5, 64, 256, -1), (6, 64, 256, -1)]
+# -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K; 6: the eight-wave 256 x 256
+# kernel (K % 64 == 0; otherwise it falls back to the 32-deep four-wave one)
 
 
 @pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}i{i}" for s, k, m, i in GEMM_VARIANTS])
@@ -41,7 +43,7 @@ def gemm_variant(request):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096),
-                                   (130, 128, 448), (520, 256, 128)])
+                                   (130, 128, 448), (520, 256, 128), (70, 200, 64)])
 def test_gemm_store_and_residual(M, N, K, gemm_variant):
     H = hip()
     rng = np.random.default_rng(M * 7 + N)
@@ -234,15 +236,18 @@ MISTRAL2 = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_he
                 max_seq_len=4096, rotary_dim=128)
 
 
-def test_gemm_variants_chosen_at_3200_rows():
-    # the per-shape choice the 3200-token prefill runs (checked before the parity tests rely on it):
-    # the 256 x 256 kernel for W1/W3 + SwiGLU and for W2's 14336-long rows, the 128-row LDS pipeline
-    # for QKV and O
+def test_gemm_variants_chosen_per_shape():
+    # the per-shape choice the prefill runs (checked before the parity tests rely on it): at 3200
+    # rows every Mistral-7B GEMM takes the eight-wave 256 x 256 kernel; with fewer rows (the
+    # 256 x 256 grid under 9/16 of the CUs) the 128-row LDS pipeline, 256-row workgroups for W1/W3
     H = hip()
-    assert H.gemm_variant(3200, 14336, 4096, 2)[0] == 1
-    assert H.gemm_variant(3200, 4096, 14336, 1)[0] == 1
-    assert H.gemm_variant(3200, 6144, 4096, 0) == (2, 64, 128)
-    assert H.gemm_variant(3200, 4096, 4096, 1) == (2, 64, 128)
+    for mode, N, K in [(2, 14336, 4096), (1, 4096, 14336), (0, 6144, 4096), (1, 4096, 4096)]:
+        assert H.gemm_variant(3200, N, K, mode) == (6, 64, 256)
+    assert H.gemm_variant(256, 14336, 4096, 2) == (2, 64, 256)
+    assert H.gemm_variant(512, 14336, 4096, 2) == (6, 64, 256)
+    assert H.gemm_variant(1024, 4096, 4096, 1) == (2, 64, 128)
+    assert H.gemm_variant(200, 6144, 4096, 0) == (2, 64, 128)
+    assert H.gemm_variant(3200, 6144, 4000, 0)[0] == 4  # K % 64 != 0: the 32-deep LDS pipeline
 
 
 @pytest.mark.parametrize("variant", ["auto", "stream_k"])
@@ -286,9 +291,9 @@ def test_gemm_production_shapes_at_3200_rows(mode, N, K, variant):
 
 def test_prefill_3200_tokens_mistral_shape_then_30_decode_steps():
     # The long-context workload at its own size on a two-layer Mistral-shape model (ctx 4096): one
-    # batched prefill of 3200 seeded ids (256 x 256 GEMM tiles for W1/W3 and W2, 100 query tiles
-    # of prefill attention) against the reference's sequential hydrate (src/main.cpp:169-177), then
-    # 30 decode steps at kv ~3200 on both sides from their own caches.
+    # batched prefill of 3200 seeded ids (eight-wave 256 x 256 GEMM tiles for all four GEMMs, 100
+    # query tiles of prefill attention) against the reference's sequential hydrate
+    # (src/main.cpp:169-177), then 30 decode steps at kv ~3200 on both sides from their own caches.
     cfg = dict(MISTRAL2)
     t = np_tensors(cfg, seed=3200)
     toks = np.random.default_rng(3201).integers(0, cfg["vocab_size"], 3200)

@@ -619,6 +619,176 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Eight-wave large-tile GEMM ("ping-pong"): 256 x 256 per workgroup as in gemm_big_kernel, but two
+// waves per SIMD. Each wave owns a 128 x 64 block of the tile (2 x 4 layout, accumulators 4 x 2
+// tiles of 32 x 32) and alternates a memory phase (the LDS fragment reads of its next 32-deep
+// half-step, then copies) with a compute phase (that half-step's 16 MFMAs on registers only). Waves
+// 0-3 and 4-7 form two groups; group 1 runs one phase behind group 0 and a workgroup barrier ends
+// every phase, so while one wave of a SIMD (waves w and w + 4 share one) issues MFMAs the other one
+// fetches.
+// k-steps are 64 deep (K % 64 == 0): the copies move 128 B row pieces, whole cache lines (measured:
+// 1.6x the copy rate of 64 B pieces). LDS is a ring of five 32 KB slots holding k-panels as items
+// A_s = 2s and B_s = 2s + 1 (slot = item % 5). Stage s is read in phases 4s .. 4s + 3 (group 0 half 0,
+// group 1 half 0, group 0 half 1, group 1 half 1). Every memory phase first reads its fragments and
+// then copies a quarter of a stage: the first one of stage s the wave's share of B_{s+1}, the second
+// one its share of A_{s+2} (their slots held A_{s-1} and B_{s-1}, last read in phase 4s - 1). So each
+// phase carries 16 KB of copies, which the CU's address unit drains well within the phase (a
+// memory phase that issued its copies before its reads, or carried a whole stage, stalled on them:
+// measured), and every copy has at least three phases to land. A_{s+1} and B_{s+1} are waited for
+// at the end of phase 4s + 3 (group 0 after its last compute phase of the stage, group 1 after its
+// last memory phase), before the barrier after which group 0 reads stage s + 1.
+// Copies past the last k-step re-read it into a slot that is not read again, so every phase has
+// the same shape.
+// SwiGLU: the B rows of a tile are W1 and W3 interleaved by 32 as in gemm_big_kernel, so a wave's
+// two column tiles are W1 and W3 of the same 32 outputs.
+// ------------------------------------------------------------------------------------------
+template <int EPI>
+struct PPTile {
+  static constexpr int BK = 64, SLOTS = 5;
+  static constexpr int CPR = BK / 8, RPI = 1024 / (2 * BK), RPW = 256 / (2 * BK);
+  static constexpr int PANEL = kBigM * BK;                // halves per slot (an A or a B k-panel)
+  static constexpr int LPI = kBigM / RPI / 8;             // copies per wave per panel
+  static constexpr int NC = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;  // output columns per tile
+  static_assert(kBigM == kBigN, "A and B panels share the ring slots");
+  static __device__ __forceinline__ int swz(int r) { return (r / RPW) % CPR; }
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g) {
+  using T = PPTile<EPI>;
+  constexpr int BK = T::BK;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[T::SLOTS * T::PANEL];
+  int tm, tn;
+  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + T::NC - 1) / T::NC, tm, tn)) return;
+  const int m0 = tm * kBigM, n0 = tn * T::NC;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wm = wave & 1, wn = wave >> 1;
+  const int nk = g.K / BK;
+
+  const uint16_t* arow[T::LPI];
+  const uint16_t* brow[T::LPI];
+#pragma unroll
+  for (int j = 0; j < T::LPI; ++j) {
+    const int r = T::RPI * (wave + 8 * j) + lane / T::CPR;
+    const int c = (lane % T::CPR) ^ T::swz(r);
+    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * c;
+    if constexpr (EPI == kGemmSwiGLU) {
+      const int col = n0 + (r >> 6) * 32 + (r & 31);
+      const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
+      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+    } else {
+      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+    }
+  }
+  // item 2s (the A panel) or 2s + 1 (the B panel) of the ring, filled with k-step kdata
+  auto issue_item = [&](int item, int kdata) {
+    uint16_t* st = smem + (item % T::SLOTS) * T::PANEL;
+    const int k0 = kdata * BK;
+    if (item & 1) {
+#pragma unroll
+      for (int j = 0; j < T::LPI; ++j) load_lds16(brow[j] + k0, st + (wave + 8 * j) * 512);
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::LPI; ++j) load_lds16(arow[j] + k0, st + (wave + 8 * j) * 512);
+    }
+  };
+  // the fragments of 32-deep half-step hs (0, 1) of k-step kt
+  u32x4 fa[2][4], fb[2][2];
+  auto read_frags = [&](int kt, int hs) {
+    const uint16_t* As = smem + ((2 * kt) % T::SLOTS) * T::PANEL;
+    const uint16_t* Bs = smem + ((2 * kt + 1) % T::SLOTS) * T::PANEL;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int c = 4 * hs + 2 * kk + (lane >> 5);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int ra = wm * 128 + t * 32 + (lane & 31);
+        fa[kk][t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ T::swz(ra)));
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int rb = wn * 64 + t * 32 + (lane & 31);
+        fb[kk][t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ T::swz(rb)));
+      }
+    }
+  };
+  auto barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  auto compute = [&] {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[kk][i], fb[kk][j], acc[i][j]);
+  };
+  constexpr unsigned kLgkm0 = 0xc07f;  // s_waitcnt lgkmcnt(0): the fragments are in registers
+
+  issue_item(0, 0);
+  issue_item(1, 0);
+  issue_item(2, min(1, nk - 1));
+  wait_vmcnt<T::LPI>();  // A_0 and B_0 have landed
+  barrier();             // stage 0 is in for every wave
+  if (grp == 1) barrier();
+  for (int kt = 0; kt < nk; ++kt) {
+    read_frags(kt, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_item(2 * kt + 3, min(kt + 1, nk - 1));  // B_{kt+1}
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    barrier();
+    compute();
+    barrier();
+    read_frags(kt, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_item(2 * kt + 4, min(kt + 2, nk - 1));  // A_{kt+2}
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    if (grp == 1) wait_vmcnt<T::LPI>();  // this wave's copies of A_{kt+1} and B_{kt+1} have landed
+    barrier();
+    compute();
+    if (grp == 0) wait_vmcnt<T::LPI>();
+    barrier();
+  }
+  wait_vmcnt<0>();
+  if (grp == 0) barrier();
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 128 + i * 32 + acc_row(r, lane);
+      if (m >= g.M) continue;
+      if constexpr (EPI == kGemmSwiGLU) {
+        const int j = n0 + wn * 32 + (lane & 31);
+        if (j < g.N) {
+          const float a1 = acc[i][0][r], a3 = acc[i][1][r];
+          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+          if (n >= g.N) continue;
+          float* cp = g.C + (long)m * g.ldc + n;
+          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
+          else *cp = acc[i][j][r];
+        }
+      }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Stream-K variant of the large-tile GEMM: one workgroup per CU, and the grid's k-steps (tiles x
 // K / BK, tiles M-fastest) dealt out evenly as contiguous ranges, so no CU idles when the tile
 // count is not a multiple of the CU count (a 3200 x 4096 output has 208 tiles of 256 x 256). The

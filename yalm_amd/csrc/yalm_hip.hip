@@ -855,37 +855,38 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 // ---- batched prefill ---------------------------------------------------------------------------
 // The prefill GEMM variant for an epilogue and shape (stages 1 = the 256 x 256 kernel, 2..4 the
 // LDS pipeline's depth, 0 the register-staged kernel), or the forced process-wide one.
-void gemm_choice(int epi, int M, int K, int& stages, int& bk, int& bm) {
+void gemm_choice(int epi, int M, int N, int K, int cus, int& stages, int& bk, int& bm) {
   stages = g_gemm_stages;
   bk = g_gemm_bk;
   bm = g_gemm_bm;
   if (!g_gemm_auto) return;
-  // Variant per shape, from a sweep of the Mistral-7B shapes over M = 64..3200 on MI355X: the
-  // 256 x 256 tiles win only from ~3K rows (W1/W3, and W2 with its 14336-long rows); below that the
-  // 128-row LDS pipeline wins (up to 2.9x for W2 at a few hundred rows), with 256-row workgroups
-  // in between for W1/W3 and W2.
+  // Variant per shape, from sweeps of the Mistral-7B shapes over M = 256..4096 on MI355X: the
+  // eight-wave 256 x 256 kernel wins once its tile grid covers 9/16 of the CUs (W1/W3 from 512
+  // rows, QKV from 1536, O and W2 from 2560); below that the 128-row LDS pipeline wins (it splits K
+  // when its own grid is short: W2 at 256 rows 55 us against 284), with 256-row workgroups in
+  // between for W1/W3 and W2.
+  const long big_tiles = (long)((M + kBigM - 1) / kBigM) * ((N + (epi == kGemmSwiGLU ? kBigN / 2 : kBigN) - 1) /
+                                                            (epi == kGemmSwiGLU ? kBigN / 2 : kBigN));
+  if (K % 64 == 0 && big_tiles * 16 >= (long)cus * 9) {
+    stages = 6;
+    bk = 64;
+    bm = kBigM;
+    return;
+  }
   const bool big_rows = epi == kGemmSwiGLU || K >= 8192;
   stages = K % 64 == 0 ? 2 : 4;
   bk = K % 64 == 0 ? 64 : 32;
   bm = 128;
-  if (big_rows && K % 64 == 0) {
-    if (M >= 3072) {
-      stages = 1;
-    } else if (M >= (epi == kGemmSwiGLU ? 192 : 1536)) {
-      bm = 256;
-    }
-  }
+  if (big_rows && K % 64 == 0 && M >= (epi == kGemmSwiGLU ? 192 : 1536)) bm = 256;
 }
 
-// Prefill GEMM launch. The variant is chosen per shape unless forced with the process-wide
-// options: the 256 x 256 large-tile kernel for the W1/W3 + SwiGLU GEMM and for long K (W2), the
-// 128 x 128 two-stage 64-deep pipeline otherwise (QKV, O), the four-stage 32-deep one when
-// K % 64 != 0 (measured per shape at n = 3200).
+// Prefill GEMM launch. The variant is chosen per shape (gemm_choice) unless forced with the
+// process-wide options.
 template <int EPI>
 int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
   int stages, bk, bm;
-  gemm_choice(EPI, g.M, g.K, stages, bk, bm);
+  gemm_choice(EPI, g.M, g.N, g.K, ctx ? ctx->num_cus : device_cus(), stages, bk, bm);
   // one-dimensional grids of 8 * ceil(tiles / 8) workgroups (gemm_tile)
   auto tiles8 = [&](int tm, int nc) {
     const int t = ((g.M + tm - 1) / tm) * ((g.N + nc - 1) / nc);
@@ -906,6 +907,14 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
     return YHIP_OK;
   }
+  if (stages == 6 && g.K % 64 == 0) {  // 256 x 256 tiles, eight waves in two alternating groups
+    const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
+    hipLaunchKernelGGL(gemm_pp_kernel<EPI>, tiles8(kBigM, nc), dim3(512), 0, s, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
+    return YHIP_OK;
+  }
+  if (stages == 6) stages = 1;  // a 64-deep k-step needs K % 64 == 0: the 32-deep large-tile kernel
   if (stages == 1) {  // 256 x 256 tiles
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
     GemmArgs gi = g;
@@ -1555,8 +1564,8 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 0 register-staged; 1 large tile; 2..4 LDS stages;
-                                        // 5 large tiles, stream-K
-      if (value < -1 || value > 5) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 5]");
+                                        // 5 large tiles, stream-K; 6 eight-wave large tiles
+      if (value < -1 || value > 6) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 6]");
       g_gemm_auto = value < 0;
       if (value >= 0) g_gemm_stages = value;
       return YHIP_OK;
@@ -2071,14 +2080,17 @@ extern "C" int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int
   if (!stages || !bk || !bm || M <= 0 || N <= 0 || K <= 0 || mode < 0 || mode > 2)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   int s = 0, k = 0, m = 0;
-  gemm_choice(mode, M, K, s, k, m);
-  if (s != 1 && s != 5) {  // the LDS pipeline's own limits (launch_gemm)
+  gemm_choice(mode, M, N, K, device_cus(), s, k, m);
+  if (s == 6 && K % 64 != 0) s = 1;  // launch_gemm's fallback
+  const bool big = s == 1 || s == 5 || s == 6;
+  if (!big) {  // the LDS pipeline's own limits (launch_gemm)
     if (K % 64 != 0) k = 32;
     if (k != 64) m = 128;
   }
+  if (s == 6) k = 64;
   *stages = s;
   *bk = k;
-  *bm = (s == 1 || s == 5) ? kBigM : m;
+  *bm = big ? kBigM : m;
   return YHIP_OK;
 }
 

@@ -266,7 +266,8 @@ def set_gemm_ksplit(n=0):
 
 def gemm_variant(M, N, K, mode):
     """(stages, k-step, workgroup rows) of the prefill GEMM yhip_prefill runs for this shape and mode
-    under the current process-wide options (stages 1 = the 256 x 256 large-tile kernel)."""
+    under the current process-wide options (stages 6 = the eight-wave 256 x 256 kernel, 1 = the
+    four-wave one, 5 = the same with stream-K, 2..4 = the 128-row LDS pipeline's depth)."""
     out = [ctypes.c_int() for _ in range(3)]
     _check(lib().yhip_gemm_variant(M, N, K, mode, *[ctypes.byref(o) for o in out]))
     return tuple(o.value for o in out)
