@@ -250,6 +250,48 @@ def test_gemm_variants_chosen_per_shape():
     assert H.gemm_variant(3200, 6144, 4000, 0)[0] == 4  # K % 64 != 0: the 32-deep LDS pipeline
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(6400, 4096, 1024), (1024, 4096, 4096)])
+def test_gemm_eight_wave_split_round(M, N, K, mode):
+    # The eight-wave kernel's split of its last, partial round of tiles (on a 256-CU GPU):
+    # 6400 x 4096 has 400 tiles, a whole round and 144 more (more than half the CUs: one tail piece
+    # per tile, two per tail worker, main parts over 11 of 16 k-steps); 1024 x 4096 has 64 (four
+    # parts per tile side by side). Checked against a float64 product on sampled rows and columns,
+    # bit-reproducible across calls, and within fp32 rounding of the unsplit kernel.
+    H = hip()
+    rng = np.random.default_rng(M + N + K + mode)
+    n_out = N // 2 if mode == 2 else N
+    a = f16(rng.standard_normal((M, K), dtype=np.float32))
+    b = f16(rng.standard_normal((n_out, K), dtype=np.float32) * 0.02)
+    b3 = f16(rng.standard_normal((n_out, K), dtype=np.float32) * 0.02) if mode == 2 else None
+    c0 = rng.standard_normal((M, n_out), dtype=np.float32) if mode == 1 else None
+    H.set_gemm_stages(6, 64, 256)
+    try:
+        got = H.gemm(a, b, mode=mode, b3=b3, c=c0)
+        again = H.gemm(a, b, mode=mode, b3=b3, c=c0)
+        H.set_gemm_ppsplit(False)
+        whole = H.gemm(a, b, mode=mode, b3=b3, c=c0)
+    finally:
+        H.set_gemm_ppsplit(True)
+        H.set_gemm_stages(-1)
+    assert np.array_equal(got, again)
+    rows = np.unique(np.concatenate([[0, 255, 256, M - 257, M - 256, M - 1], rng.choice(M, 40, replace=False)]))
+    cols = np.unique(np.concatenate([[0, 63, 64, 255, 256, n_out - 1], rng.choice(n_out, 120, replace=False)]))
+    A = h2f(a[rows]).astype(np.float64)
+    want = A @ h2f(b[cols]).astype(np.float64).T
+    if mode == 2:
+        u = A @ h2f(b3[cols]).astype(np.float64).T
+        want = want / (1 + np.exp(-want)) * u
+        g = h2f(got[np.ix_(rows, cols)]).astype(np.float64)
+        assert npref.rel_l2(g, want) < 2e-3  # fp16 output
+        assert npref.rel_l2(h2f(got).astype(np.float64), h2f(whole).astype(np.float64)) < 1e-3
+    else:
+        if mode == 1:
+            want = want + c0[np.ix_(rows, cols)]
+        assert npref.rel_l2(got[np.ix_(rows, cols)].astype(np.float64), want) < 1e-6
+        assert npref.rel_l2(got.astype(np.float64), whole.astype(np.float64)) < 1e-6
+
+
 @pytest.mark.parametrize("variant", ["auto", "stream_k"])
 @pytest.mark.parametrize("mode,N,K", [(2, 14336, 4096), (1, 4096, 14336), (0, 6144, 4096), (1, 4096, 4096)])
 def test_gemm_production_shapes_at_3200_rows(mode, N, K, variant):

@@ -618,6 +618,11 @@ __global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
   T::epilogue(g, tm * kBigM, tn * T::NC, acc, threadIdx.x);
 }
 
+// Partial slots and flags of the split large-tile GEMMs (stream-K and the eight-wave kernel's split
+// round): a slot holds one 256 x 256 fp32 tile, flags are kSkFlagStride words apart.
+constexpr int kSkSlotFloats = kBigM * kBigN;
+constexpr int kSkFlagStride = 64;
+
 // ------------------------------------------------------------------------------------------
 // Eight-wave large-tile GEMM ("ping-pong"): 256 x 256 per workgroup as in gemm_big_kernel, but two
 // waves per SIMD. Each wave owns a 128 x 64 block of the tile (2 x 4 layout, accumulators 4 x 2
@@ -653,139 +658,254 @@ struct PPTile {
   static __device__ __forceinline__ int swz(int r) { return (r / RPW) % CPR; }
 };
 
+// The last, partial round of tiles (R tiles, fewer than the CUs) split along K so every CU has
+// work: each of those tiles has a main part over k-steps [0, kd) and np tail pieces that split
+// [kd, KI) near-evenly. Main parts run in lockstep (all at the same k-step, sharing the A and B
+// panels in L2 like whole tiles), and so do the tail pieces. A tail piece stores its fp32
+// accumulators (agent-coherent) to its partial slot and sets the slot's flag to the launch epoch;
+// the main part adds the pieces' partials in piece order (deterministic) and applies the epilogue.
+// Workgroups: dp whole tiles (XCD-contiguous), then mains main parts (R used), then tails
+// workgroups dealing the R x np pieces to nt workers.
+struct PPSplit {
+  int dp;     // whole-tile workgroups (8 * ceil(tiles / 8) without a split)
+  int mains;  // main-part workgroups (8 * ceil(R / 8)); 0: no split
+  int R;      // tiles of the split round (tiles dp .. dp + R - 1)
+  int kd;     // main parts: k-steps [0, kd)
+  int np;     // tail pieces per tile
+  int tails;  // tail workgroups (8 * ceil(nt / 8))
+  int nt;     // tail workers: worker j takes pieces j, j + nt, ...
+};
+
 template <int EPI>
-__global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g, PPSplit sp, unsigned epoch) {
   using T = PPTile<EPI>;
   constexpr int BK = T::BK;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[T::SLOTS * T::PANEL];
-  int tm, tn;
-  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + T::NC - 1) / T::NC, tm, tn)) return;
-  const int m0 = tm * kBigM, n0 = tn * T::NC;
+  const int mt = (g.M + kBigM - 1) / kBigM, ntl = (g.N + T::NC - 1) / T::NC;
+  const int KI = g.K / BK;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, wm = wave & 1, wn = wave >> 1;
-  const int nk = g.K / BK;
-
-  const uint16_t* arow[T::LPI];
-  const uint16_t* brow[T::LPI];
-#pragma unroll
-  for (int j = 0; j < T::LPI; ++j) {
-    const int r = T::RPI * (wave + 8 * j) + lane / T::CPR;
-    const int c = (lane % T::CPR) ^ T::swz(r);
-    arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * c;
-    if constexpr (EPI == kGemmSwiGLU) {
-      const int col = n0 + (r >> 6) * 32 + (r & 31);
-      const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
-      brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
-    } else {
-      brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
-    }
-  }
-  // item 2s (the A panel) or 2s + 1 (the B panel) of the ring, filled with k-step kdata
-  auto issue_item = [&](int item, int kdata) {
-    uint16_t* st = smem + (item % T::SLOTS) * T::PANEL;
-    const int k0 = kdata * BK;
-    if (item & 1) {
-#pragma unroll
-      for (int j = 0; j < T::LPI; ++j) load_lds16(brow[j] + k0, st + (wave + 8 * j) * 512);
-    } else {
-#pragma unroll
-      for (int j = 0; j < T::LPI; ++j) load_lds16(arow[j] + k0, st + (wave + 8 * j) * 512);
-    }
-  };
-  // the fragments of 32-deep half-step hs (0, 1) of k-step kt
-  u32x4 fa[2][4], fb[2][2];
-  auto read_frags = [&](int kt, int hs) {
-    const uint16_t* As = smem + ((2 * kt) % T::SLOTS) * T::PANEL;
-    const uint16_t* Bs = smem + ((2 * kt + 1) % T::SLOTS) * T::PANEL;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int c = 4 * hs + 2 * kk + (lane >> 5);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int ra = wm * 128 + t * 32 + (lane & 31);
-        fa[kk][t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ T::swz(ra)));
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int rb = wn * 64 + t * 32 + (lane & 31);
-        fb[kk][t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ T::swz(rb)));
-      }
-    }
-  };
-  auto barrier = [] {
-    __builtin_amdgcn_sched_barrier(0);
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
   f32x16 acc[4][2];
+
+  // acc = A[m0 .. m0 + 256) . B[n0 ...]^T over k-steps [k0, k1), every wave taking part; the LDS
+  // ring is free again on return
+  auto mainloop = [&](int m0, int n0, int k0, int k1) {
+    const uint16_t* arow[T::LPI];
+    const uint16_t* brow[T::LPI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < T::LPI; ++j) {
+      const int r = T::RPI * (wave + 8 * j) + lane / T::CPR;
+      const int c = (lane % T::CPR) ^ T::swz(r);
+      arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * c;
+      if constexpr (EPI == kGemmSwiGLU) {
+        const int col = n0 + (r >> 6) * 32 + (r & 31);
+        const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
+        brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
+      } else {
+        brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
+      }
+    }
+    // item 2s (the A panel) or 2s + 1 (the B panel) of the ring, filled with k-step kdata
+    auto issue_item = [&](int item, int kdata) {
+      uint16_t* st = smem + (item % T::SLOTS) * T::PANEL;
+      const int koff = kdata * BK;
+      if (item & 1) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-  auto compute = [&] {
+        for (int j = 0; j < T::LPI; ++j) load_lds16(brow[j] + koff, st + (wave + 8 * j) * 512);
+      } else {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+        for (int j = 0; j < T::LPI; ++j) load_lds16(arow[j] + koff, st + (wave + 8 * j) * 512);
+      }
+    };
+    // the fragments of 32-deep half-step hs (0, 1) of ring stage s
+    u32x4 fa[2][4], fb[2][2];
+    auto read_frags = [&](int st, int hs) {
+      const uint16_t* As = smem + ((2 * st) % T::SLOTS) * T::PANEL;
+      const uint16_t* Bs = smem + ((2 * st + 1) % T::SLOTS) * T::PANEL;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int c = 4 * hs + 2 * kk + (lane >> 5);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int ra = wm * 128 + t * 32 + (lane & 31);
+          fa[kk][t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ T::swz(ra)));
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int rb = wn * 64 + t * 32 + (lane & 31);
+          fb[kk][t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ T::swz(rb)));
+        }
+      }
+    };
+    auto barrier = [] {
+      __builtin_amdgcn_sched_barrier(0);
+      __asm__ volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto compute = [&] {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[kk][i], fb[kk][j], acc[i][j]);
+    };
+    constexpr unsigned kLgkm0 = 0xc07f;  // s_waitcnt lgkmcnt(0): the fragments are in registers
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    const int ns = k1 - k0;  // ring stage st holds k-step k0 + st
+    issue_item(0, k0);
+    issue_item(1, k0);
+    issue_item(2, k0 + min(1, ns - 1));
+    wait_vmcnt<T::LPI>();  // A_0 and B_0 have landed
+    barrier();             // stage 0 is in for every wave
+    if (grp == 1) barrier();
+    for (int st = 0; st < ns; ++st) {
+      read_frags(st, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_item(2 * st + 3, k0 + min(st + 1, ns - 1));  // B_{st+1}
+      __builtin_amdgcn_s_waitcnt(kLgkm0);
+      barrier();
+      compute();
+      barrier();
+      read_frags(st, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_item(2 * st + 4, k0 + min(st + 2, ns - 1));  // A_{st+2}
+      __builtin_amdgcn_s_waitcnt(kLgkm0);
+      if (grp == 1) wait_vmcnt<T::LPI>();  // this wave's copies of A_{st+1} and B_{st+1} have landed
+      barrier();
+      compute();
+      if (grp == 0) wait_vmcnt<T::LPI>();
+      barrier();
+    }
+    wait_vmcnt<0>();  // the copies past the end have landed before the ring is refilled
+    if (grp == 0) barrier();
+  };
+
+  // Epilogue through buffer accesses bounded to the tile's rows (rows past M fall outside the
+  // buffer, columns past N get an offset outside it: the hardware drops those accesses), so it has
+  // no per-element branches and the residual's loads go out 32 at a time ahead of their stores
+  // (per-element guarded read-modify-writes serialised into one memory round trip each: 40 us of
+  // a 3200 x 4096 tile round).
+  auto epilogue = [&](int m0, int n0) {
+    const int rows = min(kBigM, g.M - m0);
+    constexpr unsigned kOut = 0x80000000u;  // a byte offset past any tile's buffer
+    if constexpr (EPI == kGemmSwiGLU) {
+      const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+          g.H + (long)m0 * g.ldh, 0, (int)((long)rows * g.ldh * 2), kBufferConfig);
+      const int j = n0 + wn * 32 + (lane & 31);
+      const unsigned col = j < g.N ? 2u * j : kOut;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[kk][i], fb[kk][j], acc[i][j]);
-  };
-  constexpr unsigned kLgkm0 = 0xc07f;  // s_waitcnt lgkmcnt(0): the fragments are in registers
-
-  issue_item(0, 0);
-  issue_item(1, 0);
-  issue_item(2, min(1, nk - 1));
-  wait_vmcnt<T::LPI>();  // A_0 and B_0 have landed
-  barrier();             // stage 0 is in for every wave
-  if (grp == 1) barrier();
-  for (int kt = 0; kt < nk; ++kt) {
-    read_frags(kt, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_item(2 * kt + 3, min(kt + 1, nk - 1));  // B_{kt+1}
-    __builtin_amdgcn_s_waitcnt(kLgkm0);
-    barrier();
-    compute();
-    barrier();
-    read_frags(kt, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_item(2 * kt + 4, min(kt + 2, nk - 1));  // A_{kt+2}
-    __builtin_amdgcn_s_waitcnt(kLgkm0);
-    if (grp == 1) wait_vmcnt<T::LPI>();  // this wave's copies of A_{kt+1} and B_{kt+1} have landed
-    barrier();
-    compute();
-    if (grp == 0) wait_vmcnt<T::LPI>();
-    barrier();
-  }
-  wait_vmcnt<0>();
-  if (grp == 0) barrier();
-
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 128 + i * 32 + acc_row(r, lane);
-      if (m >= g.M) continue;
-      if constexpr (EPI == kGemmSwiGLU) {
-        const int j = n0 + wn * 32 + (lane & 31);
-        if (j < g.N) {
+        for (int r = 0; r < 16; ++r) {
+          const int m = wm * 128 + i * 32 + acc_row(r, lane);
           const float a1 = acc[i][0][r], a3 = acc[i][1][r];
           const float h = g.act == 1 ? silu(a1) : gelu(a1);
-          g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
+          const unsigned off = col == kOut ? kOut : (unsigned)(m * g.ldh * 2) + col;
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)(h * a3)), hr, off, 0, 0);
         }
-      } else {
+    } else {
+      const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+          g.C + (long)m0 * g.ldc, 0, (int)((long)rows * g.ldc * 4), kBufferConfig);
+      unsigned col[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-          if (n >= g.N) continue;
-          float* cp = g.C + (long)m * g.ldc + n;
-          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
-          else *cp = acc[i][j][r];
-        }
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        col[j] = n < g.N ? 4u * n : kOut;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        unsigned off[2][16];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            off[j][r] = col[j] == kOut ? kOut : (unsigned)((wm * 128 + i * 32 + acc_row(r, lane)) * g.ldc * 4) + col[j];
+        float v[2][16];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            v[j][r] = acc[i][j][r];
+            if constexpr (EPI == kGemmResid)
+              v[j][r] += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(cr, off[j][r], 0, 0));
+          }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[j][r]), cr, off[j][r], 0, 0);
       }
     }
+  };
+  // partial slot layout: 16-byte chunks, lane-contiguous (each access moves 1 KB of whole lines)
+  auto slot_byte = [&](int i, int j, int r4) { return ((((wave * 8 + 2 * i + j) * 4 + r4) * 64) + lane) * 16; };
+  auto slot_rsrc = [&](int s) {
+    return __builtin_amdgcn_make_buffer_rsrc(g.P + (long)s * kSkSlotFloats, 0, kSkSlotFloats * (int)sizeof(float),
+                                             kBufferConfig);
+  };
+
+  const int b = blockIdx.x;
+  if (b < sp.dp) {  // a whole tile
+    const int t = (b % 8) * (sp.dp / 8) + b / 8;
+    if (t >= mt * ntl) return;
+    const int m0 = (t % mt) * kBigM, n0 = (t / mt) * T::NC;
+    mainloop(m0, n0, 0, KI);
+    epilogue(m0, n0);
+    return;
+  }
+  if (b < sp.dp + sp.mains) {  // the main part of a split tile
+    const int bb = b - sp.dp, r = (bb % 8) * (sp.mains / 8) + bb / 8;
+    if (r >= sp.R) return;
+    const int t = sp.dp + r, m0 = (t % mt) * kBigM, n0 = (t / mt) * T::NC;
+    mainloop(m0, n0, 0, sp.kd);
+    for (int p = 0; p < sp.np; ++p) {
+      const int s = r * sp.np + p;
+      wait_flag(g.sk_flags + (long)s * kSkFlagStride, epoch, g.abort_flag);
+      const __amdgpu_buffer_rsrc_t sr = slot_rsrc(s);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4 v = load_shared4(sr, slot_byte(i, j, r4));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * r4 + e] += v[e];
+          }
+    }
+    epilogue(m0, n0);
+    return;
+  }
+  // tail pieces
+  const int bb = b - sp.dp - sp.mains, j0 = (bb % 8) * (sp.tails / 8) + bb / 8;
+  if (j0 >= sp.nt) return;
+  const int KT = KI - sp.kd;
+  for (int s = j0; s < sp.R * sp.np; s += sp.nt) {
+    const int r = s / sp.np, p = s % sp.np;
+    const int t = sp.dp + r, m0 = (t % mt) * kBigM, n0 = (t / mt) * T::NC;
+    mainloop(m0, n0, sp.kd + p * KT / sp.np, sp.kd + (p + 1) * KT / sp.np);
+    const __amdgpu_buffer_rsrc_t sr = slot_rsrc(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 v = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), sr, slot_byte(i, j, r4), 0, kCpolSc1);
+        }
+    publish();
+    __syncthreads();
+    if (tid == 0)
+      __hip_atomic_store(g.sk_flags + (long)s * kSkFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -803,8 +923,6 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g) {
 // error) and the tile's result is then wrong, never hung.
 // P: gridDim.x slots of 65536 floats; flags: gridDim.x words, 64 apart, below the epoch on entry.
 // ------------------------------------------------------------------------------------------
-constexpr int kSkSlotFloats = kBigM * kBigN;
-constexpr int kSkFlagStride = 64;
 
 template <int EPI, int S, int BK>
 __global__ void __launch_bounds__(256) gemm_sk_kernel(GemmArgs g, unsigned* flags, unsigned epoch,

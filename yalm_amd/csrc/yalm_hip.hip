@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <string>
@@ -37,6 +38,7 @@ bool g_attn_mfma = true;  // attention kernel of the kernel-level entry points (
 // -1 (default) = per shape: 2 for K >= 8192, else 1. Same box, 3200 rows (us): W1/W3 962 / 890 /
 // 905, W2 510 / 488 / 463.
 int g_gemm_il = -1;
+int g_gemm_ppsplit = 1;   // eight-wave prefill GEMM: split the last, partial round of tiles along K
 int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-staged kernel)
 int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
@@ -855,6 +857,46 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
 // ---- batched prefill ---------------------------------------------------------------------------
 // The prefill GEMM variant for an epilogue and shape (stages 1 = the 256 x 256 kernel, 2..4 the
 // LDS pipeline's depth, 0 the register-staged kernel), or the forced process-wide one.
+// Split of the eight-wave GEMM's last, partial round (tiles % CUs of them; the kernel's PPSplit):
+// with more of those tiles than half the CUs, one tail piece per tile, the idle CUs taking q of
+// them each and the main parts' k-range kd balancing the two (W1/W3 at 3200 rows: 176 tiles after
+// five whole rounds, 80 tail workers of up to 3 pieces, kd 48 of 64 k-steps); with fewer, S parts
+// per tile (S = CUs / tiles, at most 8, pieces of at least 8 k-steps) run side by side (QKV at
+// 3200 rows: 56 tiles, 4 parts each). A grid of fewer tiles than CUs but more than half of them
+// (W2 and O at 3200 rows: 208) is not split: filling the idle CUs slowed every main part by ~10%
+// (the GPU is at its power limit), measured neutral for W2 and 16% slower for O. No split without
+// the partial workspace, when the round is full, or when the pieces would be too small or too
+// many per worker.
+PPSplit pp_split_plan(long tiles, int KI, int P, bool workspace) {
+  PPSplit sp{};
+  sp.dp = 8 * (int)((tiles + 7) / 8);
+  const long R = tiles % P;
+  if (!g_gemm_ppsplit || !workspace || P % 8 != 0 || R == 0) return sp;
+  if (tiles < P && 2 * R > P) return sp;
+  int kd = 0, np = 0, nt = 0;
+  if (2 * R > P) {
+    nt = P - (int)R;
+    const int q = (int)((R + nt - 1) / nt);
+    kd = (q * KI + q) / (q + 1);  // ceil(q KI / (q + 1))
+    np = 1;
+    if (q > 8 || KI - kd < 2) return sp;
+  } else {
+    const int S = std::min({(int)(P / R), KI / 8, 8});
+    if (S < 2) return sp;
+    kd = KI / S;
+    np = S - 1;
+    nt = (int)R * np;
+  }
+  sp.dp = (int)(tiles - R);
+  sp.R = (int)R;
+  sp.mains = 8 * (int)((R + 7) / 8);
+  sp.kd = kd;
+  sp.np = np;
+  sp.nt = nt;
+  sp.tails = 8 * ((nt + 7) / 8);
+  return sp;
+}
+
 void gemm_choice(int epi, int M, int N, int K, int cus, int& stages, int& bk, int& bm) {
   stages = g_gemm_stages;
   bk = g_gemm_bk;
@@ -909,7 +951,11 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   }
   if (stages == 6 && g.K % 64 == 0) {  // 256 x 256 tiles, eight waves in two alternating groups
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
-    hipLaunchKernelGGL(gemm_pp_kernel<EPI>, tiles8(kBigM, nc), dim3(512), 0, s, g);
+    const int P = ctx ? ctx->num_cus : device_cus();
+    const PPSplit sp = pp_split_plan((long)((g.M + kBigM - 1) / kBigM) * ((g.N + nc - 1) / nc), g.K / 64, P,
+                                     g.P && g.sk_flags && g.abort_flag && g.p_floats >= (long)P * kSkSlotFloats);
+    const unsigned epoch = sp.mains ? ++g_sk_epoch : 0;
+    hipLaunchKernelGGL(gemm_pp_kernel<EPI>, dim3(sp.dp + sp.mains + sp.tails), dim3(512), 0, s, g, sp, epoch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
     return YHIP_OK;
@@ -1568,6 +1614,10 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       if (value < -1 || value > 6) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 6]");
       g_gemm_auto = value < 0;
       if (value >= 0) g_gemm_stages = value;
+      return YHIP_OK;
+    }
+    if (!strcmp(key, "gemm_ppsplit")) {
+      g_gemm_ppsplit = value != 0;
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_il")) {

@@ -258,6 +258,11 @@ def set_gemm_interleave(mode=-1):
     _check(lib().yhip_set_option(None, b"gemm_il", int(mode)))
 
 
+def set_gemm_ppsplit(on=True):
+    """Process-wide: the eight-wave prefill GEMM splits its last, partial round of tiles along K."""
+    _check(lib().yhip_set_option(None, b"gemm_ppsplit", int(bool(on))))
+
+
 def set_gemm_ksplit(n=0):
     """Prefill GEMM K splits on the LDS-pipeline kernel: 0 = chosen per shape (split when the output
     has too few tiles to fill the GPU), n >= 1 = forced (must divide the k-steps)."""
