@@ -27,6 +27,23 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+// Prefill attention's K rows in LDS: row i of a 32-key tile holds key key_row(i) (bits 2 and 3
+// swapped, an involution), so a lane's 8 probabilities of MFMA step kk (score rows
+// 16 kk + 8 a + 4 half + c, a in {0, 1}, c in 0..3) are keys 16 kk + 8 half + 0..7 in order: the
+// value MFMA's B fragment is one contiguous 16-byte read of a V row.
+__device__ __forceinline__ int key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// x of the partner lane in the other half-wave (lane ^ 32): v_permlane32_swap exchanges lanes 32-63
+// of its first operand with lanes 0-31 of its second, both x here. The second operand is passed
+// through an empty asm so the compiler cannot treat the two results as equal (it folded a max of
+// them to the first one).
+__device__ __forceinline__ float half_swap_other(float x) {
+  unsigned y = __builtin_bit_cast(unsigned, x);
+  __asm__ volatile("" : "+v"(y));
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), y, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float half_swap_max(float x) { return fmaxf(x, half_swap_other(x)); }
 
 // ------------------------------------------------------------------------------------------
 // GEMM C[M][N] = A[M][K] . B[N][K]^T, A and B fp16 row-major (both K-contiguous, as activations
@@ -1153,13 +1170,20 @@ __global__ void __launch_bounds__(kBlock) v_rows_kernel(const float* C, int ldc,
 // Causal GQA prefill attention on MFMA (reference src/infer.cpp:218-250 per query position:
 // scores over keys 0..pos read back from the fp16 cache, softmax with max subtraction, weighted
 // sum of V). A workgroup serves kv head g and QT consecutive 32-query tiles: wave (qs, gh) handles
-// query tile qs for query head g*G + gh. Each 32-key tile of K and V is staged once into LDS
-// (double-buffered: the next tile is loaded while the current one is used) and read by all the
-// workgroup's waves, so K/V reaches the CU once per workgroup instead of once per wave.
+// query tile qs for query head g*G + gh. Each 32-key tile of K and V is staged once into LDS (a
+// ring of four tiles) and read by all the workgroup's waves, so K/V reaches the CU once per
+// workgroup instead of once per wave.
+// Ping-pong: a wave alternates an MFMA phase (the value MFMAs of tile j - 1, then the score MFMAs
+// of tile j) with a softmax phase (tile j's online softmax, staging tile j + 2 from registers into
+// the ring, requesting tile j + 3). The waves form two groups, the second one phase behind, with a
+// workgroup barrier ending every phase, so the two waves of a SIMD (w and w + NW/2) keep the matrix
+// core and the vector ALU busy at the same time (with one barrier per tile both waves of a SIMD
+// reached the same phase together: measured 28% slower). Tile j sits in buffer j % 4: read in
+// phases 2j .. 2j + 3, written in phases 2j - 3 and 2j - 2, rewritten (tile j + 4) from phase 2j + 5.
 // Per key tile a wave computes S^T = K Q^T (keys as rows), so each lane holds 16 scores of one query
 // (its partner lane l^32 the other 16) and runs the online softmax for that query with one
 // cross-half exchange; then O^T += V^T P^T, whose B operand is exactly the lane's own
-// probabilities (the MFMA k order is chosen to match the score layout). O^T keeps the query in the
+// probabilities (the K rows are stored permuted so that they are 8 consecutive keys: key_row). O^T keeps the query in the
 // column, so the softmax rescale and the final 1/sum are lane-local. Queries are at positions
 // start + t; keys are the cache entries 0 .. position.
 // Requires HD % 32 == 0, max_seq_len % 32 == 0 and 64 * G * QT threads <= 1024.
@@ -1176,14 +1200,17 @@ struct PrefillAttnArgs {
 template <int HD, int G, int QT>
 __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnArgs a) {
   static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
-  constexpr int NT = 64 * G * QT;
+  constexpr int NT = 64 * G * QT, NW = G * QT;
+  static_assert(NW % 2 == 0, "two wave groups");
   constexpr int KS = HD / 16;   // k steps of the score MFMA
   constexpr int DT = HD / 32;   // 32-dim tiles of the output
   constexpr int KLD = HD + 8;   // LDS row of a key (halves), padded
   constexpr int VLD = 32 + 8;   // LDS row of a V dim (halves), padded
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][32 * KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][HD * VLD];
+  constexpr int NB = 4;         // key tiles in the LDS ring
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[NB][32 * KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[NB][HD * VLD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = __builtin_amdgcn_readfirstlane(wave / (NW / 2));
   const int gh = wave % G, qs = wave / G;
   // latest (longest) query tiles first, of every kv head: the dispatcher starts the workgroups in
   // order, so the long ones of all heads start in the first round and the short ones fill in
@@ -1240,7 +1267,7 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
       const int pc = tid + NT * i;
       if (pc < KPIECES) {
         const int c = pc / 64, key = (pc % 64) >> 1, hh = pc & 1;
-        *reinterpret_cast<u32x4*>(&Ks[buf][key * KLD + c * 16 + 8 * hh]) = kst[i];
+        *reinterpret_cast<u32x4*>(&Ks[buf][key_row(key) * KLD + c * 16 + 8 * hh]) = kst[i];
       }
     }
 #pragma unroll
@@ -1253,84 +1280,121 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     }
   };
 
+  auto barrier = [] {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS stores are done
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
   const int nkt = block_last / 32 + 1;
+  // the V buffer the first MFMA phase reads (as tile -1, with P = 0) holds zeros, not stale bits
+  // that could be Inf or NaN; tile NB - 1 overwrites it later
+  for (int i = tid; i < HD * VLD / 8; i += NT) reinterpret_cast<u32x4*>(Vs[NB - 1])[i] = u32x4{0u, 0u, 0u, 0u};
   gload(0);
   lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1, k0 = kt * 32;
-    if (kt + 1 < nkt) gload(k0 + 32);
-    // S^T = K Q^T; the tile's K fragments are all requested before the first MFMA
-    f32x16 s = f32x16{};
-    const uint16_t* krow = &Ks[buf][(lane & 31) * KLD + 8 * half];
-    u32x4 kf[KS];
+  if (1 < nkt) {
+    gload(32);
+    lstore(1);
+  }
+  if (2 < nkt) gload(64);
+  __syncthreads();  // tiles 0 and 1 are in
+  if (grp == 1) barrier();
+  u32x4 pf[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // P of the previous tile
+  for (int j = 0; j <= nkt; ++j) {
+    // MFMA phase: O^T += V^T P^T of tile j - 1 and S^T = K Q^T of tile j. Every fragment read is
+    // issued first (left to itself the compiler waits for each read in front of its MFMA), then
+    // the MFMAs alternate between the two products, so each score MFMA's wait on its predecessor
+    // is covered by an independent value MFMA. One shape for every iteration: at j = 0 the value
+    // MFMAs read the zeroed buffer NB - 1 with P = 0, at j = nkt the scores of a stale tile are
+    // computed and not used.
+    u32x4 vf[DT][2], kf[KS];
+    {
+      const uint16_t* vb = Vs[(j + NB - 1) % NB];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(krow + 16 * ks);
+      for (int t = 0; t < DT; ++t) {
+        // k order of step kk: keys 16 kk + 8 half + 0..7 of the tile (the permuted score rows)
+        const uint16_t* vrow = vb + (t * 32 + (lane & 31)) * VLD + 8 * half;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) vf[t][kk] = *reinterpret_cast<const u32x4*>(vrow + 16 * kk);
+      }
+      const uint16_t* krow = &Ks[j % NB][(lane & 31) * KLD + 8 * half];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(krow + 16 * ks);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    f32x16 s = f32x16{};
+    static_assert(KS == 2 * DT, "one value MFMA per score MFMA");
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(kf[ks], qf[ks], s);
-    // mask (key position > query position), scale, tile max of this query
-    float mt = kNegBig;
-    if (k0 + 31 <= a.start + q0) {  // every key of the tile precedes the wave's first query
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] *= scale;  // log2 units
-        mt = fmaxf(mt, s[r]);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + acc_row(r, lane);
-        s[r] = key <= q_pos ? s[r] * scale : kNegBig;
-        mt = fmaxf(mt, s[r]);
-      }
+    for (int i = 0; i < KS; ++i) {
+      s = mfma32(kf[i], qf[i], s);
+      o[i >> 1] = mfma32(vf[i >> 1][i & 1], pf[i & 1], o[i >> 1]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float corr = exp2_fast(m_run - m_new);
-    float ps = 0.f;
-    u32x4 pf[2];
+    barrier();
+    // softmax phase: the online softmax of tile j (O rescaled here, its P added in the next MFMA
+    // phase), then tile j + 2 into the ring and tile j + 3 requested
+    if (j < nkt) {
+      const int k0 = j * 32;
+      if (k0 + 31 > a.start + q0) {  // some key of the tile follows the wave's first query
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      half8 p8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int r = 8 * kk + e;
-        const float p = s[r] > kNegBig ? exp2_fast(s[r] - m_new) : 0.f;
-        ps += p;
-        p8[e] = (f16)p;
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + key_row(acc_row(r, lane));
+          s[r] = key <= q_pos ? s[r] : kNegBig;
+        }
       }
-      pf[kk] = __builtin_bit_cast(u32x4, p8);
-    }
-    ps += __shfl_xor(ps, 32, 64);
-    l_run = l_run * corr + ps;
-    m_run = m_new;
-    // O^T += V^T P^T; k order of step kk: keys 16 kk + {0..3, 8..11} + 4 half of the tile
-    // rescale only when some query's running maximum moved (after the first tiles it rarely does)
-    const bool rescale = __any(corr != 1.f);
-    // the tile's V fragments, all requested before the first value MFMA
-    u32x4 vf[DT][2];
+      // tile max in raw score units (the scale is positive, so the max commutes with it), a tree,
+      // combined with the other half-wave's rows of the same query
+      float mx[8];
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const uint16_t* vrow = &Vs[buf][(t * 32 + (lane & 31)) * VLD + 4 * half];
+      for (int r = 0; r < 8; ++r) mx[r] = fmaxf(s[2 * r], s[2 * r + 1]);
+#pragma unroll
+      for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int r = 0; r < w; ++r) mx[r] = fmaxf(mx[r], mx[r + w]);
+      // the running max moves only when it would grow by more than 8 in log2 units (softmax is
+      // invariant to it; p stays below 2^8, well within fp16), so O is rarely rescaled: with a
+      // plain running max, some query of the wave moved it on about half the tiles
+      const float m_cand = fmaxf(m_run, half_swap_max(mx[0]));
+      const bool grow = (m_cand - m_run) * scale > 8.f;
+      const float m_new = grow ? m_cand : m_run;
+      const float corr = exp2_fast((m_run - m_new) * scale);
+      // p = 2^(scale s - scale m): tile 0 holds key 0, which precedes every query, so m_new is
+      // finite from the first tile on and a masked score (kNegBig) underflows to p = 0 with no test
+      const float ms = m_new * scale;
+      float pv[16];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * kk);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * kk + 8);
-        vf[t][kk] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        half8 p8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * kk + e;
+          pv[r] = exp2_fast(fmaf(s[r], scale, -ms));
+          p8[e] = (f16)pv[r];
+        }
+        pf[kk] = __builtin_bit_cast(u32x4, p8);
+      }
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int r = 0; r < w; ++r) pv[r] += pv[r + w];
+      // this lane's rows only: the two half-waves' sums are added once, after the last tile
+      l_run = l_run * corr + pv[0];
+      m_run = m_new;
+      if (__any(grow)) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= corr;
       }
     }
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      if (rescale)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) o[t] = mfma32(vf[t][kk], pf[kk], o[t]);
-    }
-    if (kt + 1 < nkt) lstore(buf ^ 1);
-    __syncthreads();
+    if (j + 2 < nkt) lstore((j + 2) % NB);
+    if (j + 3 < nkt) gload(32 * (j + 3));
+    barrier();
   }
+  if (grp == 0) barrier();
+  l_run += half_swap_other(l_run);
   if (my_q < a.n) {
     const float inv = 1.0f / l_run;
     uint16_t* orow = a.out + (long)my_q * qd + h * HD;
