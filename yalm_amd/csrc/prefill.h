@@ -44,6 +44,19 @@ __device__ __forceinline__ float half_swap_other(float x) {
   return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
 }
 __device__ __forceinline__ float half_swap_max(float x) { return fmaxf(x, half_swap_other(x)); }
+// Max of 16 MFMA results in 8 v_max3_f32. Written out because fmaxf first quiets each input that
+// the compiler cannot prove canonical (an extra v_max_f32 x, x per MFMA result); scores from finite
+// fp16 operands are never signalling NaNs.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max16(const f32x16& s) {
+  const float a = max3f(s[0], s[1], s[2]), b = max3f(s[3], s[4], s[5]), c = max3f(s[6], s[7], s[8]);
+  const float d = max3f(s[9], s[10], s[11]), e = max3f(s[12], s[13], s[14]);
+  return max3f(max3f(a, b, c), max3f(d, e, s[15]), s[15]);
+}
 
 // ------------------------------------------------------------------------------------------
 // GEMM C[M][N] = A[M][K] . B[N][K]^T, A and B fp16 row-major (both K-contiguous, as activations
@@ -1346,17 +1359,10 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
       }
       // tile max in raw score units (the scale is positive, so the max commutes with it), a tree,
       // combined with the other half-wave's rows of the same query
-      float mx[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) mx[r] = fmaxf(s[2 * r], s[2 * r + 1]);
-#pragma unroll
-      for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-        for (int r = 0; r < w; ++r) mx[r] = fmaxf(mx[r], mx[r + w]);
       // the running max moves only when it would grow by more than 8 in log2 units (softmax is
       // invariant to it; p stays below 2^8, well within fp16), so O is rarely rescaled: with a
       // plain running max, some query of the wave moved it on about half the tiles
-      const float m_cand = fmaxf(m_run, half_swap_max(mx[0]));
+      const float m_cand = fmaxf(m_run, half_swap_max(max16(s)));
       const bool grow = (m_cand - m_run) * scale > 8.f;
       const float m_new = grow ? m_cand : m_run;
       const float corr = exp2_fast((m_run - m_new) * scale);
