@@ -1117,42 +1117,48 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
   }
   __syncthreads();
   const float* c = C + (long)t * ldc;
-  const int pairs = (q_dim + kv_dim) / 2;  // q and k; v goes through v_rows_kernel
-  const int hp = head_dim / 2;             // pairs per head: aligned groups of hp lanes (hp <= 64)
+  // a lane takes 4 consecutive values (two rotary pairs): 16-byte loads, 8-byte stores (the 4 dims
+  // lie in one 16-dim chunk of the K layout); a head is an aligned group of head_dim / 4 lanes
+  // (a power of two, head_dim in {32, 64, 128}), and q_dim, kv_dim are multiples of 32
+  const int quads = (q_dim + kv_dim) / 4;  // q and k; v goes through v_rows_kernel
+  const int hq = head_dim / 4;
   // every thread runs the same number of iterations, so the head-wide maximum below can use
-  // cross-lane shuffles; heads are whole groups of lanes, and a group is all live or all dead
-  for (int p0 = 0; p0 < pairs; p0 += kBlock) {
+  // cross-lane shuffles; a head's group of lanes is all live or all dead
+  for (int p0 = 0; p0 < quads; p0 += kBlock) {
     const int p = p0 + threadIdx.x;
-    const bool live = p < pairs;
-    const int i = 2 * p;
-    float v0 = 0.f, v1 = 0.f;
+    const bool live = p < quads;
+    const int i = 4 * p;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (live) {
-      v0 = clipf(c[i], qkv_clip);
-      v1 = clipf(c[i + 1], qkv_clip);
+      v = *reinterpret_cast<const f32x4*>(c + i);
       const int j = i % head_dim;
-      const float cs = rope[j], sn = rope[j + 1];
-      const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
-      v0 = r0;
-      v1 = r1;
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const float v0 = clipf(v[e], qkv_clip), v1 = clipf(v[e + 1], qkv_clip);
+        const float cs = rope[j + e], sn = rope[j + e + 1];
+        v[e] = v0 * cs - v1 * sn;
+        v[e + 1] = v0 * sn + v1 * cs;
+      }
     }
-    float amax = fmaxf(fabsf(v0), fabsf(v1));
-    for (int o = 1; o < hp; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    for (int o = 1; o < hq; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     if (!live) continue;
     if (i < q_dim) {
       const int qe = q_range_exp(amax);
       const float qmul = __builtin_ldexpf(1.0f, qe);
-      v0 *= qmul;
-      v1 *= qmul;
-      if (p % hp == 0) qscale[(long)t * (q_dim / head_dim) + i / head_dim] = __builtin_ldexpf(1.0f, -qe);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] *= qmul;
+      if (p % hq == 0) qscale[(long)t * (q_dim / head_dim) + i / head_dim] = __builtin_ldexpf(1.0f, -qe);
     }
-    const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0), h1 = __builtin_bit_cast(uint16_t, (f16)v1);
-    const uint32_t h01 = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    unsigned long long h = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h |= (unsigned long long)__builtin_bit_cast(uint16_t, (f16)v[e]) << (16 * e);
     if (i < q_dim) {
-      *reinterpret_cast<uint32_t*>(Q + (long)t * q_dim + i) = h01;  // i even: one 4-byte store
-    } else {  // k: dims j, j+1 (j even) are adjacent in a 16-dim chunk of the K layout
+      *reinterpret_cast<unsigned long long*>(Q + (long)t * q_dim + i) = h;
+    } else {  // k: dims j .. j+3 (j % 4 == 0) are adjacent in a 16-dim chunk of the K layout
       const int ik = i - q_dim;
       const int g = ik / head_dim, j = ik % head_dim;
-      *reinterpret_cast<uint32_t*>(kcache + (long)g * head_dim * msl + k_cache_idx(j, pos, msl)) = h01;
+      *reinterpret_cast<unsigned long long*>(kcache + (long)g * head_dim * msl + k_cache_idx(j, pos, msl)) = h;
     }
   }
 }
@@ -1196,9 +1202,9 @@ __global__ void __launch_bounds__(kBlock) v_rows_kernel(const float* C, int ldc,
 // Per key tile a wave computes S^T = K Q^T (keys as rows), so each lane holds 16 scores of one query
 // (its partner lane l^32 the other 16) and runs the online softmax for that query with one
 // cross-half exchange; then O^T += V^T P^T, whose B operand is exactly the lane's own
-// probabilities (the K rows are stored permuted so that they are 8 consecutive keys: key_row). O^T keeps the query in the
-// column, so the softmax rescale and the final 1/sum are lane-local. Queries are at positions
-// start + t; keys are the cache entries 0 .. position.
+// probabilities (the K rows are stored permuted so that they are 8 consecutive keys: key_row).
+// O^T keeps the query in the column, so the softmax rescale and the final 1/sum are lane-local.
+// Queries are at positions start + t; keys are the cache entries 0 .. position.
 // Requires HD % 32 == 0, max_seq_len % 32 == 0 and 64 * G * QT threads <= 1024.
 // ------------------------------------------------------------------------------------------
 struct PrefillAttnArgs {
