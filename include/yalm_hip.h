@@ -128,7 +128,10 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
  * GEMM variant: stages -1 = chosen per shape (default), 0 = register-staged kernel, 1 = 256 x 256
- * large tiles, 2..4 = LDS pipeline stages; k-step 32 or 64; workgroup rows 128 or 256),
+ * large tiles (four waves), 2..4 = LDS pipeline stages, 5 = the large tiles with stream-K, 6 = the
+ * eight-wave 256 x 256 kernel; k-step 32 or 64; workgroup rows 128 or 256), "gemm_ppsplit" (1 =
+ * default: the eight-wave kernel splits its last, partial round of tiles along K where that pays;
+ * 0 = whole tiles only), "gemm_il" (four-wave large tiles: k-step schedule, -1 = per shape),
  * "upload_stage_mb" (yhip_upload_layer / yhip_upload_globals copy tensors of 64 KB and more through
  * a ring of three pinned staging chunks of this many MB, default 64; 0 = direct copies from the
  * caller's pageable memory as the reference's upload_cuda, src/infer.cu:34-39) and
