@@ -1165,23 +1165,37 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
 
 // The v columns of the QKV GEMM output into the V cache (clip, fp16 RNE; reference
 // src/infer.cpp:284-305): V[g][d][pos] is position-contiguous, so a workgroup transposes a tile of
-// 64 positions x 64 value dims through LDS and writes 128 contiguous bytes per dim instead of one
-// 2-byte store per (position, dim).
+// 64 positions x 64 value dims through LDS: 16-byte loads of 4 dims of a row, and, when the tile's
+// first position is a multiple of 8 and the tile is full, 16-byte stores of 8 positions of a dim
+// (otherwise 2-byte stores). kv_dim % 4 == 0.
 __global__ void __launch_bounds__(kBlock) v_rows_kernel(const float* C, int ldc, int q_dim, int kv_dim, int n,
                                                         float qkv_clip, int start, int msl, uint16_t* vcache) {
-  __shared__ uint16_t tile[64][64 + 2];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][64 + 8];  // [dim][position]
   const int p0 = blockIdx.x * 64, d0 = blockIdx.y * 64;  // positions (rows of C), value dims
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += kBlock / 64) {  // read: a row's 64 dims, coalesced
-    const int t = p0 + r, d = d0 + tx;
-    float v = 0.f;
-    if (t < n && d < kv_dim) v = clipf(C[(long)t * ldc + q_dim + kv_dim + d], qkv_clip);
-    tile[tx][r] = __builtin_bit_cast(uint16_t, (f16)v);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // read: 16 lanes cover a row's 64 dims
+    const int r = (tid >> 4) + 16 * k, d = d0 + 4 * (tid & 15), t = p0 + r;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (t < n && d < kv_dim) v = *reinterpret_cast<const f32x4*>(C + (long)t * ldc + q_dim + kv_dim + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[4 * (tid & 15) + e][r] = __builtin_bit_cast(uint16_t, (f16)clipf(v[e], qkv_clip));
   }
   __syncthreads();
-  for (int r = ty; r < 64; r += kBlock / 64) {  // write: a dim's 64 positions, coalesced
-    const int d = d0 + r, t = p0 + tx;
-    if (t < n && d < kv_dim) vcache[(long)d * msl + start + t] = tile[r][tx];
+  if ((start + p0) % 8 == 0 && p0 + 64 <= n) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // write: 8 lanes cover a dim's 64 positions
+      const int r = (tid >> 3) + 32 * k, w = tid & 7, d = d0 + r;
+      if (d < kv_dim)
+        *reinterpret_cast<u32x4*>(vcache + (long)d * msl + start + p0 + 8 * w) =
+            *reinterpret_cast<const u32x4*>(&tile[r][8 * w]);
+    }
+  } else {
+    const int tx = tid & 63, ty = tid >> 6;
+    for (int r = ty; r < 64; r += kBlock / 64) {  // write: a dim's 64 positions, coalesced
+      const int d = d0 + r, t = p0 + tx;
+      if (t < n && d < kv_dim) vcache[(long)d * msl + start + t] = tile[r][tx];
+    }
   }
 }
 
