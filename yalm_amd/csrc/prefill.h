@@ -1098,6 +1098,23 @@ __global__ void __launch_bounds__(kBlock) rmsnorm_rows_kernel(const float* X, co
   for (int i = threadIdx.x; i < dim; i += kBlock) o[i] = __builtin_bit_cast(uint16_t, (f16)(x[i] * inv * gain[i]));
 }
 
+// Max over an aligned group of n lanes (n in {8, 16, 32}) by DPP moves inside the vector ALU (quad
+// permutes for xor 1 and 2, then the 8- and 16-lane mirrors, each pairing the two halves of the
+// previous group), plus one cross-row shuffle for 32; __shfl_xor took an LDS round trip per step.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+  return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf,
+                                                                        false)));
+}
+__device__ __forceinline__ float group_max(float x, int n) {
+  x = dpp_max<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+  x = dpp_max<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+  x = dpp_max<0x141>(x);  // row_half_mirror
+  if (n >= 16) x = dpp_max<0x140>(x);  // row_mirror
+  if (n >= 32) x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return x;
+}
+
 // Row t of the QKV GEMM output (position start + t): clip, RoPE on q and k pairs
 // (reference src/infer.cpp:197-215, 284-305), q as fp16 into Q, k as fp16 into the cache at the
 // row's position (no ring: start + n <= max_seq_len). The v columns go to v_rows_kernel.
@@ -1140,8 +1157,7 @@ __global__ void __launch_bounds__(kBlock) qkv_rows_kernel(const float* C, int ld
         v[e + 1] = v0 * sn + v1 * cs;
       }
     }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    for (int o = 1; o < hq; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float amax = group_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))), hq);
     if (!live) continue;
     if (i < q_dim) {
       const int qe = q_range_exp(amax);
