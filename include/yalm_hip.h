@@ -123,7 +123,12 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * their rows of Wo . attention in per-row integer words, bit-reproducibly; 0 = separate launches),
  * "split_o" (1 = default: beyond that, the split-KV attention stores every slice's partial and the
  * O launch merges them, with at most 32 slices per kv head; 0 = the attention launch merges its
- * own slices). The results of every option setting agree to fp32 rounding; each is tested against
+ * own slices), "qao" (1 = QKV, attention and O in one launch for the steps attn_o would run, with
+ * at most "qao_max" cached tokens (default 700), at head_dim 128, 4 query heads per kv head, 8 kv
+ * heads and dim 4096, where a probe launch at yhip_create found the round-robin workgroup-to-XCD
+ * order the launch relies on; 2 = the same, and the call fails when that launch is unavailable;
+ * 0 = off, the default, measured slower), "qao_wo_after" (that launch's Wo loads go out after
+ * this many of its workgroup barriers, 0..5, default 2). The results of every option setting agree to fp32 rounding; each is tested against
  * the CPU reference. With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill

@@ -25,10 +25,12 @@ def hip():
 # The ways a step can run: one launch per token (a dataflow of workgroups), the captured hipGraph
 # of per-op kernels (the default: attention and O share a launch up to 700 keys, beyond that the
 # attention's slice merge moves into the O launch), the same kernels launched directly, the graph
-# with the SIMT attention, and the graph with attention (merge included) and O in separate launches.
+# with the SIMT attention, the graph with attention (merge included) and O in separate launches, and
+# the graph with QKV, attention and O in one launch where the shape allows it (opt-in).
 PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
          "direct": dict(single_launch=0, graph=0), "graph_simt": dict(single_launch=0, graph=1, attn_mfma=0),
-         "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0)}
+         "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0),
+         "graph_qao": dict(single_launch=0, graph=1, qao=1)}
 
 
 def use_path(m, path):
@@ -75,7 +77,7 @@ def test_embedding_gather_bit_exact(path):
             assert np.array_equal(x, h2f(t["model.embed.weight"][tok]))
 
 
-@pytest.mark.parametrize("path", ["single", "graph", "direct"])
+@pytest.mark.parametrize("path", ["single", "graph", "direct", "graph_qao"])
 @pytest.mark.parametrize("shape", ["tiny", "mistral"])
 def test_embedding_gather_bit_exact_through_layer0(path, shape):
     # The production gather: layer 0's QKV matvec stages the fp16 embedding row and writes it to
@@ -177,7 +179,7 @@ def test_teacher_forced_logits_and_kv(cfg_name, path):
     hm.close()
 
 
-@pytest.mark.parametrize("path", ["single", "graph", "graph_sep"])
+@pytest.mark.parametrize("path", ["single", "graph", "graph_sep", "graph_qao"])
 def test_mistral_shape_two_layers(path):
     # The Mistral-7B layer shape (dim 4096, hidden 14336, 32/8 heads of 128) with two layers: the
     # instantiations the full model runs, checked teacher-forced against the oracle.
@@ -369,6 +371,7 @@ def test_attention_and_o_in_one_launch_matches_oracle(path, shape):
     cfg = ATTN_O_SHAPES[shape]
     t = np_tensors(cfg, seed=57, std=0.02)
     om, hm = _models(cfg, t, path)
+    hm.set_option("qao", 0)  # the attention + O launch itself (the QKV + attention + O one is tested below)
     hm.set_option("attn_o", 1)
     hm.set_option("attn_o_max", 600)
     rng = np.random.default_rng(58)
@@ -443,6 +446,7 @@ def test_attention_and_o_in_one_launch_is_bit_reproducible():
     runs = []
     for ao in (1, 1, 0):
         with hip().HipModel(cfg, t) as m:
+            m.set_option("qao", 0)
             m.set_option("attn_o", ao)
             rng = np.random.default_rng(60)
             out = [m.forward(int(tok), pos, 1) for pos, tok in enumerate(rng.integers(0, cfg["vocab_size"], 24))]
@@ -452,6 +456,64 @@ def test_attention_and_o_in_one_launch_is_bit_reproducible():
     for (ka, va), (kb, vb) in zip(kva, kvb):
         assert np.array_equal(ka, kb) and np.array_equal(va, vb)
     assert npref.rel_l2(la, ls) < 1e-5
+
+
+@pytest.mark.parametrize("path", ["graph", "direct"])
+def test_qkv_attention_and_o_in_one_launch_matches_oracle(path):
+    # QKV, attention and O in one launch at the Mistral shape: the workgroups of a kv head run on one
+    # XCD and hand q and this position's K/V to each other through its L2, then each repeats the kv
+    # head's attention over four waves before combining its Wo rows. Positions with one to six
+    # 32-key tiles per wave, the first (embedding residual) and second layer, against the oracle on
+    # a cache pre-filled from the host; qao = 2 fails unless this GPU's placement allows the launch.
+    cfg = ATTN_O_SHAPES["mistral"]
+    t = np_tensors(cfg, seed=71, std=0.02)
+    om, hm = _models(cfg, t, path)
+    hm.set_option("qao", 2)
+    rng = np.random.default_rng(72)
+    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
+    for layer in range(cfg["n_layers"]):
+        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
+        om.set_kv(layer, k, v)
+        hm.set_kv(layer, k, v)
+    tok = 5
+    for pos in (0, 1, 2, 31, 32, 33, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 640, 699):
+        mode = 0 if pos in (1, 128) else 1
+        lo = om.forward(tok, pos, mode)
+        lh = hm.forward(tok, pos, mode)
+        if mode == 1:
+            assert npref.rel_l2(lh, lo) < 1e-4, pos
+        tok = O.argmax(lo) if mode == 1 else tok + 1
+    # the written entries within fp16 rounding of the oracle's (on a pre-filled cache a near-zero
+    # entry may round to zero on one side only, so no zero-pattern check here)
+    for layer in range(cfg["n_layers"]):
+        for a, b in zip(hm.kv(layer), om.kv(layer)):
+            fa, fb = h2f(a), h2f(b)
+            assert np.max(np.abs(fa - fb)) <= 2e-3 * np.max(np.abs(fb))
+            assert npref.rel_l2(fa, fb) < 1e-3
+    hm.close()
+
+
+def test_qkv_attention_and_o_in_one_launch_is_bit_reproducible():
+    # The one-launch step twice (bit for bit: the row words make x independent of arrival order),
+    # against the attention + O launch after a separate QKV launch (fp32 noise, growing along the
+    # 40 positions through fp16 cache roundings: the RMSNorm sum and the attention's merge run over
+    # eight waves in a different order).
+    cfg = ATTN_O_SHAPES["mistral"]
+    t = np_tensors(cfg, seed=73, std=0.02)
+    runs = []
+    for qao in (2, 2, 0):
+        with hip().HipModel(cfg, t) as m:
+            m.set_option("qao", qao)
+            rng = np.random.default_rng(74)
+            toks = rng.integers(0, cfg["vocab_size"], 40)
+            out = [m.forward(int(tok), pos, 1) for pos, tok in enumerate(toks)]
+            runs.append((np.stack(out), [m.kv(layer) for layer in range(cfg["n_layers"])]))
+    (la, kva), (lb, kvb), (ls, kvs) = runs
+    assert np.array_equal(la, lb)
+    for (ka, va), (kb, vb) in zip(kva, kvb):
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    assert npref.rel_l2(la, ls) < 1e-4
 
 
 def test_slice_merge_in_the_o_launch_is_bit_reproducible():

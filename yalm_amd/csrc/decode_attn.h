@@ -88,14 +88,16 @@ struct AttnMfmaSmem {
 // K/V tile and its q loads are issued (at once in a wave without a tile): loads it issues are
 // younger than those, and loads retire in issue order, so waiting for the tile and q does not wait
 // for them.
-template <int HD, int G, int NW, bool COH, int NB, class Issue>
+// LCPOL (with COH false): cache policy of the q and K/V loads, kCpolSc0 when q and this position's
+// K/V were written earlier in the same launch by workgroups on the same XCD (served by its L2).
+template <int HD, int G, int NW, bool COH, int NB, int LCPOL = 0, class Issue>
 __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_begin, int t_end,
                                                 AttnMfmaSmem<HD, G, NW>& sm, Issue issue) {
   static_assert(HD % 32 == 0 && G >= 1 && G <= 8, "head_dim % 32, 1..8 query heads per kv head");
   static_assert(NB == 1 || NB == 2, "tile buffers per wave");
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int TS = 32;  // keys per wave tile
-  constexpr int CPOL = COH ? kCpolSc1 : 0;
+  constexpr int CPOL = COH ? kCpolSc1 : LCPOL;
   auto& om = sm.om;
   auto& oml = sm.oml;
 
@@ -141,6 +143,15 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
         for (int ks = 0; ks < KS; ++ks) {
           q4[ks][0] = load_shared4(qr, qoff + 128 * ks);
           q4[ks][1] = load_shared4(qr, qoff + 128 * ks + 16);
+        }
+      } else if constexpr (LCPOL != 0) {
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.q + (long)g * G * HD), 0, G * HD * (int)sizeof(float), kBufferConfig);
+        const int qoff = (h * HD + 8 * grp) * (int)sizeof(float);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          q4[ks][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, qoff + 128 * ks, 0, LCPOL));
+          q4[ks][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, qoff + 128 * ks + 16, 0, LCPOL));
         }
       } else {
 #pragma unroll
@@ -427,6 +438,10 @@ struct AttnOArgs {
   float* x;                  // [dim], x += Wo . attn
   unsigned long long* rowacc;  // [dim] combining words, zero between launches
   int dim, q_dim;
+  // when not null: the residual stream is row params->token of this fp16 embedding table instead of
+  // x (the first layer of the QKV + attention + O launch, which writes x only once, at the end)
+  const uint16_t* emb = nullptr;
+  const StepParams* params = nullptr;
 };
 
 constexpr int kRowAccCountShift = 60;
@@ -491,7 +506,7 @@ __device__ __forceinline__ void attn_o_rows(const AttnOArgs& o, const float* ao,
   }
   const int row = row0 + lane;
   if (lane < RW && row < o.dim) {
-    const float xr = o.x[row];
+    const float xr = o.emb ? (float)__builtin_bit_cast(f16, o.emb[(long)o.params->token * o.dim + row]) : o.x[row];
     const unsigned long long term = rowacc_term(mine);
     const unsigned long long old =
         __hip_atomic_fetch_add(o.rowacc + row, term, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -623,5 +638,228 @@ __global__ void __launch_bounds__(64 * NW) merge_o_kernel(AttnArgs a, AttnOArgs 
   }
   __syncthreads();
   attn_o_rows<HD, G, NW, U>(o, ao, rs, wv, row0, lane, wave, a.n_kv_heads);
+}
+}  // namespace yk
+
+namespace yk {
+// ------------------------------------------------------------------------------------------
+// QKV, attention and the O projection in one launch (short contexts, no sink rotation),
+// reference src/infer.cpp:279-344, for shapes with one kv head per XCD (n_kv_heads == 8): the
+// dispatcher deals a launch's workgroups to the 8 XCDs round-robin, workgroup b to XCD (s + b) % 8
+// for a start s that depends on earlier launches.
+//
+// Workgroup b takes kv head g = b % nkv and row block rb = b / nkv, so all of kv head g's
+// workgroups run on one XCD and what they hand to each other stays in that XCD's L2. Twelve waves in
+// two roles:
+//   - waves 8..11 issue their 32 Wo row segments (kv head g's columns of rows rb*128 + 32(w-8) ..)
+//     early and hold them in registers; they take part in the workgroup barriers until the
+//     attention output is in LDS, then multiply and combine the rows as attn_o_kernel does;
+//   - waves 0..7 stage x (RMSNorm, reference src/infer.cpp:136-146; the embedding row in the
+//     first layer) and stream rb's share of kv head g's rows of [Wq;Wk;Wv] (G*HD q rows, HD k and
+//     HD v rows, as row pairs: up to two per wave, the second issued once x is staged) with the
+//     matvec's QKV epilogue
+//     (clip, RoPE, q and this position's fp16 K/V). A workgroup whose rows are stored counts itself
+//     on kv head g's counter; once all of kv head g's workgroups have (bounded wait), waves 0..7 run
+//     the whole-context MFMA attention of kv head g, reading q and the caches through the XCD's L2
+//     (sc0 loads), and put the normalised output into LDS.
+// The roles keep each wave's loads in one stream: loads return in issue order, so attention loads
+// queued behind Wo loads would wait for the Wo block, and a wave that stored rows could not wait
+// for its stores without also waiting for Wo loads issued before them.
+// Each workgroup counts itself as 2^(6 x) on its kv head's 64-bit counter (x: the XCD it runs on,
+// from the XCC_ID register) and waits for exactly 2^(6 x) times the head's workgroup count, so a
+// head whose workgroups are not all on the waiting workgroup's XCD never completes the wait: it
+// times out and the host reports an error for the step instead of reading another L2's data. The
+// host enables the launch only after a probe launch of the same grid found the round-robin order,
+// and only when the grid fits the GPU at one workgroup per CU (every workgroup of a kv head must be
+// resident while the others wait for it).
+// ------------------------------------------------------------------------------------------
+constexpr int kQaoRowWaves = 8, kQaoWoWaves = 4, kQaoWoLoads = 32, kQaoPairsPerWave = 2, kQaoXcds = 8;
+
+struct QaoArgs {
+  // kv head g: 64-bit count of its workgroups whose rows are stored, 2^(6 XCD) each, at
+  // done[g * kQkvDoneStride] (zeroed every step)
+  unsigned* done;
+  unsigned* abort_flag;  // a wait timed out
+  int blocks_per_head;   // workgroups per kv head (Wo row blocks), below 64
+  int wo_after;          // the Wo waves issue their loads after this many of the workgroup's barriers (0..5)
+};
+
+// Thread 0 polls until the 64-bit word *c equals target (bounded, as wait_count); the workgroup
+// waits at the barrier.
+__device__ __forceinline__ void wait_word(const unsigned long long* c, unsigned long long target, unsigned* abort_flag) {
+  if (threadIdx.x == 0) {
+    unsigned spins = 0;
+    while (__hip_atomic_load(const_cast<unsigned long long*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target) {
+      __builtin_amdgcn_s_sleep(1);
+      if ((++spins & 255u) == 0 &&
+          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xfu;
+}
+
+// LDS writes of this wave complete, then the workgroup barrier (no wait for global accesses).
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+template <int HD, int G>
+__global__ void __launch_bounds__(64 * (kQaoRowWaves + kQaoWoWaves)) qao_kernel(MatvecArgs m, AttnArgs a, AttnOArgs o,
+                                                                                 QaoArgs z) {
+  constexpr int NR = kQaoRowWaves, NT = 64 * NR, KC = 8, K = 512 * KC, NPT = K / (4 * NT);  // K 4096: 2 float4 per row thread
+  constexpr int QP = G * HD / 2, KP = HD / 2, NP = QP + 2 * KP;                          // row pairs of one kv head
+  using Geo = AttnOGeom<HD, G, kQaoWoWaves, kQaoWoLoads>;
+  static_assert(NPT * 4 * NT == K, "x staging: whole float4 per row thread");
+  __shared__ AttnMfmaSmem<HD, G, NR> sm;
+  __shared__ __attribute__((aligned(16))) float xs[K + HD];  // normalised x, then the step's RoPE table
+  __shared__ __attribute__((aligned(16))) float ao[G * HD];
+  __shared__ float red[NR];
+  __shared__ float rs[kQaoWoWaves][Geo::RW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkv = a.n_kv_heads;
+  const int g = (int)blockIdx.x % nkv, rb = (int)blockIdx.x / nkv;
+
+  if (wave >= NR) {  // Wo waves
+    const int ww = wave - NR;
+    const int row0 = rb * Geo::RB + ww * Geo::RW;
+    u32x4 wv[kQaoWoLoads];
+    // the row waves' six barriers (staging sums, staged input, rows stored, kv head's rows
+    // complete, attention outputs, normalised output); the Wo loads go out after wo_after of them
+    // (the row waves' first loads then meet fewer bytes ahead of them) and stay in flight
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      if (k == z.wo_after) attn_o_issue<HD, G, kQaoWoWaves, kQaoWoLoads>(o, g, row0, lane, wv);
+      __builtin_amdgcn_s_barrier();
+    }
+    __asm__ volatile("" ::: "memory");
+    attn_o_rows<HD, G, kQaoWoWaves, kQaoWoLoads>(o, ao, rs, wv, row0, lane, ww, nkv);
+    return;
+  }
+
+  // row waves: the staging reads first, then the first two row pairs' weight loads
+  const int pos = m.params->pos;
+  const uint16_t* x16 = m.emb ? m.emb + (long)m.params->token * K : nullptr;
+  f32x4 xv[NPT], gv[NPT];
+  unsigned long long hv[NPT];
+  if (x16) {
+    const unsigned long long* h4 = reinterpret_cast<const unsigned long long*>(x16);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) hv[k] = h4[tid + NT * k];
+  } else {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(m.x);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) xv[k] = x4[tid + NT * k];
+  }
+  const f32x4* g4 = reinterpret_cast<const f32x4*>(m.gain);
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) gv[k] = g4[tid + NT * k];
+  const float rc = tid < HD ? m.rope_cs[tid] : 0.f;
+
+  const int ppb = (NP + z.blocks_per_head - 1) / z.blocks_per_head;
+  auto pair_of = [&](int k, bool& valid) {  // this workgroup's k-th row pair of kv head g, as a [Wq;Wk;Wv] pair
+    const int j = rb * ppb + k;
+    valid = k < ppb && j < NP;
+    if (!valid) return 0;
+    if (j < QP) return g * QP + j;
+    if (j < QP + KP) return m.q_dim / 2 + g * KP + (j - QP);
+    return (m.q_dim + m.kv_dim) / 2 + g * KP + (j - QP - KP);
+  };
+  bool v0, v1;
+  const int p0 = pair_of(wave, v0), p1 = pair_of(wave + NR, v1);
+  u32x4 wa[2][KC], wb[2][KC];
+  auto issue = [&](u32x4 (&wv)[2][KC], int p, bool valid) {
+    const uint16_t* rows[2];
+    group_rows<2>(m, p, rows);
+    load_group_uniform<KC, 2>(wv, rows, lane, valid);
+  };
+  issue(wa, p0, v0);
+
+  // RMSNorm into LDS
+  if (x16) {
+#pragma unroll
+    for (int k = 0; k < NPT; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[k][e] = (float)__builtin_bit_cast(f16, (uint16_t)(hv[k] >> (16 * e)));
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPT; ++k)
+    ss += xv[k][0] * xv[k][0] + xv[k][1] * xv[k][1] + xv[k][2] * xv[k][2] + xv[k][3] * xv[k][3];
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  lds_barrier();  // 1
+  ss = 0.f;
+#pragma unroll
+  for (int w = 0; w < NR; ++w) ss += red[w];
+  const float inv = 1.0f / sqrtf(ss / (float)K + m.eps);
+  f32x4* o4 = reinterpret_cast<f32x4*>(xs);
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    f32x4 v;
+    v[0] = xv[k][0] * inv * gv[k][0];
+    v[1] = xv[k][1] * inv * gv[k][1];
+    v[2] = xv[k][2] * inv * gv[k][2];
+    v[3] = xv[k][3] * inv * gv[k][3];
+    o4[tid + NT * k] = v;
+  }
+  if (tid < HD) xs[K + tid] = rc;
+  lds_barrier();  // 2
+  issue(wb, p1, v1);  // the second pair after the staging: its reads then queue behind fewer bytes
+
+  const float none[2] = {0.f, 0.f};
+  auto use = [&](const u32x4 (&wv)[2][KC], int p, bool valid) {
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < KC; ++u) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) acc[r] = dot8(wv[r][u], xs + 8 * (lane + kWave * u), acc[r]);
+      if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[r] = wave_sum(acc[r]);
+    epilogue<2, kEpiQkvRope, false>(m, p, acc, none, pos, xs + K, valid && lane == 0);
+  };
+  use(wa, p0, v0);
+  use(wb, p1, v1);
+  publish();  // this thread's q / K / V stores are in the L2
+  __builtin_amdgcn_s_barrier();  // 3
+  __asm__ volatile("" ::: "memory");
+  unsigned long long* done = reinterpret_cast<unsigned long long*>(z.done + (long)g * kQkvDoneStride);
+  const unsigned long long mine = 1ull << (6 * xcc_id());
+  if (tid == 0) __hip_atomic_fetch_add(done, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_word(done, mine * (unsigned)z.blocks_per_head, z.abort_flag);  // 4: every row of kv head g is stored
+
+  attn_mfma_waves<HD, G, NR, false, 1, kCpolSc0>(a, g, 0, pos + 1, sm, [] {});  // 5 (its closing barrier)
+  for (int e = tid; e < G * HD; e += NT) {
+    const int h = e / HD, d = e % HD;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < NR; ++w) M = fmaxf(M, sm.oml[w][h][0]);
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NR; ++w) {
+      const float wt = exp2_fast(sm.oml[w][h][0] - M);
+      O = fmaf(sm.om[w][h][d], wt, O);
+      L = fmaf(sm.oml[w][h][1], wt, L);
+    }
+    ao[e] = O / L;
+  }
+  lds_barrier();  // 6
+}
+
+// Workgroup b records the XCD it runs on (the round-robin order qao_kernel relies on).
+__global__ void __launch_bounds__(512) xcc_probe_kernel(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 }  // namespace yk

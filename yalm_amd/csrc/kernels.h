@@ -187,6 +187,7 @@ __device__ __forceinline__ void wait_flag(const unsigned* f, unsigned value, uns
 
 constexpr int kBufferConfig = 0x00020000;  // raw buffer descriptor word 3 on gfx9-family GPUs
 constexpr int kCpolSc1 = 16;               // cache-policy operand: sc1, the agent-scope coherent load
+constexpr int kCpolSc0 = 1;                // cache-policy operand: sc0, served by the XCD's L2 (not the CU's L1)
 
 // 16 bytes that another workgroup of the same launch wrote with store_shared: one dwordx4 load
 // with the agent-coherence bit (the access load_shared makes per float).

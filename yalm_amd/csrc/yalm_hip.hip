@@ -69,7 +69,10 @@ __global__ void set_params_kernel(StepParams* p, int token, int pos, const float
     p->pos = pos;
     *argmax_key = 0ull;
   }
-  for (int i = threadIdx.x; i < n_layers * kQkvDoneParts; i += blockDim.x) qkv_done[kQkvDoneStride * i] = 0u;
+  for (int i = threadIdx.x; i < n_layers * kQkvDoneParts; i += blockDim.x) {  // 32- or 64-bit counters
+    qkv_done[kQkvDoneStride * i] = 0u;
+    qkv_done[kQkvDoneStride * i + 1] = 0u;
+  }
   fill_rope_table(inv_freq, rope_cs, half, pos);
 }
 
@@ -128,8 +131,17 @@ struct yhip_ctx {
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   unsigned* pf_sink = nullptr;
   // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepQkvAttn,
-  // kStepAttnO, kStepSplitO]
-  hipGraphExec_t graph[3][4] = {};
+  // kStepAttnO, kStepSplitO, kStepQao]
+  hipGraphExec_t graph[3][5] = {};
+  // QKV, attention and O in one launch (qao_kernel) where attn_o applies and the shape has one kv
+  // head per XCD (opt-in: measured slower than the QKV launch followed by attn_o, see the design
+  // notes); qao_ok: a probe launch found the dispatcher's workgroup-to-XCD order it needs
+  bool qao = false;
+  bool qao_ok = false;
+  std::string qao_note;  // why not, when qao_ok is false
+  int qao_max = 700;     // most cached tokens of a step that runs it
+  int qao_wo_after = 2;  // barriers of its workgroups before the Wo loads go out
+
   // attention and the O projection in one launch (attn_o_kernel) for contexts up to attn_o_max
   // tokens: 108-119 us less per token than the separate launches up to 350 keys, 60 at 500, 17 at
   // 700, slower from ~800 on (Mistral-7B shape on MI355X)
@@ -496,14 +508,71 @@ int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStrea
   return YHIP_OK;
 }
 
+// ---- QKV + attention + O projection in one launch ----------------------------------------------
+// The shape qao_kernel is built for: head_dim 128, 4 query heads per kv head, 8 kv heads (one per
+// XCD), dim = q_dim = 4096 (32 Wo row blocks of 128 rows per kv head, 12 row pairs of [Wq;Wk;Wv]
+// per workgroup), and a grid of one workgroup per CU at most.
+constexpr int kQaoRowsPerBlock = AttnOGeom<128, 4, kQaoWoWaves, kQaoWoLoads>::RB;
+bool qao_shape(const yhip_config& c, int num_cus) {
+  const int G = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
+  if (c.head_dim != 128 || G != 4 || c.n_kv_heads != kQaoXcds || c.dim != 4096 || c.n_heads * c.head_dim != 4096)
+    return false;
+  const int bph = c.dim / kQaoRowsPerBlock;
+  const int pairs = (G + 2) * c.head_dim / 2;
+  return (pairs + bph - 1) / bph <= kQaoPairsPerWave * kQaoRowWaves && bph < 64 && c.n_kv_heads * bph <= num_cus;
+}
+
+// The probe launch: workgroup b of qao_kernel's grid must run on XCD (s + b) % 8 for one s.
+// Returns an empty string when it does, else what was found.
+std::string qao_probe(yhip_ctx* ctx) {
+  const int grid = ctx->c.n_kv_heads * (ctx->c.dim / kQaoRowsPerBlock);
+  unsigned* d = nullptr;
+  std::vector<unsigned> h(grid, 0xffffffffu);
+  (void)hipGetLastError();  // an earlier call's error is not this launch's
+  if (hipMalloc(&d, grid * sizeof(unsigned)) != hipSuccess) return "probe: out of device memory";
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(grid), dim3(512), 0, ctx->stream, d);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(h.data(), d, grid * sizeof(unsigned), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(d);
+  if (e != hipSuccess) return std::string("probe launch: ") + hipGetErrorString(e);
+  for (int b = 0; b < grid; ++b)
+    if (h[b] != (h[0] + b) % kQaoXcds)
+      return "probe: workgroup 0 ran on XCD " + std::to_string(h[0]) + ", workgroup " + std::to_string(b) + " on " +
+             std::to_string(h[b]);
+  return "";
+}
+
+// The step at pos runs QKV, attention and O in one launch where attn_o would run and the shape and
+// the probed placement allow it.
+bool qao_at(const yhip_ctx* ctx, int pos) {
+  return ctx->qao && ctx->qao_ok && attn_o_at(ctx, pos) && pos + 1 <= ctx->qao_max && qao_shape(ctx->c, ctx->num_cus);
+}
+
+int launch_qao(yhip_ctx* ctx, const MatvecArgs& m, const AttnArgs& t, const AttnOArgs& o, int layer, hipStream_t s) {
+  const yhip_config& c = ctx->c;
+  QaoArgs z;
+  z.done = ctx->qkv_done + (size_t)layer * kQkvDoneParts * kQkvDoneStride;
+  z.abort_flag = ctx->step_abort;
+  z.blocks_per_head = c.dim / kQaoRowsPerBlock;
+  z.wo_after = ctx->qao_wo_after;
+  hipLaunchKernelGGL((qao_kernel<128, 4>), dim3(c.n_kv_heads * z.blocks_per_head),
+                     dim3(64 * (kQaoRowWaves + kQaoWoWaves)), 0, s, m, t, o, z);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("QKV + attention + O launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
 // variant: kStepSeparate (every kernel its own launch), kStepQkvAttn (the attention runs inside
 // the QKV launch, fused_attention_at), kStepAttnO (attention and O in one launch, attn_o_at) or
 // kStepSplitO (split-KV attention, then slice merge and O in one launch, split_o_at).
-enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3 };
+// kStepQao: QKV, attention and O in one launch (qao_at).
+enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3, kStepQao = 4 };
 int step_variant(const yhip_ctx* ctx, int pos) {
   if (fused_attention_at(ctx, pos)) return kStepQkvAttn;  // opt-in, so it takes precedence
+  if (qao_at(ctx, pos)) return kStepQao;
   if (attn_o_at(ctx, pos)) return kStepAttnO;
   return split_o_at(ctx, pos) ? kStepSplitO : kStepSeparate;
 }
@@ -556,7 +625,22 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
     t.min_slice = attn_min_slice_for(ctx, attn_uses_mfma(ctx));
     t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
-    if (fused) {
+    if (variant == kStepQao) {
+      // 1 + 2 + 3 in one launch; in the first layer the residual stream is read from the embedding
+      // row by the workgroups that complete x's rows, and nothing writes x before them
+      AttnOArgs o;
+      o.wo = L.wo;
+      o.x = ctx->x;
+      o.rowacc = ctx->rowacc;
+      o.dim = c.dim;
+      o.q_dim = qd;
+      if (l == 0) {
+        a.emb_out = nullptr;
+        o.emb = ctx->embed;
+        o.params = ctx->params;
+      }
+      if ((rc = launch_qao(ctx, a, t, o, l, s))) return rc;
+    } else if (fused) {
       a.coh_store = 1;
       if ((rc = launch_qkv_attn(ctx, a, t, ctx->qkv_done + (size_t)l * kQkvDoneParts * kQkvDoneStride, s))) return rc;
     } else {
@@ -592,7 +676,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
     }
     if (variant == kStepSeparate && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
-    if (variant != kStepAttnO && variant != kStepSplitO) {
+    if (variant != kStepAttnO && variant != kStepSplitO && variant != kStepQao) {
     a = mv_base();
     a.w0 = L.wo;
     a.row_step = 2L * qd;
@@ -660,7 +744,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     HIP_TRY(ctx, hipGetLastError());
   }
-  if (fused)  // the fused launches' wait time-out flag, checked after the caller's synchronisation
+  if (fused || variant == kStepQao)  // the wait time-out / placement flag, checked after the caller's synchronisation
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (mode == 1) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
@@ -774,13 +858,14 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   return YHIP_OK;
 }
 
-// After a synchronised step: a wait of a fused QKV + attention launch that timed out poisons it.
+// After a synchronised step: a wait of a fused launch that timed out poisons it (in the QKV +
+// attention + O launch also the sign of a kv head whose workgroups were not all on one XCD).
 int check_step_abort(yhip_ctx* ctx) {
   if (ctx->argmax_host[4] == 0) return YHIP_OK;
   ctx->argmax_host[4] = 0;
   hipMemsetAsync(ctx->step_abort, 0, sizeof(unsigned), ctx->stream);
   hipStreamSynchronize(ctx->stream);
-  return fail(ctx, YHIP_EDEVICE, "fused QKV + attention: a dependency wait timed out");
+  return fail(ctx, YHIP_EDEVICE, "fused QKV + attention launch: a dependency wait timed out");
 }
 
 // After a synchronised single-launch step: a wait that timed out poisons the step.
@@ -1246,6 +1331,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->attn_splits = std::max(1, std::min(64, 3 * ctx->num_cus / (4 * std::max(1, c.n_kv_heads))));
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "stream create failed"));
+  ctx->qao_note = qao_shape(c, ctx->num_cus) ? qao_probe(ctx) : std::string("shape");
+  ctx->qao_ok = ctx->qao_note.empty();
 
   // Weights: one allocation, 256-byte aligned sub-buffers.
   const size_t dim = c.dim, hid = c.hidden_dim, qd = ctx->q_dim(), kvd = ctx->kv_dim(), V = c.vocab_size;
@@ -1684,6 +1771,16 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "attn_o_max")) {
     if (value < 0) return fail(ctx, YHIP_EINVAL, "attn_o_max must be >= 0");
     ctx->attn_o_max = value;
+  } else if (!strcmp(key, "qao")) {
+    if (value == 2 && !ctx->qao_ok)
+      return fail(ctx, YHIP_EINVAL, "qao: no QKV + attention + O launch for this context (" + ctx->qao_note + ")");
+    ctx->qao = value != 0;
+  } else if (!strcmp(key, "qao_wo_after")) {
+    if (value < 0 || value > 5) return fail(ctx, YHIP_EINVAL, "qao_wo_after must be in [0, 5]");
+    ctx->qao_wo_after = value;
+  } else if (!strcmp(key, "qao_max")) {
+    if (value < 0) return fail(ctx, YHIP_EINVAL, "qao_max must be >= 0");
+    ctx->qao_max = value;
   } else if (!strcmp(key, "fuse_attn")) {
     ctx->fuse_attn = value != 0;
   } else if (!strcmp(key, "fuse_attn_max")) {
