@@ -534,9 +534,9 @@ def test_slice_merge_in_the_o_launch_is_bit_reproducible():
 @pytest.mark.parametrize("path", ["graph", "direct"])
 def test_mfma_attention_slice_rule_across_lengths(path):
     # The MFMA attention picks its KV slice length from the context length (one slice up to 320
-    # keys, then 64/128, 256 and 384-key slices); positions on both sides of each boundary, with
-    # a KV cache pre-filled from the host, against the oracle.
-    cfg = dict(MICRO, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, max_seq_len=4608)
+    # keys, then 64-, 128- and 384-key slices); positions on both sides of each boundary, with a KV
+    # cache pre-filled from the host, against the oracle.
+    cfg = dict(MICRO, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, max_seq_len=5248)
     t = np_tensors(cfg, seed=44, std=0.1)
     om, hm = _models(cfg, t, path)
     rng = np.random.default_rng(45)
@@ -547,7 +547,7 @@ def test_mfma_attention_slice_rule_across_lengths(path):
         om.set_kv(layer, k, v)
         hm.set_kv(layer, k, v)
     tok = 3
-    for pos in (318, 320, 321, 700, 1023, 1536, 1537, 4095, 4096, 4500):
+    for pos in (318, 320, 321, 700, 1023, 1024, 1536, 1537, 2400, 4095, 4096, 4500, 5119, 5120, 5121):
         lo = om.forward(tok, pos)
         lh = hm.forward(tok, pos)
         assert npref.rel_l2(lh, lo) < 1e-4, pos

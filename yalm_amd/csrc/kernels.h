@@ -957,17 +957,19 @@ __host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int m
 }
 
 // Slice length of the MFMA decode attention: min_slice > 0 is a fixed floor; 0 picks it by context
-// length, from a sweep on MI355X (Mistral shape, 24 slices per kv head; µs per layer):
-//   - up to 320 keys one slice per kv head, no cross-workgroup merge (300 keys: 7.8 against 9.7
-//     with two 256-key slices);
-//   - up to 1536 keys slices of 64 (128 from 1024 keys on): the merge of many short slices costs
-//     less than two or three long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1);
-//   - up to 4096 keys 256 (2048: 10.5 against 11.0 with 128), beyond that 384 (6000: 13.8
-//     against 14.8); from ~8K keys the slice count (nsplit) decides and the floor does not matter.
+// length, from sweeps on MI355X (Mistral shape, 24 slices per kv head):
+//   - up to 320 keys one slice per kv head, no cross-workgroup merge (300 keys: 7.8 against 9.7 µs
+//     per layer with two 256-key slices);
+//   - up to 1024 keys slices of 64: the merge of many short slices costs less than two or three
+//     long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1);
+//   - up to 5120 keys slices of 128 (the slice merge runs in the O launch there: µs per decode
+//     step against 256-key slices, 1600 keys 2683 / 2735, 2400: 2704 / 2748, 3216: 2766 / 2775;
+//     against 384-key slices at 4500: 2797 / 2818), beyond that 384 (6000: equal, 8000: 2853
+//     against 2865 with 128); from ~8K keys the slice count (nsplit) decides.
 __host__ __device__ __forceinline__ int attn_mfma_chunk(int kv_len, int nsplit, int min_slice) {
   if (min_slice > 0) return attn_chunk(kv_len, nsplit, min_slice, 32);
   if (kv_len <= 320) return (kv_len + 31) / 32 * 32;
-  return attn_chunk(kv_len, nsplit, kv_len <= 1536 ? 64 : (kv_len <= 4096 ? 256 : 384), 32);
+  return attn_chunk(kv_len, nsplit, kv_len <= 1024 ? 64 : (kv_len <= 5120 ? 128 : 384), 32);
 }
 
 // Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the
