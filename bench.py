@@ -324,6 +324,19 @@ def main():
     w13_gbs = W13_BYTES / (us * 1e-6) / 1e9
     log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {w13_gbs:.0f} GB/s")
 
+    # what the step's launch structure allows: the same weight bytes through memory-only launches
+    # of the same sizes and order (matvec access pattern), and through one launch
+    ms_seq, ms_one = hip.bench_stream(cfg, reps=5)
+    weights = WEIGHT_BYTES
+    ceiling = {"ms_per_token": round(ms_seq, 4), "tok_s": round(1e3 / ms_seq, 1),
+               "GBps": round(weights / (ms_seq * 1e-3) / 1e9, 1),
+               "one_launch_ms": round(ms_one, 4), "one_launch_tok_s": round(1e3 / ms_one, 1),
+               "value_frac": round(tok_s / (1e3 / ms_seq), 4),
+               "note": "memory-only streaming launches with the decode step's weight bytes per launch "
+                       "(129 launches) and as one launch"}
+    log(f"[bench] launch-structure ceiling: {ms_seq:.3f} ms/token ({1e3 / ms_seq:.0f} tok/s), one launch "
+        f"{ms_one:.3f} ms ({1e3 / ms_one:.0f} tok/s); decode at {100 * ceiling['value_frac']:.1f}% of the first")
+
     extra = {}
     if extras:
         extra["long"] = run_long(hip, host, ctxp, cfg)
@@ -384,6 +397,7 @@ def main():
         "roofline": roofline,
         "w13_kernel": w13,
         "device_us_per_step": round(step_us, 2),
+        "launch_ceiling": ceiling,
         "cpu_baseline": cpu,
         **extra,
     }

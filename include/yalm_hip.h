@@ -215,6 +215,13 @@ int yhip_test_argmax(const float* logits, int n, int* out);
 int yhip_bench_kernel(int kind, int rows, int cols, int copies, int warmup, int reps, int blocks_per_cu,
                       float* us_per_launch);
 
+/* Memory-only ceiling of one decode step at this config: its weight bytes read by pure streaming
+ * launches in the order and sizes of the decode launches (per layer [Wq;Wk;Wv], Wo, W1 and W3,
+ * W2; then the lm_head; every launch over fresh memory, the matvecs' access pattern), and the
+ * same bytes as one launch. Writes milliseconds per token for both. Needs device memory for one
+ * copy of the weights. No reference counterpart (a measurement hook). */
+int yhip_bench_stream(const yhip_config* cfg, int reps, float* ms_launches, float* ms_one_launch);
+
 /* Times one prefill GEMM launch (mode as yhip_test_gemm) on device-filled operands: average
  * microseconds over `reps` launches after `warmup`, with HIP events on a private stream. No
  * reference counterpart (the reference has no batched prefill). */

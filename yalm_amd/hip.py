@@ -26,7 +26,7 @@ EXPORTS = (
     "yhip_forward_argmax", "yhip_prefill", "yhip_logits_host", "yhip_kv_read", "yhip_kv_write", "yhip_set_option",
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
-    "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc", "yhip_kv_fill_normal",
+    "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc", "yhip_kv_fill_normal", "yhip_bench_stream",
 )
 
 
@@ -87,6 +87,7 @@ def lib():
         "yhip_bench_kernel": (ctypes.c_int, [ctypes.c_int] * 7 + [_f32p]),
         "yhip_bench_attention": (ctypes.c_int, [ctypes.c_int] * 10 + [_f32p]),
         "yhip_bench_gemm": (ctypes.c_int, [ctypes.c_int] * 6 + [_f32p]),
+        "yhip_bench_stream": (ctypes.c_int, [ctypes.POINTER(HipConfig), ctypes.c_int, _f32p, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -283,6 +284,15 @@ def set_upload(stage_mb=64, threads=8):
     the host threads that fill a chunk."""
     _check(lib().yhip_set_option(None, b"upload_stage_mb", int(stage_mb)))
     _check(lib().yhip_set_option(None, b"upload_threads", int(threads)))
+
+
+def bench_stream(cfg, reps=10):
+    """Memory-only ceiling of one decode step: (ms per token through the step's launch sequence,
+    ms per token as one launch)."""
+    a, b = ctypes.c_float(), ctypes.c_float()
+    c = make_config(cfg)
+    _check(lib().yhip_bench_stream(ctypes.byref(c), reps, ctypes.byref(a), ctypes.byref(b)))
+    return a.value, b.value
 
 
 def bench_gemm(M, N, K, mode, warmup=3, reps=20):
