@@ -201,6 +201,44 @@ def test_mistral_shape_two_layers(path):
     hm.close()
 
 
+def test_full_depth_mistral_7b_shape_greedy_and_logits_match_oracle():
+    # The whole Mistral-7B-shaped model (32 layers, 14.5 GB of fp16 weights from the host library's
+    # seeded generator) through the drop-in path: the reference completion loop on the HIP device
+    # (16 prompt ids hydrated, then 32 greedy tokens, device argmax) against the oracle on the same
+    # host weights -- the greedy contract at full depth (reference src/main.cpp:169-193) -- and the
+    # teacher-forced logits of the last prompt position and the first generated ones within rel-L2
+    # 2e-3 (contract 1e-2; observed 6e-4: 32 layers of fp16 cache roundings where the two sides'
+    # fp32 sums differ in order).
+    from yalm_amd import host
+    with host.Session.synthetic(dict(host.MISTRAL_7B), context=4096) as sess:
+        cfg = sess.config()
+        sess.hip(0)
+        prompt = [int(v) for v in host.uniform_ids(16, 81, cfg["vocab_size"])]
+        toks, _, _ = sess.generate(prompt, 32, temperature=0.0, device_argmax=True)
+        om = O.OracleModel(dict(cfg), sess.tensors())
+        lo = None
+        for i, tok in enumerate(prompt):
+            lo = om.forward(tok, i, 1 if i == len(prompt) - 1 else 0)
+        ref, logits_o = [], [lo]
+        for k in range(32):
+            nxt = O.argmax(lo)
+            ref.append(nxt)
+            lo = om.forward(nxt, len(prompt) + k)
+            if k < 4:
+                logits_o.append(lo)
+        om.close()
+        assert [int(t) for t in toks] == ref
+        # teacher-forced on the device: the same tokens rewrite the same cache entries
+        seq = prompt + ref
+        worst = 0.0
+        for i in range(len(prompt) + 4):
+            mode = 1 if i >= len(prompt) - 1 else 0
+            lh = sess.forward(seq[i], i, mode)
+            if mode == 1:
+                worst = max(worst, npref.rel_l2(lh, logits_o[i - len(prompt) + 1]))
+        assert worst < 2e-3, worst
+
+
 @pytest.mark.parametrize("path", ["single", "graph"])
 def test_greedy_sequence_matches_32_tokens(path):
     cfg = dict(TINY)
