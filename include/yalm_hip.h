@@ -128,7 +128,12 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * heads and dim 4096, where a probe launch at yhip_create found the round-robin workgroup-to-XCD
  * order the launch relies on; 2 = the same, and the call fails when that launch is unavailable;
  * 0 = off, the default, measured slower), "qao_wo_after" (that launch's Wo loads go out after
- * this many of its workgroup barriers, 0..5, default 2). The results of every option setting agree to fp32 rounding; each is tested against
+ * this many of its workgroup barriers, 0..5, default 2), "slice_o" (1 = beyond "attn_o_max" cached
+ * tokens, below max_seq_len, with 8 kv heads on that probed order and head_dim * query heads per
+ * kv head at most 512: the O launch's own workgroups take the split-KV slices, one each, and merge
+ * them through the XCD's L2; 2 = the same, and the call fails when that launch is unavailable;
+ * 0 = off, the default, measured no faster than the attention launch followed by the merge + O
+ * launch). The results of every option setting agree to fp32 rounding; each is tested against
  * the CPU reference. With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
  * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
  * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill

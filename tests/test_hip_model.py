@@ -455,6 +455,7 @@ def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
     cfg = SPLIT_O_SHAPES[shape]
     t = np_tensors(cfg, seed=61, std=0.02)
     om, hm = _models(cfg, t, path)
+    hm.set_option("slice_o", 0)  # the merge + O launch itself (the one-launch slices are tested below)
     rng = np.random.default_rng(62)
     n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
     for layer in range(cfg["n_layers"]):
@@ -562,11 +563,66 @@ def test_slice_merge_in_the_o_launch_is_bit_reproducible():
     outs = []
     for so in (1, 1, 0):
         with hip().HipModel(cfg, t) as m:
+            m.set_option("slice_o", 0)
             m.set_option("split_o", so)
             m.kv_fill_normal(3000, 64)
             outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
     assert np.array_equal(outs[0], outs[1])
     assert npref.rel_l2(outs[0], outs[2]) < 1e-5
+
+
+SLICE_O_SHAPES = {
+    "mistral": SPLIT_O_SHAPES["mistral"],
+    "hd64_g4_kv8": dict(TINY, dim=2048, head_dim=64, n_heads=32, n_kv_heads=8, rotary_dim=64, n_layers=2,
+                        max_seq_len=2048),
+}
+
+
+@pytest.mark.parametrize("path", ["graph", "direct"])
+@pytest.mark.parametrize("shape", list(SLICE_O_SHAPES))
+def test_attention_slices_and_o_in_one_launch_matches_oracle(path, shape):
+    # Beyond 700 keys with one kv head per XCD, the O launch's own workgroups take the split-KV
+    # slices (one per workgroup of the kv head), hand the partials to each other through the
+    # XCD's L2 and merge them before the Wo rows: positions from one 32-key slice per workgroup to
+    # the end of the context, then past it (sink mode falls back to the separate attention launch
+    # and the merge + O launch), against the oracle on a cache pre-filled from the host. slice_o = 2
+    # fails unless the launch is available on this GPU.
+    cfg = SLICE_O_SHAPES[shape]
+    t = np_tensors(cfg, seed=75, std=0.02)
+    om, hm = _models(cfg, t, path)
+    hm.set_option("slice_o", 2)
+    rng = np.random.default_rng(76)
+    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
+    for layer in range(cfg["n_layers"]):
+        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
+        om.set_kv(layer, k, v)
+        hm.set_kv(layer, k, v)
+    msl = cfg["max_seq_len"]
+    tok = 3
+    for pos in (700, 701, 1023, 1024, 1025, 2047, 3216, 4000, msl - 2, msl - 1, msl, msl + 1):
+        if pos > msl + 1:
+            continue
+        lo = om.forward(tok, pos)
+        lh = hm.forward(tok, pos)
+        assert npref.rel_l2(lh, lo) < 1e-4, pos
+        tok = O.argmax(lo)
+    hm.close()
+
+
+def test_attention_slices_and_o_in_one_launch_is_bit_reproducible():
+    # Twice bit for bit (the partials are merged in slice order and the rows meet in integer
+    # words), and within fp32 noise of the separate split-KV attention launch + merge + O launch.
+    cfg = SPLIT_O_SHAPES["mistral"]
+    t = np_tensors(cfg, seed=77, std=0.02)
+    outs = []
+    for so in (2, 2, 0):
+        with hip().HipModel(cfg, t) as m:
+            m.set_option("slice_o", so)
+            m.kv_fill_normal(3000, 64)
+            outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
+    assert np.array_equal(outs[0], outs[1])
+    assert npref.rel_l2(outs[0], outs[2]) < 1e-4
 
 
 @pytest.mark.parametrize("path", ["graph", "direct"])

@@ -863,3 +863,127 @@ __global__ void __launch_bounds__(512) xcc_probe_kernel(unsigned* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 }  // namespace yk
+
+namespace yk {
+// ------------------------------------------------------------------------------------------
+// Split-KV attention, slice merge and the O projection in one launch (contexts beyond attn_o's,
+// no sink rotation; reference src/infer.cpp:218-250, 327-344), for shapes with one kv head per
+// XCD (n_kv_heads == 8, the dispatcher's round-robin order as qao_kernel relies on it).
+//
+// Workgroup b takes kv head g = b % nkv and Wo row block rb = b / nkv, as attn_o_kernel; the
+// workgroups also take one KV slice each (keys [rb c, rb c + c), c = kv_len / NS rounded up to
+// the 32-key tile, NS = the head's workgroup count; the last ones may hold no keys). All of kv
+// head g's workgroups run on one XCD, so what they hand to each other meets in its L2. A slice
+// workgroup (one whose slice holds keys) issues its first K/V tile and q, then its Wo block, runs
+// the MFMA attention over its slice and stores the slice's (o, m, l) (m in natural units, as the
+// split-KV partials) with plain stores, then counts itself on kv head g's counter with
+// qao_kernel's XCD-weighted term (2^(6 x); the wait is for exactly the slice count times the own
+// term, so a head split across XCDs times out and the host reports an error). Every workgroup reads
+// the head's NS partials with sc0 loads into LDS, merges them (out_h = sum_s w_s o_s /
+// sum_s w_s l_s, w_s = exp(m_s - max m)) and multiplies and combines its Wo rows as
+// attn_o_kernel. The wait for a slice's partial stores also waits for the wave's Wo loads issued
+// before them (loads and stores retire in issue order); by then the Wo stream has mostly landed.
+// ------------------------------------------------------------------------------------------
+constexpr int kSliceOMaxSlices = 32;  // KV slices per kv head (the partial block in LDS holds this many)
+
+struct SliceOArgs {
+  unsigned* done;        // kv head g: 64-bit XCD-weighted count at done[g * kQkvDoneStride] (zeroed every step)
+  unsigned* abort_flag;  // a wait timed out
+  int slices;            // KV slices per kv head: the head's workgroup count, at most kSliceOMaxSlices
+};
+
+template <int HD, int G, int NW, int U>
+__global__ void __launch_bounds__(64 * NW) slice_o_kernel(AttnArgs a, AttnOArgs o, SliceOArgs z) {
+  using Geo = AttnOGeom<HD, G, NW, U>;
+  constexpr int RW = Geo::RW, NT = 64 * NW, NSMAX = kSliceOMaxSlices, ST = HD + 2;
+  constexpr int PB = G * NSMAX * ST, PPT = (PB / 4 + NT - 1) / NT;  // partial block floats, float4 per thread
+  static_assert(ST % 2 == 0 && NSMAX <= 64, "partial rows");
+  __shared__ AttnMfmaSmem<HD, G, NW> sm;
+  __shared__ __attribute__((aligned(16))) float pb[PB];
+  __shared__ float wts[G][NSMAX];
+  __shared__ float linv[G];
+  __shared__ __attribute__((aligned(16))) float ao[G * HD];
+  __shared__ float rs[NW][RW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkv = a.n_kv_heads;
+  const int g = (int)blockIdx.x % nkv, rb = (int)blockIdx.x / nkv;
+  const int row0 = rb * Geo::RB + wave * RW;
+  const int kv_len = min(a.params->pos + 1, a.msl);  // the host runs this kernel only for pos < msl
+  const int ns = z.slices;
+  const int chunk = ((kv_len + ns - 1) / ns + 31) / 32 * 32;
+  const int active = (kv_len + chunk - 1) / chunk;  // slices holding keys (at most ns)
+  float* part = a.partial + (long)g * G * a.nsplit * ST;  // rows (h nsplit + s) of ST floats
+  unsigned long long* done = reinterpret_cast<unsigned long long*>(z.done + (long)g * kQkvDoneStride);
+  const unsigned long long mine = 1ull << (6 * xcc_id());
+
+  u32x4 wv[U];
+  if (rb < active) {
+    const int t_begin = rb * chunk, t_end = min(kv_len, t_begin + chunk);
+    attn_mfma_waves<HD, G, NW, false, 1>(a, g, t_begin, t_end, sm,
+                                         [&] { attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv); });
+    // this slice's partial: the waves' (m, l, o) combined
+    for (int e = tid; e < G * HD; e += NT) {
+      const int h = e / HD, d = e % HD;
+      float M = kNegBig;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.oml[w][h][0]);
+      float O = 0.f, L = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float wt = exp2_fast(sm.oml[w][h][0] - M);
+        O = fmaf(sm.om[w][h][d], wt, O);
+        L = fmaf(sm.oml[w][h][1], wt, L);
+      }
+      float* dst = part + (long)(h * a.nsplit + rb) * ST;
+      dst[d] = O;
+      if (d == 0) {
+        dst[HD] = M * kLn2;  // natural units, as the split-KV partials
+        dst[HD + 1] = L;
+      }
+    }
+    publish();  // this thread's partial stores are in the L2 (and its Wo loads have landed)
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(done, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv);
+  }
+  wait_word(done, mine * (unsigned)active, z.abort_flag);  // every slice of kv head g is stored
+
+  // kv head g's partial block (rows h nsplit + s, s < active), read through the L2 into LDS:
+  // every load issued before the first use
+  const int nfl = G * a.nsplit * ST;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(part, 0, nfl * (int)sizeof(float), kBufferConfig);
+  f32x4 pv[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int f = 4 * (tid + NT * k);  // float index in the block; chunks wholly in slices >= active are not read
+    const bool want = f < nfl && ((f / ST) % a.nsplit < active || ((f + 3) / ST) % a.nsplit < active);
+    pv[k] = want ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, 4 * f, 0, kCpolSc0))
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int k = 0; k < PPT; ++k)
+    if (4 * (tid + NT * k) < nfl) *reinterpret_cast<f32x4*>(pb + 4 * (tid + NT * k)) = pv[k];
+  __syncthreads();
+  // per head (one wave each): the slices' weights relative to the largest maximum, 1 / sum_s w_s l_s
+  for (int i = tid; i < G * 64; i += NT) {
+    const int h = i / 64, s = i % 64;
+    const float* row = pb + (h * a.nsplit + s) * ST;
+    const float m = s < active ? row[HD] : kNegBig;
+    const float M = wave_max(m);
+    const float w = s < active ? expf(m - M) : 0.f;
+    const float L = wave_sum(s < active ? w * row[HD + 1] : 0.f);
+    if (s < NSMAX) wts[h][s] = w;
+    if (s == 0) linv[h] = 1.0f / L;
+  }
+  __syncthreads();
+  for (int e = tid; e < G * HD; e += NT) {
+    const int h = e / HD, d = e % HD;
+    float O = 0.f;
+    for (int s = 0; s < active; ++s) O = fmaf(wts[h][s], pb[(h * a.nsplit + s) * ST + d], O);
+    ao[e] = O * linv[h];
+  }
+  __syncthreads();
+  attn_o_rows<HD, G, NW, U>(o, ao, rs, wv, row0, lane, wave, nkv);
+}
+}  // namespace yk

@@ -131,8 +131,15 @@ struct yhip_ctx {
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   unsigned* pf_sink = nullptr;
   // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepQkvAttn,
-  // kStepAttnO, kStepSplitO, kStepQao]
-  hipGraphExec_t graph[3][5] = {};
+  // kStepAttnO, kStepSplitO, kStepQao, kStepSliceO]
+  hipGraphExec_t graph[3][6] = {};
+  // xcd_rr: a probe launch found workgroup b of a launch on XCD (s + b) % 8 for b < kXcdProbeGrid
+  // (checked when there are 8 kv heads: then every kv head's workgroups of attn_o's grid share one)
+  bool xcd_rr = false;
+  // split-KV attention, slice merge and O in one launch (slice_o_kernel) beyond attn_o_max where
+  // the kv heads' workgroups share an XCD
+  // (opt-in: measured no faster than the split-KV attention launch followed by merge_o)
+  bool slice_o = false;
   // QKV, attention and O in one launch (qao_kernel) where attn_o applies and the shape has one kv
   // head per XCD (opt-in: measured slower than the QKV launch followed by attn_o, see the design
   // notes); qao_ok: a probe launch found the dispatcher's workgroup-to-XCD order it needs
@@ -522,10 +529,12 @@ bool qao_shape(const yhip_config& c, int num_cus) {
   return (pairs + bph - 1) / bph <= kQaoPairsPerWave * kQaoRowWaves && bph < 64 && c.n_kv_heads * bph <= num_cus;
 }
 
-// The probe launch: workgroup b of qao_kernel's grid must run on XCD (s + b) % 8 for one s.
-// Returns an empty string when it does, else what was found.
-std::string qao_probe(yhip_ctx* ctx) {
-  const int grid = ctx->c.n_kv_heads * (ctx->c.dim / kQaoRowsPerBlock);
+// The probe launch: workgroup b of a launch must run on XCD (s + b) % 8 for one s, for every b below
+// kXcdProbeGrid (the launches that rely on it have at most that many workgroups). Returns an empty
+// string when it does, else what was found.
+constexpr int kXcdProbeGrid = 1024;
+std::string xcd_probe(yhip_ctx* ctx) {
+  const int grid = kXcdProbeGrid;
   unsigned* d = nullptr;
   std::vector<unsigned> h(grid, 0xffffffffu);
   (void)hipGetLastError();  // an earlier call's error is not this launch's
@@ -563,17 +572,76 @@ int launch_qao(yhip_ctx* ctx, const MatvecArgs& m, const AttnArgs& t, const Attn
   return YHIP_OK;
 }
 
+// ---- split-KV attention + slice merge + O projection in one launch ----------------------------
+// attn_o's grid (kv head b % nkv, 32 Wo row blocks of 128 rows per kv head at the Mistral shape),
+// each workgroup also taking one KV slice of its kv head.
+template <int HD, int G>
+int slice_o_slices(const yhip_config& c) {
+  return attn_o_blocks<HD, G>(c) / c.n_kv_heads;
+}
+// Shapes whose partial block fits LDS (G * HD <= 512).
+int slice_o_slices_for(const yhip_config& c) {
+  switch (c.head_dim * 16 + c.n_heads / std::max(1, c.n_kv_heads)) {
+#define YK_SS(HD, G) case HD * 16 + G: return slice_o_slices<HD, G>(c);
+    YK_SS(32, 1) YK_SS(32, 2) YK_SS(32, 4) YK_SS(32, 8) YK_SS(64, 1) YK_SS(64, 2) YK_SS(64, 4) YK_SS(64, 8)
+    YK_SS(128, 1) YK_SS(128, 2) YK_SS(128, 4)
+#undef YK_SS
+    default: return 0;
+  }
+}
+
+// The step at pos runs it where attn_o would not (more than attn_o_max cached tokens, below
+// max_seq_len), with 8 kv heads on the probed round-robin order, the matrix-core attention's
+// shapes and a grid of one workgroup per CU at most.
+bool slice_o_at(const yhip_ctx* ctx, int pos) {
+  const yhip_config& c = ctx->c;
+  if (!ctx->slice_o || !ctx->xcd_rr || !attn_uses_mfma(ctx) || !attn_o_shape(c) || c.n_kv_heads != kQaoXcds ||
+      pos >= c.max_seq_len || pos + 1 <= ctx->attn_o_max)
+    return false;
+  const int ns = slice_o_slices_for(c);
+  return ns > 0 && ns <= kSliceOMaxSlices && c.n_kv_heads * ns <= std::min(ctx->num_cus, kXcdProbeGrid);
+}
+
+template <int HD, int G>
+void go_slice_o(const yhip_config& c, const AttnArgs& t, const AttnOArgs& o, const SliceOArgs& z, hipStream_t s) {
+  hipLaunchKernelGGL((slice_o_kernel<HD, G, kAttnOWaves, attn_o_loads<HD, G>()>), dim3(attn_o_blocks<HD, G>(c)),
+                     dim3(64 * kAttnOWaves), 0, s, t, o, z);
+}
+
+int launch_slice_o(yhip_ctx* ctx, AttnArgs t, const AttnOArgs& o, int layer, hipStream_t s) {
+  const yhip_config& c = ctx->c;
+  SliceOArgs z;
+  z.done = ctx->qkv_done + (size_t)layer * kQkvDoneParts * kQkvDoneStride;
+  z.abort_flag = ctx->step_abort;
+  z.slices = slice_o_slices_for(c);
+  t.nsplit = z.slices;  // the partial buffer's rows per head for this launch
+  switch (t.head_dim * 16 + t.n_heads / t.n_kv_heads) {
+#define YK_SO(HD, G) case HD * 16 + G: go_slice_o<HD, G>(c, t, o, z, s); break;
+    YK_SO(32, 1) YK_SO(32, 2) YK_SO(32, 4) YK_SO(32, 8) YK_SO(64, 1) YK_SO(64, 2) YK_SO(64, 4) YK_SO(64, 8)
+    YK_SO(128, 1) YK_SO(128, 2) YK_SO(128, 4)
+#undef YK_SO
+    default: return fail(ctx, YHIP_EINVAL, "attention slices + O: unsupported shape");
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention slices + O launch: ") + hipGetErrorString(e));
+  return YHIP_OK;
+}
+
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
 // variant: kStepSeparate (every kernel its own launch), kStepQkvAttn (the attention runs inside
 // the QKV launch, fused_attention_at), kStepAttnO (attention and O in one launch, attn_o_at) or
 // kStepSplitO (split-KV attention, then slice merge and O in one launch, split_o_at).
 // kStepQao: QKV, attention and O in one launch (qao_at).
-enum StepVariant : int { kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3, kStepQao = 4 };
+// kStepSliceO: split-KV attention, slice merge and O in one launch (slice_o_at).
+enum StepVariant : int {
+  kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3, kStepQao = 4, kStepSliceO = 5
+};
 int step_variant(const yhip_ctx* ctx, int pos) {
   if (fused_attention_at(ctx, pos)) return kStepQkvAttn;  // opt-in, so it takes precedence
   if (qao_at(ctx, pos)) return kStepQao;
   if (attn_o_at(ctx, pos)) return kStepAttnO;
+  if (slice_o_at(ctx, pos)) return kStepSliceO;
   return split_o_at(ctx, pos) ? kStepSplitO : kStepSeparate;
 }
 
@@ -664,7 +732,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       t.defer_merge = 1;
       if ((rc = launch_attention(ctx, t, s))) return rc;
     }
-    if (variant == kStepAttnO || variant == kStepSplitO) {
+    if (variant == kStepAttnO || variant == kStepSplitO || variant == kStepSliceO) {
       // 2 + 3. attention (or its slice merge) and O-proj + residual in one launch
       AttnOArgs o;
       o.wo = L.wo;
@@ -672,11 +740,15 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       o.rowacc = ctx->rowacc;
       o.dim = c.dim;
       o.q_dim = qd;
-      if ((rc = launch_attn_o(ctx, t, o, s, variant == kStepSplitO))) return rc;
+      if (variant == kStepSliceO) {
+        if ((rc = launch_slice_o(ctx, t, o, l, s))) return rc;
+      } else if ((rc = launch_attn_o(ctx, t, o, s, variant == kStepSplitO))) {
+        return rc;
+      }
     }
     if (variant == kStepSeparate && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
-    if (variant != kStepAttnO && variant != kStepSplitO && variant != kStepQao) {
+    if (variant != kStepAttnO && variant != kStepSplitO && variant != kStepQao && variant != kStepSliceO) {
     a = mv_base();
     a.w0 = L.wo;
     a.row_step = 2L * qd;
@@ -744,7 +816,7 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     HIP_TRY(ctx, hipGetLastError());
   }
-  if (fused || variant == kStepQao)  // the wait time-out / placement flag, checked after the caller's synchronisation
+  if (fused || variant == kStepQao || variant == kStepSliceO)  // a wait's time-out flag, checked after the caller's synchronisation
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (mode == 1) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
@@ -1331,7 +1403,9 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->attn_splits = std::max(1, std::min(64, 3 * ctx->num_cus / (4 * std::max(1, c.n_kv_heads))));
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "stream create failed"));
-  ctx->qao_note = qao_shape(c, ctx->num_cus) ? qao_probe(ctx) : std::string("shape");
+  const std::string probe = c.n_kv_heads == kQaoXcds ? xcd_probe(ctx) : std::string("kv heads");
+  ctx->xcd_rr = probe.empty();
+  ctx->qao_note = qao_shape(c, ctx->num_cus) ? probe : std::string("shape");
   ctx->qao_ok = ctx->qao_note.empty();
 
   // Weights: one allocation, 256-byte aligned sub-buffers.
@@ -1771,6 +1845,15 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "attn_o_max")) {
     if (value < 0) return fail(ctx, YHIP_EINVAL, "attn_o_max must be >= 0");
     ctx->attn_o_max = value;
+  } else if (!strcmp(key, "slice_o")) {
+    if (value == 2) {
+      const yhip_config& c = ctx->c;
+      const int ns = slice_o_slices_for(c);
+      if (!ctx->xcd_rr || !attn_uses_mfma(ctx) || !attn_o_shape(c) || c.n_kv_heads != kQaoXcds || ns <= 0 ||
+          ns > kSliceOMaxSlices || c.n_kv_heads * ns > std::min(ctx->num_cus, kXcdProbeGrid))
+        return fail(ctx, YHIP_EINVAL, "slice_o: no attention slices + O launch for this context");
+    }
+    ctx->slice_o = value != 0;
   } else if (!strcmp(key, "qao")) {
     if (value == 2 && !ctx->qao_ok)
       return fail(ctx, YHIP_EINVAL, "qao: no QKV + attention + O launch for this context (" + ctx->qao_note + ")");
