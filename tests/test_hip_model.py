@@ -38,6 +38,15 @@ def use_path(m, path):
         m.set_option(k, v)
 
 
+def require_launch(m, key):
+    """Turn on a launch that relies on the probed workgroup-to-XCD order (value 2 fails when this
+    GPU's order differs); the test is skipped, with the reason, where it is unavailable."""
+    try:
+        m.set_option(key, 2)
+    except hip().HipError as e:
+        pytest.skip(f"{key} unavailable on this GPU: {e}")
+
+
 def _models(cfg, tensors, path="single"):
     hm = hip().HipModel(cfg, tensors)
     use_path(hm, path)
@@ -507,7 +516,7 @@ def test_qkv_attention_and_o_in_one_launch_matches_oracle(path):
     cfg = ATTN_O_SHAPES["mistral"]
     t = np_tensors(cfg, seed=71, std=0.02)
     om, hm = _models(cfg, t, path)
-    hm.set_option("qao", 2)
+    require_launch(hm, "qao")
     rng = np.random.default_rng(72)
     n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
     for layer in range(cfg["n_layers"]):
@@ -543,7 +552,10 @@ def test_qkv_attention_and_o_in_one_launch_is_bit_reproducible():
     runs = []
     for qao in (2, 2, 0):
         with hip().HipModel(cfg, t) as m:
-            m.set_option("qao", qao)
+            if qao == 2:
+                require_launch(m, "qao")
+            else:
+                m.set_option("qao", qao)
             rng = np.random.default_rng(74)
             toks = rng.integers(0, cfg["vocab_size"], 40)
             out = [m.forward(int(tok), pos, 1) for pos, tok in enumerate(toks)]
@@ -590,7 +602,7 @@ def test_attention_slices_and_o_in_one_launch_matches_oracle(path, shape):
     cfg = SLICE_O_SHAPES[shape]
     t = np_tensors(cfg, seed=75, std=0.02)
     om, hm = _models(cfg, t, path)
-    hm.set_option("slice_o", 2)
+    require_launch(hm, "slice_o")
     rng = np.random.default_rng(76)
     n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
     for layer in range(cfg["n_layers"]):
@@ -618,7 +630,10 @@ def test_attention_slices_and_o_in_one_launch_is_bit_reproducible():
     outs = []
     for so in (2, 2, 0):
         with hip().HipModel(cfg, t) as m:
-            m.set_option("slice_o", so)
+            if so == 2:
+                require_launch(m, "slice_o")
+            else:
+                m.set_option("slice_o", so)
             m.kv_fill_normal(3000, 64)
             outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
     assert np.array_equal(outs[0], outs[1])
