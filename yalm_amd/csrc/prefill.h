@@ -70,6 +70,15 @@ __device__ __forceinline__ float max16(const f32x16& s) {
 // ------------------------------------------------------------------------------------------
 enum GemmEpi : int { kGemmStore = 0, kGemmResid = 1, kGemmSwiGLU = 2 };
 
+// SiLU of the SwiGLU epilogues, x * 1 / (1 + 2^(-x log2 e)) with the hardware exponential and
+// reciprocal (each within about an ulp): the epilogue stores fp16 (2^-11 relative), far coarser
+// than the few-ulp difference from the reference form x / (1 + expf(-x)) (src/infer.cpp:362-382),
+// whose range-reduced expf and IEEE divide take ~25 instructions per output, about 8% of a W1/W3
+// tile at 3200 rows. Both limits hold: 2^(+inf) makes the product -0, 2^(-inf) leaves x.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + exp2_fast(-x * kLog2e));
+}
+
 struct GemmArgs {
   const uint16_t* A;
   long lda;
@@ -186,7 +195,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) g
         const int j = n0 + wn * 32 + (lane & 31);
         if (j < g.N) {
           const float a1 = acc[i][0][r], a3 = acc[i][1][r];
-          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
           g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
         }
       } else {
@@ -386,7 +395,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_lds_kernel(GemmArgs g) {
         const int j = n0 + wn * 32 + (lane & 31);
         if (j < g.N) {
           const float a1 = acc[i][0][r], a3 = acc[i][1][r];
-          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
           g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
         }
       } else {
@@ -417,7 +426,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs g) {
         a1 += pp[0];
         a3 += pp[g.N];
       }
-      const float h = g.act == 1 ? silu(a1) : gelu(a1);
+      const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
       g.H[(long)m * g.ldh + n] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
     } else {
       float v = 0.f;
@@ -595,7 +604,7 @@ struct BigTile {
           const int j = n0 + wn * 64 + q * 32 + (lane & 31);
           if (j < g.N) {
             const float a1 = v[2 * q][r], a3 = v[2 * q + 1][r];
-            const float h = g.act == 1 ? silu(a1) : gelu(a1);
+            const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
             g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
           }
         }
@@ -836,7 +845,7 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g, PPSplit sp, un
         for (int r = 0; r < 16; ++r) {
           const int m = wm * 128 + i * 32 + acc_row(r, lane);
           const float a1 = acc[i][0][r], a3 = acc[i][1][r];
-          const float h = g.act == 1 ? silu(a1) : gelu(a1);
+          const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
           const unsigned off = col == kOut ? kOut : (unsigned)(m * g.ldh * 2) + col;
           __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)(h * a3)), hr, off, 0, 0);
         }
