@@ -1308,14 +1308,18 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int pc = min(tid + NT * i, KPIECES - 1);  // piece: chunk c, key, 8-dim half of the chunk
-      const int c = pc / 64, key = (pc % 64) >> 1, hh = pc & 1;
-      kst[i] = *reinterpret_cast<const u32x4*>(kh + (long)c * 16 * a.msl + (long)(k0 + key) * 16 + 8 * hh);
+      // piece: chunk c, LDS row (of key key_row(row)), 8-dim half hh of the chunk; consecutive lanes
+      // take consecutive rows with the same half, so each 16-lane LDS store pass hits distinct banks
+      const int pc = min(tid + NT * i, KPIECES - 1);
+      const int c = pc / 64, row = pc & 31, hh = (pc >> 5) & 1;
+      kst[i] = *reinterpret_cast<const u32x4*>(kh + (long)c * 16 * a.msl + (long)(k0 + key_row(row)) * 16 + 8 * hh);
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int pc = min(tid + NT * i, VPIECES - 1);  // piece: dim, 8 consecutive keys
-      const int d = pc >> 2, part = pc & 3;
+      // piece: dim d, 8 consecutive keys (part); 16 consecutive lanes take 16 dims of one part (row
+      // stride 5 banks-of-4 apart, distinct modulo 16) for conflict-free LDS stores
+      const int pc = min(tid + NT * i, VPIECES - 1);
+      const int d = (pc & 15) + 16 * (pc >> 6), part = (pc >> 4) & 3;
       vst[i] = *reinterpret_cast<const u32x4*>(vh + (long)d * a.msl + k0 + 8 * part);
     }
   };
@@ -1324,15 +1328,15 @@ __global__ void __launch_bounds__(64 * G * QT) prefill_attn_kernel(PrefillAttnAr
     for (int i = 0; i < KPT; ++i) {
       const int pc = tid + NT * i;
       if (pc < KPIECES) {
-        const int c = pc / 64, key = (pc % 64) >> 1, hh = pc & 1;
-        *reinterpret_cast<u32x4*>(&Ks[buf][key_row(key) * KLD + c * 16 + 8 * hh]) = kst[i];
+        const int c = pc / 64, row = pc & 31, hh = (pc >> 5) & 1;
+        *reinterpret_cast<u32x4*>(&Ks[buf][row * KLD + c * 16 + 8 * hh]) = kst[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int pc = tid + NT * i;
       if (pc < VPIECES) {
-        const int d = pc >> 2, part = pc & 3;
+        const int d = (pc & 15) + 16 * (pc >> 6), part = (pc >> 4) & 3;
         *reinterpret_cast<u32x4*>(&Vs[buf][d * VLD + 8 * part]) = vst[i];
       }
     }
