@@ -248,6 +248,42 @@ def test_full_depth_mistral_7b_shape_greedy_and_logits_match_oracle():
         assert worst < 2e-3, worst
 
 
+def test_tied_lm_head_greedy_and_logits_match_oracle():
+    # A checkpoint without model.output.weight reads the logits through the embedding table (reference
+    # src/model.cpp:425-434). The host Model hands the device no lm_head (yalm_amd/host/model.cpp),
+    # so the device's lm_head must stream the uploaded embedding: 24 greedy tokens through the
+    # completion loop equal to the oracle's, and the teacher-forced logits within rel-L2 1e-4.
+    from yalm_amd import host
+    shape = dict(host.TINY, n_layers=2)
+    with host.Session.synthetic(shape, context=256, seed=77, tied=True) as sess:
+        cfg = sess.config()
+        tensors = sess.tensors()
+        assert "model.output.weight" not in tensors
+        sess.hip(0)
+        prompt = [int(v) for v in host.uniform_ids(8, 91, cfg["vocab_size"])]
+        toks, _, _ = sess.generate(prompt, 24, temperature=0.0, device_argmax=True)
+        om = O.OracleModel(dict(cfg), tensors)
+        lo = None
+        for i, tok in enumerate(prompt):
+            lo = om.forward(tok, i, 1 if i == len(prompt) - 1 else 0)
+        ref, logits_o = [], [lo]
+        for k in range(24):
+            nxt = O.argmax(lo)
+            ref.append(nxt)
+            lo = om.forward(nxt, len(prompt) + k)
+            logits_o.append(lo)
+        om.close()
+        assert [int(t) for t in toks] == ref
+        seq = prompt + ref
+        worst = 0.0
+        for i in range(len(seq) - 1):
+            mode = 1 if i >= len(prompt) - 1 else 0
+            lh = sess.forward(seq[i], i, mode)
+            if mode == 1:
+                worst = max(worst, npref.rel_l2(lh, logits_o[i - len(prompt) + 1]))
+        assert worst < 1e-4, worst
+
+
 @pytest.mark.parametrize("path", ["single", "graph"])
 def test_greedy_sequence_matches_32_tokens(path):
     cfg = dict(TINY)

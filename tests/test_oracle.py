@@ -237,6 +237,23 @@ def test_forward_matches_float64_model(gain):
             assert np.array_equal(a != 0, b != 0) or np.all(np.abs(fa - fb) < 1e-6)
 
 
+def test_forward_tied_lm_head_reads_the_embedding():
+    # Without model.output.weight the logits come from the embedding table (reference
+    # src/model.cpp:425-434): equal bit for bit to the same model with the embedding passed as an
+    # explicit output matrix, and within 1e-4 of the float64 model
+    cfg = dict(MICRO)
+    t = np_tensors(cfg, seed=13, std=0.1)
+    t.pop("model.output.weight", None)
+    explicit = dict(t, **{"model.output.weight": t["model.embed.weight"].copy()})
+    om, oe, nm = O.OracleModel(cfg, t), O.OracleModel(cfg, explicit), npref.NpModel(cfg, t)
+    for pos, tok in enumerate([7, 300, 41, 2]):
+        lo = om.forward(tok, pos)
+        assert np.array_equal(lo, oe.forward(tok, pos)), pos
+        assert npref.rel_l2(lo, nm.forward(tok, pos)) < 1e-4, pos
+    om.close()
+    oe.close()
+
+
 def test_forward_hydrate_mode_writes_kv_only():
     cfg = dict(MICRO)
     t = np_tensors(cfg, seed=13, std=0.1)

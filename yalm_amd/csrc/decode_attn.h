@@ -575,8 +575,8 @@ __global__ void __launch_bounds__(64 * NW) attn_o_kernel(AttnArgs a, AttnOArgs o
 // launch before it stores every slice's partial (unnormalised output o_s, running maximum m_s in
 // natural units, sum l_s; AttnArgs::defer_merge) and skips its own last-slice merge. Workgroup b
 // (kv head g = b % nkv, rows as attn_o_kernel) requests kv head g's partial block (G heads x nsplit
-// slices x (HD + 2) floats, at most kMergeOMaxSplits slices) before its Wo block, merges
-// out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s) in LDS while the Wo
+// slices x (HD + 2) floats, at most kMergeOMaxSplits slices) into registers before its Wo block,
+// merges out_h = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s) while the Wo
 // stream is in flight (reference src/infer.cpp:172-187,218-250: one softmax over all keys,
 // restated over slices), then multiplies and combines rows as attn_o_kernel.
 // ------------------------------------------------------------------------------------------
@@ -586,11 +586,10 @@ template <int HD, int G, int NW, int U>
 __global__ void __launch_bounds__(64 * NW) merge_o_kernel(AttnArgs a, AttnOArgs o) {
   using Geo = AttnOGeom<HD, G, NW, U>;
   constexpr int RW = Geo::RW, NT = 64 * NW;
-  constexpr int PB = G * kMergeOMaxSplits * (HD + 2);  // floats of the largest partial block
-  constexpr int PPT = (PB / 4 + NT - 1) / NT;             // float4 per thread
-  static_assert((HD + 2) % 2 == 0, "partial rows");
-  __shared__ __attribute__((aligned(16))) float pb[PB];
-  __shared__ float wts[G][kMergeOMaxSplits];
+  constexpr int EPT = (G * HD + NT - 1) / NT;  // output elements per thread
+  constexpr int NS = kMergeOMaxSplits;
+  static_assert(G <= NW && NS <= 64, "one wave per head for the slice weights");
+  __shared__ float wts[G][NS];
   __shared__ float linv[G];
   __shared__ __attribute__((aligned(16))) float ao[G * HD];
   __shared__ float rs[NW][RW];
@@ -601,40 +600,54 @@ __global__ void __launch_bounds__(64 * NW) merge_o_kernel(AttnArgs a, AttnOArgs 
   const int chunk = attn_mfma_chunk(pss.kv_len, a.nsplit, a.min_slice);
   const int active = (pss.kv_len + chunk - 1) / chunk;  // as the attention launch counted them
 
-  // kv head g's partials: rows (g G + h) nsplit + s of HD + 2 floats, one contiguous block; the
-  // loads go out before the Wo loads, so waiting for them leaves the Wo stream in flight
-  const int nfl = G * a.nsplit * (HD + 2);
+  // kv head g's partials: rows (g G + h) nsplit + s of HD + 2 floats, one block (reads past it
+  // return zero). Straight into registers, before the Wo loads, so waiting for them leaves the Wo
+  // stream in flight: wave h < G takes (m, l) of slice s in lane s; every thread takes, for its
+  // output element (h, d), the d column of head h's active slices.
+  const int rowf = HD + 2;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      a.partial + (long)g * G * a.nsplit * (HD + 2), 0, nfl * (int)sizeof(float), kBufferConfig);
-  f32x4 pv[PPT];
+      a.partial + (long)g * G * a.nsplit * rowf, 0, G * a.nsplit * rowf * (int)sizeof(float), kBufferConfig);
+  float pm = kNegBig, pl = 0.f;
+  if (wave < G && lane < active) {
+    const int off = 4 * ((wave * a.nsplit + lane) * rowf + HD);
+    pm = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 0));
+    pl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, off + 4, 0, 0));
+  }
+  float po[EPT][NS];
 #pragma unroll
-  for (int k = 0; k < PPT; ++k)
-    pv[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * (tid + NT * k), 0, 0));
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + NT * i, h = e / HD, d = e % HD;
+    const int base = 4 * (h * a.nsplit * rowf + d);
+    if (e < G * HD) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        if (s < active)  // active is wave-uniform: a scalar branch
+          po[i][s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, base + 4 * s * rowf, 0, 0));
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   u32x4 wv[U];
   attn_o_issue<HD, G, NW, U>(o, g, row0, lane, wv);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < PPT; ++k)
-    if (4 * (tid + NT * k) < nfl) *reinterpret_cast<f32x4*>(pb + 4 * (tid + NT * k)) = pv[k];
-  __syncthreads();
   // per head: the slices' weights relative to the largest maximum, and 1 / sum_s w_s l_s
-  if (tid < G * 64) {
-    const int h = tid / 64, s = tid % 64;
-    const float* row = pb + (h * a.nsplit + s) * (HD + 2);
-    const float m = s < active ? row[HD] : kNegBig;
-    const float M = wave_max(m);
-    const float w = s < active ? expf(m - M) : 0.f;
-    const float L = wave_sum(s < active ? w * row[HD + 1] : 0.f);
-    if (s < kMergeOMaxSplits) wts[h][s] = w;
-    if (s == 0) linv[h] = 1.0f / L;
+  if (wave < G) {
+    const float M = wave_max(pm);
+    const float w = lane < active ? expf(pm - M) : 0.f;
+    const float L = wave_sum(w * pl);
+    if (lane < NS) wts[wave][lane] = w;
+    if (lane == 0) linv[wave] = 1.0f / L;
   }
   __syncthreads();
-  for (int e = tid; e < G * HD; e += NT) {
-    const int h = e / HD, d = e % HD;
-    float O = 0.f;
-    for (int s = 0; s < active; ++s) O = fmaf(wts[h][s], pb[(h * a.nsplit + s) * (HD + 2) + d], O);
-    ao[e] = O * linv[h];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + NT * i, h = e / HD;
+    if (e < G * HD) {
+      float O = 0.f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        if (s < active) O = fmaf(wts[h][s], po[i][s], O);
+      ao[e] = O * linv[h];
+    }
   }
   __syncthreads();
   attn_o_rows<HD, G, NW, U>(o, ao, rs, wv, row0, lane, wave, a.n_kv_heads);
