@@ -121,7 +121,7 @@ HOST_CPU = host_cpu()
 
 def cpu_baseline(session, cfg, prompt, gpu_tokens, budget_s):
     """The oracle on the host cores: hydrate the prompt, then greedy decode until the budget ends."""
-    from oracle import binding as O  # the checker, timed here as the CPU baseline
+    from oracle import binding as O  # the oracle, timed here as the CPU baseline
     om = O.OracleModel(dict(cfg), session.tensors())
     t0 = time.perf_counter()
     lg = None
@@ -242,8 +242,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py runs on one GPU only: this build has no multi-GPU path (the sharding design is "
-              "described in DESIGN.md); rerun with --gpus 1", file=sys.stderr)
+        print("bench.py runs on one GPU only: there is no multi-GPU path (the decode step is measured "
+              "on one GPU's share); rerun with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     from yalm_amd import hip, host

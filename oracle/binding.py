@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
 Imported only by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg, where the
-oracle is the checker (or the timed CPU baseline), never the product path.
+oracle is what results are compared against (or the timed CPU baseline), never the product path.
 """
 from __future__ import annotations
 

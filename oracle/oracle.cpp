@@ -1,7 +1,8 @@
 /*
  * CPU oracle: restatement of the reference `-d cpu` decode path -- TEST INFRASTRUCTURE ONLY.
  *
- * Loaded only by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg, as the checker.
+ * Loaded only by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg, as the reference
+ * that results are compared against.
  * Built like the reference CPU path (Makefile:32-36 of the reference): -O3 -ffast-math -fopenmp
  * -mf16c -mavx2 -mfma.
  *
