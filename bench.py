@@ -23,6 +23,10 @@ Printed JSON line extras:
   roofline      the dominant kernel (fused RMSNorm + W1/W3 + SwiGLU matvec, 234.9 MB of fp16 weights
                 per launch) timed live with HIP events on its launch stream over rotating weight copies
   step_roofline algorithmic bytes per token (all weights once + K/V read + K/V write) / step time
+  microbench    the per-layer kernels at the Mistral-7B shape (fused RMSNorm + QKV, O + residual,
+                RMSNorm + W1/W3 + SwiGLU, W2 + residual, RMSNorm + lm_head), each timed with HIP
+                events on its own stream over >= 1 GiB of rotating weight copies: microseconds,
+                GB/s of algorithmic bytes, fraction of 8 TB/s, and the recorded traffic ratio
   cpu_baseline  the CPU oracle (a restatement of the reference -d cpu path, OpenMP over the host
                 cores given to this process) on the same host weights, over a bounded sample of the
                 decode workload: decode tok/s, and the reference's own figure (prompt + generated
@@ -54,6 +58,20 @@ KV_BYTES_PER_POS = 131_072          # 32 layers x 8 kv heads x 128 x (K + V) x 2
 W13_BYTES = 2 * 14336 * 4096 * 2 + 4096 * 4 * 2 + 14336 * 4  # weights + x + gain + hb out
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 GREEDY_CHECK = 32  # generated tokens the CPU baseline compares with the GPU's, at least
+
+# The per-layer kernel workload at the Mistral-7B shape (fused RMSNorm feeding the fp16 matvecs):
+# (name, yhip_bench_kernel kind, output rows, row length, RMSNorm on the input, residual added).
+MICRO_KERNELS = [("qkv", 0, 6144, 4096, True, False), ("o", 1, 4096, 4096, False, True),
+                 ("w13", 2, 14336, 4096, True, False), ("w2", 3, 4096, 14336, False, True),
+                 ("lm_head", 4, 32000, 4096, True, False)]
+MICRO_WORKING_SET = 1 << 30  # rotating weight copies per kernel: at least 4 and at least 1 GiB in total
+
+
+def micro_bytes(kind, rows, cols, norm, resid):
+    """Algorithmic bytes of one launch: fp16 weights once (W1 and W3 for kind 2), the fp32 input,
+    the fp32 gain when normed, the fp32 outputs (SwiGLU: one per row pair), the residual read."""
+    nmat = 2 if kind == 2 else 1
+    return rows * cols * 2 * nmat + 4 * cols + (4 * cols if norm else 0) + 4 * rows + (4 * rows if resid else 0)
 
 
 def prefill_flops(cfg, n, start=0):
@@ -222,6 +240,37 @@ def run_attn(hip, host, sess, cfg, steps=64, fill=16384, ctx_len=16448, opts=())
             "step_roofline": step_roofline(kv_mean, tok_s)}
 
 
+def recorded_traffic():
+    """Per-kernel HBM traffic over algorithmic bytes, recorded from rocprofv3 FETCH_SIZE/WRITE_SIZE
+    passes of `bench.py --profile-kernel micro` (copy-calibrated); {} when not recorded."""
+    tf = os.path.join(ROOT, "profiles", "microbench_traffic.json")
+    if not os.path.exists(tf):
+        return {}
+    with open(tf) as f:
+        return json.load(f).get("kernels", {})
+
+
+def run_microbench(hip, reps, warmup=20):
+    """Each per-layer kernel on its own stream, HIP-event timed over rotating weight copies."""
+    traffic = recorded_traffic()
+    out = {}
+    for name, kind, rows, cols, norm, resid in MICRO_KERNELS:
+        wbytes = rows * cols * 2 * (2 if kind == 2 else 1)
+        copies = max(4, -(-MICRO_WORKING_SET // wbytes))
+        us = hip.bench_kernel(kind, rows, cols, copies=copies, warmup=warmup, reps=reps)
+        alg = micro_bytes(kind, rows, cols, norm, resid)
+        gbs = alg / (us * 1e-6) / 1e9
+        rec = traffic.get(name)
+        out[name] = {"shape": f"{rows}x{cols}" + (" x2" if kind == 2 else ""), "us_per_launch": round(us, 3),
+                     "bytes_per_launch": alg, "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                     "copies": copies, "traffic_ratio_recorded": rec.get("ratio") if rec else None}
+        log(f"[bench] microbench {name} {rows}x{cols}: {us:.2f} us/launch, {gbs:.0f} GB/s "
+            f"({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
+    out["traffic_source"] = ("profiles/microbench_traffic.json: recorded rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                             "passes of these launches, scaled by a plain copy's counters" if traffic else None)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,8 +286,9 @@ def main():
     ap.add_argument("--attn-min-slice", type=int, default=0, help="override the attention slice floor")
     ap.add_argument("--option", action="append", default=[], metavar="KEY=VALUE",
                     help="a context option of the HIP library (yhip_set_option), repeatable")
-    ap.add_argument("--profile-kernel", choices=["w13", "copy"], default=None,
-                    help="run only that kernel (for hardware-counter passes) and exit")
+    ap.add_argument("--profile-kernel", choices=["w13", "copy", "micro"], default=None,
+                    help="run only that kernel (micro: the five per-layer kernels, then the copy) for "
+                         "hardware-counter passes, and exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -248,6 +298,12 @@ def main():
 
     from yalm_amd import hip, host
 
+    if args.profile_kernel == "micro":
+        res = {name: round(hip.bench_kernel(kind, rows, cols, copies=4, warmup=2, reps=args.kernel_reps), 3)
+               for name, kind, rows, cols, _, _ in MICRO_KERNELS}
+        res["copy"] = round(hip.bench_kernel(5, 2 * 14336, 4096, copies=4, warmup=2, reps=args.kernel_reps), 3)
+        print(json.dumps({"kernel": "micro", "us_per_launch": res, "reps": args.kernel_reps}))
+        return
     if args.profile_kernel:
         # W1/W3 (2 x 14336 x 4096 fp16) or a plain copy of the same 234.9 MB; 7 rotating copies
         kind = 2 if args.profile_kernel == "w13" else 5
@@ -323,6 +379,7 @@ def main():
     us = hip.bench_kernel(2, 14336, 4096, copies=7, warmup=20, reps=args.kernel_reps)
     w13_gbs = W13_BYTES / (us * 1e-6) / 1e9
     log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {w13_gbs:.0f} GB/s")
+    micro = run_microbench(hip, args.kernel_reps)
 
     # what the step's launch structure allows: the same weight bytes through memory-only launches
     # of the same sizes and order (matvec access pattern), and through one launch
@@ -361,6 +418,8 @@ def main():
 
     w13 = {"bound": "hbm", "achieved": round(w13_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
            "frac": round(w13_gbs / PEAK_GBS, 4), "traffic": traffic_of("w13_swiglu_traffic.json"),
+           "traffic_kind": "recorded: profiles/w13_swiglu_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                           "per dispatch, copy-calibrated), not measured in this run",
            "kernel": "matvec_kernel<8,2> as rmsnorm + W1/W3 + SwiGLU (14336 x 4096 x 2)",
            "bytes_per_launch": W13_BYTES, "us_per_launch": round(us, 3)}
     if args.path == "single":
@@ -368,6 +427,7 @@ def main():
         achieved = step_bytes / (step_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_of("decode_step_traffic.json"),
+                    "traffic_kind": "recorded (profiles/decode_step_traffic.json), not measured in this run",
                     "kernel": "decode_flow_kernel<128,4> (the whole token, one launch)",
                     "bytes_per_launch": int(step_bytes), "us_per_launch": round(step_us, 3)}
     else:
@@ -396,6 +456,7 @@ def main():
         "reference_style_tok_s": round((n_prompt + steps) / (hydrate_s + total), 2),
         "roofline": roofline,
         "w13_kernel": w13,
+        "microbench": micro,
         "device_us_per_step": round(step_us, 2),
         "launch_ceiling": ceiling,
         "cpu_baseline": cpu,

@@ -36,6 +36,12 @@ extern "C" {
 #define YHIP_ACT_GELU 0
 #define YHIP_ACT_SILU 1
 
+/* Launch structure of one decode step (yhip_step_plan). */
+#define YHIP_STEP_SEPARATE 0 /* QKV, attention, O + residual, W1/W3, W2: each its own launch */
+#define YHIP_STEP_ATTN_O 1   /* attention and O in one launch (each workgroup repeats its kv head's attention) */
+#define YHIP_STEP_SPLIT_O 2  /* split-KV attention storing every slice's partial; the O launch merges them */
+#define YHIP_STEP_SINGLE 3   /* the whole step as one launch (option "single_launch") */
+
 typedef struct yhip_ctx yhip_ctx;
 
 /* Mirrors the decode-relevant fields of the reference Config (src/model.h:56-82). */
@@ -107,46 +113,36 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for
  * the MFMA attention one slice up to 320 cached tokens, then 64 up to 1024, 128 up to 5120 and 384
  * beyond; 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode
- * attention on the matrix cores where head_dim %
- * 32 == 0 and max_seq_len % 32 == 0, default; 0 = the SIMT kernel), "prefetch_o" /
- * "prefetch_w13_mb" / "prefetch_blocks" (extra workgroups of the attention launch read the layer's
- * O weights / the first MB of W1 and W3 into the caches; worker count, a multiple of 8; off by
- * default), "bpc_qkv" / "bpc_o" / "bpc_w13" / "bpc_w2" / "bpc_lm" (workgroups per CU of the decode
- * matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for W2; the
- * results do not depend on it), "stats" (1 = time every synchronised step on the device with HIP
- * events and reset the totals; 0 = off), "fuse_attn" (1 = run the decode attention inside the QKV
- * launch for steps with at most "fuse_attn_max" cached tokens (default 1024), below max_seq_len,
- * on the matrix-core attention's shapes; 0 = its own launch, the default, measured faster),
- * "attn_o" (1 = default: for steps with at most "attn_o_max" cached tokens (default 700), below
- * max_seq_len, on the matrix-core attention's shapes with at most 15 kv heads, attention and the O
- * projection run in one launch whose workgroups each repeat their kv head's attention and combine
- * their rows of Wo . attention in per-row integer words, bit-reproducibly; 0 = separate launches),
- * "split_o" (1 = default: beyond that, the split-KV attention stores every slice's partial and the
- * O launch merges them, with at most 32 slices per kv head; 0 = the attention launch merges its
- * own slices), "qao" (1 = QKV, attention and O in one launch for the steps attn_o would run, with
- * at most "qao_max" cached tokens (default 700), at head_dim 128, 4 query heads per kv head, 8 kv
- * heads and dim 4096, where a probe launch at yhip_create found the round-robin workgroup-to-XCD
- * order the launch relies on; 2 = the same, and the call fails when that launch is unavailable;
- * 0 = off, the default, measured slower), "qao_wo_after" (that launch's Wo loads go out after
- * this many of its workgroup barriers, 0..5, default 2), "slice_o" (1 = beyond "attn_o_max" cached
- * tokens, below max_seq_len, with 8 kv heads on that probed order and head_dim * query heads per
- * kv head at most 512: the O launch's own workgroups take the split-KV slices, one each, and merge
- * them through the XCD's L2; 2 = the same, and the call fails when that launch is unavailable;
- * 0 = off, the default, measured no faster than the attention launch followed by the merge + O
- * launch). The results of every option setting agree to fp32 rounding; each is tested against
- * the CPU reference. With ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the
- * yhip_test_* hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the
- * yhip_test_* / yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" (prefill
- * GEMM variant: stages -1 = chosen per shape (default), 0 = register-staged kernel, 1 = 256 x 256
- * large tiles (four waves), 2..4 = LDS pipeline stages, 5 = the large tiles with stream-K, 6 = the
- * eight-wave 256 x 256 kernel; k-step 32 or 64; workgroup rows 128 or 256), "gemm_ppsplit" (1 =
+ * attention on the matrix cores where head_dim % 32 == 0 and max_seq_len % 32 == 0, default;
+ * 0 = the SIMT kernel), "bpc_qkv" / "bpc_o" / "bpc_w13" / "bpc_w2" / "bpc_lm" (workgroups per CU
+ * of the decode matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for
+ * W2; the results do not depend on it), "stats" (1 = time every synchronised step on the device
+ * with HIP events and reset the totals; 0 = off), "attn_o" (1 = default: for steps with at most
+ * "attn_o_max" cached tokens (default 700), below max_seq_len, on the matrix-core attention's
+ * shapes with at most 8 kv heads, attention and the O projection run in one launch whose
+ * workgroups each repeat their kv head's attention and combine their rows of Wo . attention in
+ * per-row integer words, bit-reproducibly; 0 = separate launches), "split_o" (1 = default: beyond
+ * that, the split-KV attention stores every slice's partial and the O launch merges them, with at
+ * most 32 slices per kv head; 0 = the attention launch merges its own slices). The results of
+ * every option setting agree to fp32 rounding; each is tested against the CPU reference. With
+ * ctx == NULL it sets process-wide options: "test_bpc" (workgroups per CU used by the yhip_test_*
+ * hooks; 0 = the decode path's default), "attn_mfma" (attention kernel of the yhip_test_* /
+ * yhip_bench_* hooks, as above), "gemm_stages" / "gemm_bk" / "gemm_bm" / "gemm_ksplit" (prefill
+ * GEMM variant: stages -1 = chosen per shape (default), 2..4 = the LDS pipeline's depth (4 with
+ * 32-deep k-steps, 2 or 3 with 64-deep ones), 6 = the eight-wave 256 x 256 kernel; k-step 32 or
+ * 64; workgroup rows 128 or 256; K splits of the LDS pipeline, 0 = per shape), "gemm_ppsplit" (1 =
  * default: the eight-wave kernel splits its last, partial round of tiles along K where that pays;
- * 0 = whole tiles only), "gemm_il" (four-wave large tiles: k-step schedule, -1 = per shape),
- * "upload_stage_mb" (yhip_upload_layer / yhip_upload_globals copy tensors of 64 KB and more through
- * a ring of three pinned staging chunks of this many MB, default 64; 0 = direct copies from the
- * caller's pageable memory as the reference's upload_cuda, src/infer.cu:34-39) and
- * "upload_threads" (host threads filling a staging chunk, default 8). */
+ * 0 = whole tiles only), "upload_stage_mb" (yhip_upload_layer / yhip_upload_globals copy tensors
+ * of 64 KB and more through a ring of three pinned staging chunks of this many MB, default 64;
+ * 0 = direct copies from the caller's pageable memory as the reference's upload_cuda,
+ * src/infer.cu:34-39) and "upload_threads" (host threads filling a staging chunk, default 8). */
 int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
+
+/* The launch plan of the decode step at `pos` under the context's current options: *variant one
+ * of YHIP_STEP_*, *slices the KV slices per kv head that hold keys and *slice_len their length in
+ * keys (YHIP_STEP_ATTN_O: 1 and the context length, every workgroup attends to the whole
+ * context). Any output may be NULL. No reference counterpart (a test and diagnostics hook). */
+int yhip_step_plan(yhip_ctx* ctx, int pos, int* variant, int* slices, int* slice_len);
 
 /* Device time of the steps timed since "stats" was set: total microseconds between HIP events
  * recorded on the context's stream around each LOGITS/argmax step's kernels, and the step count.
@@ -154,7 +150,8 @@ int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 int yhip_step_stats(const yhip_ctx* ctx, double* us_total, int* steps);
 
 /* Debug read of a device activation after the last forward: which = 0 x [dim], 1 q [nh*hd],
- * 2 attention output [nh*hd], 3 hb [hidden], 4 logits [vocab]. Mirrors the reference's
+ * 2 attention output [nh*hd], 3 hb [hidden], 4 logits [vocab]; 5 the rotary frequencies the
+ * step uses [head_dim / 2] (fp32, 1 / powf(theta, j / rotary_dim) rounded on the host). Mirrors the reference's
  * DEBUG_MODEL tensor dumps (src/infer.cu:93-109). */
 int yhip_debug_read(yhip_ctx* ctx, int which, float* host, size_t n);
 
@@ -172,7 +169,10 @@ int yhip_test_matvec(const float* x, const float* gain, float eps, const uint16_
 int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* w1, const uint16_t* w2,
                   const uint16_t* w3, int hidden_dim, int dim, int act, const float* resid, float* out);
 /* GQA attention over reference-layout caches (src/infer.cpp:218-250, 394-415); `nsplit` KV slices
- * per kv head (0 = default). att_out [n_heads*hd]. pos >= max_seq_len exercises sink rotation, which
+ * per kv head of at least 64 keys, or 0 = the decode step's own slice plan (3/4 of the compute
+ * units over the kv heads; the MFMA kernel's length rule, as option "attn_min_slice" 0).
+ * The slices are merged inside the launch (the decode step beyond 700 keys defers that merge to
+ * its O launch instead). att_out [n_heads*hd]. pos >= max_seq_len exercises sink rotation, which
  * rewrites kcache (the updated K cache is copied back). kv_len is derived from pos. */
 int yhip_test_attention(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,
                         int max_seq_len, int n_heads, int n_kv_heads, int nsplit, float rope_theta,
@@ -202,9 +202,8 @@ int yhip_test_qkv(const float* x, const float* gain, float eps, const uint16_t* 
 int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16_t* b3, int M, int N, int K, int mode, int act,
                    float* c, uint16_t* h);
 /* The prefill GEMM variant yhip_prefill runs for this shape and mode (as yhip_test_gemm), under the
- * current process-wide options: stages 6 = the eight-wave 256 x 256 kernel, 1 = the four-wave
- * 256 x 256 kernel, 5 = the same with stream-K, 2..4 = the LDS pipeline's depth, 0 = the
- * register-staged kernel; bk the k-step; bm the workgroup's rows. No
+ * current process-wide options: stages 6 = the eight-wave 256 x 256 kernel, 2..4 = the LDS
+ * pipeline's depth; bk the k-step; bm the workgroup's rows. No
  * reference counterpart (the reference has no batched prefill). */
 int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int* bk, int* bm);
 /* Greedy argmax on the device with the reference tie rule. */

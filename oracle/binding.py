@@ -71,6 +71,8 @@ def lib():
         L.oracle_value_cache.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.oracle_x.restype = _f32p
         L.oracle_x.argtypes = [ctypes.c_void_p]
+        L.oracle_set_rope_freqs.restype = ctypes.c_int
+        L.oracle_set_rope_freqs.argtypes = [ctypes.c_void_p, _f32p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -254,6 +256,13 @@ class OracleModel:
 
     def x(self):
         return np.ctypeslib.as_array(lib().oracle_x(self.h), shape=(self.cfg.dim,)).copy()
+
+    def set_rope_freqs(self, freqs=None):
+        """Rotate with these head_dim / 2 frequencies instead of the reference's expression
+        (None restores it)."""
+        f = np.ascontiguousarray(freqs if freqs is not None else [], np.float32)
+        if lib().oracle_set_rope_freqs(self.h, f.ctypes.data_as(_f32p), int(f.size)) != 0:
+            raise ValueError("oracle_set_rope_freqs: expected head_dim / 2 frequencies")
 
     def close(self):
         if self.h:

@@ -232,7 +232,35 @@ struct oracle_model {
   const uint16_t* wcls = nullptr;
   // InferenceState workspace (model.cpp:291-307)
   std::vector<float> x, xb, xb2, hb, hb2, q, k, v, att;
+  // Rotary frequencies set from outside (oracle_set_rope_freqs), one per pair of a head; empty:
+  // each rotation computes them as the reference does (infer.cpp:205)
+  std::vector<float> rope_freqs;
 };
+
+// The model's RoPE: oracle_rope, or the same rotation with the frequencies set from outside.
+static void model_rope(const oracle_model* m, float* vec, int d, int pos) {
+  const oracle_config& c = m->c;
+  if (m->rope_freqs.empty()) {
+    oracle_rope(vec, d, c.head_dim, pos, c.rope_theta, c.rotary_dim);
+    return;
+  }
+  for (int i = 0; i < d; i += 2) {
+    float ang = pos * m->rope_freqs[(i % c.head_dim) / 2];
+    float cs = cosf(ang), sn = sinf(ang);
+    float a = vec[i], b = vec[i + 1];
+    vec[i] = a * cs - b * sn;
+    vec[i + 1] = a * sn + b * cs;
+  }
+}
+
+// Test hook: rotate with these frequencies (head_dim / 2 of them) instead of the reference's
+// 1 / powf(theta, j / rotary_dim), which a -ffast-math build may round an ulp away from the
+// correctly rounded value. n = 0 restores the reference's expression.
+extern "C" int oracle_set_rope_freqs(oracle_model* m, const float* freqs, int n) {
+  if (!m || n < 0 || (n > 0 && (!freqs || n != m->c.head_dim / 2))) return -1;
+  m->rope_freqs.assign(freqs, freqs + n);
+  return 0;
+}
 
 extern "C" int oracle_create(const oracle_config* cfg, oracle_model** out) {
   if (!cfg || !out) return -1;
@@ -311,8 +339,8 @@ static void block_forward(oracle_model* m, OracleLayer& L, int pos, int kv_sink,
     k[i] = clampf(k[i], c.qkv_clip);
     v[i] = clampf(v[i], c.qkv_clip);
   }
-  oracle_rope(q, qd, c.head_dim, pos, c.rope_theta, c.rotary_dim);  // :293-294
-  oracle_rope(k, kvd, c.head_dim, pos, c.rope_theta, c.rotary_dim);
+  model_rope(m, q, qd, pos);  // :293-294
+  model_rope(m, k, kvd, pos);
 
   uint16_t* kb = L.kcache.data();
   uint16_t* vb = L.vcache.data();
@@ -326,7 +354,7 @@ static void block_forward(oracle_model* m, OracleLayer& L, int pos, int kv_sink,
       int g = i / c.head_dim, j = i % c.head_dim;
       k[i] = oracle_h2f(kb[g * c.head_dim * msl + oracle_k_cache_idx(j, r, c.max_seq_len)]);
     }
-    oracle_rope(k, kvd, c.head_dim, 1, c.rope_theta, c.rotary_dim);
+    model_rope(m, k, kvd, 1);
     for (int i = 0; i < kvd; ++i) {
       int g = i / c.head_dim, j = i % c.head_dim;
       kb[g * c.head_dim * msl + oracle_k_cache_idx(j, r, c.max_seq_len)] = oracle_f2h(k[i]);

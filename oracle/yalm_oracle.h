@@ -68,6 +68,9 @@ uint16_t* oracle_key_cache(oracle_model* m, int layer);
 uint16_t* oracle_value_cache(oracle_model* m, int layer);
 /* The fp32 residual stream x after the last forward (dim floats). */
 const float* oracle_x(oracle_model* m);
+/* Test hook: the model rotates with these head_dim / 2 frequencies instead of the reference's
+ * 1 / powf(theta, j / rotary_dim) (n = 0 restores it). */
+int oracle_set_rope_freqs(oracle_model* m, const float* freqs, int n);
 
 #ifdef __cplusplus
 }

@@ -37,9 +37,10 @@ def bpc(request):
 
 
 # (1002, 4096) and (6, 14336): more waves than row groups on the unrolled paths (the idle waves'
-# first loads go through zero-length descriptors)
+# first loads go through zero-length descriptors); (4096, 4096) and (32000, 4096): the O projection
+# (with the residual) and the lm_head (with the final norm) at the Mistral-7B shape
 @pytest.mark.parametrize("d,n", [(32, 64), (100, 256), (384, 768), (6144, 4096), (4096, 14336), (1000, 4096),
-                                 (1002, 4096), (6, 14336)])
+                                 (1002, 4096), (6, 14336), (4096, 4096), (32000, 4096)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_matvec_parity(d, n, norm, bpc):
     rng = np.random.default_rng(d * 7 + n)
@@ -85,6 +86,32 @@ def test_ffn_parity(dim, hidden, act, bpc):
     assert npref.rel_l2(got, want) < RTOL
 
 
+def test_per_layer_kernels_of_the_microbenchmark_workload():
+    # The per-layer kernel workload at the Mistral-7B shape, as the benchmark runs it: x fp16 [4096]
+    # ~ N(0, 1) (seed 2), weights N(0, 0.02), RMSNorm (eps 1e-5, unit gains) feeding QKV
+    # 4096 -> 6144, O 4096 -> 4096 plus the residual, W1/W3 4096 -> 14336 with SwiGLU then W2
+    # 14336 -> 4096 plus the residual, and the lm_head 4096 -> 32000; each against the oracle's
+    # fp32-accumulated matvec (reference src/infer.cpp:63-100, 136-146, 339-344, 362-390, 501-527).
+    rng = np.random.default_rng(2)
+    x = h2f(f16(rng.standard_normal(4096)))
+    g = np.ones(4096, np.float32)
+    xn = O.rmsnorm(x, g, 1e-5)
+    r = rng.standard_normal(4096).astype(np.float32)
+
+    def w(d, n):
+        return f16(rng.standard_normal((d, n), dtype=np.float32) * 0.02)
+
+    wqkv = w(6144, 4096)
+    assert npref.rel_l2(hip().matvec(x, wqkv, gain=g, eps=1e-5), O.matmul_f16(xn, wqkv)) < RTOL
+    wo = w(4096, 4096)
+    assert npref.rel_l2(hip().matvec(x, wo, resid=r), O.matmul_f16(x, wo) + r) < RTOL
+    w1, w3, w2 = w(14336, 4096), w(14336, 4096), w(4096, 14336)
+    got = hip().ffn(x, w1, w2, w3, gain=g, eps=1e-5, act=1, resid=r)
+    assert npref.rel_l2(got, O.ffn(xn, w1, w2, w3, 1) + r) < RTOL
+    wcls = w(32000, 4096)
+    assert npref.rel_l2(hip().matvec(x, wcls, gain=g, eps=1e-5), O.matmul_f16(xn, wcls)) < RTOL
+
+
 @pytest.mark.parametrize("hidden", [1024, 4096, 8192])
 def test_swiglu_rows_exact_over_row_loop(hidden, bpc):
     # Square down-projection with identity rows makes the FFN output equal hb itself, so every
@@ -105,7 +132,9 @@ def test_swiglu_rows_exact_over_row_loop(hidden, bpc):
 
 
 ATTN_CASES = [
-    # hd, nh, nkv, msl, kv_len, nsplit
+    # hd, nh, nkv, msl, kv_len, nsplit; nsplit 0 = the decode step's own slice plan (3/4 of the CUs
+    # over the kv heads; on the matrix cores one slice up to 320 keys, then 64-, 128- and 384-key
+    # slices: 16417 keys as 24 slices of 704 on a 256-CU part), else nsplit slices of at least 64
     (16, 4, 2, 64, 1, 0),
     (32, 8, 2, 512, 17, 0),
     (32, 8, 2, 512, 512, 3),
@@ -116,21 +145,24 @@ ATTN_CASES = [
     (128, 32, 8, 16448, 16417, 0),
     (128, 8, 1, 1024, 700, 1),
     (64, 8, 8, 100, 99, 0),       # max_seq_len not a multiple of 8: scalar V path
-    (128, 32, 8, 4096, 64, 0),    # exactly one 64-token slice
-    (128, 32, 8, 4096, 65, 0),    # a second slice holding one token
+    (128, 32, 8, 4096, 64, 32),   # exactly one 64-token slice
+    (128, 32, 8, 4096, 65, 32),   # a second slice holding one token
+    (128, 32, 8, 4096, 700, 0),   # 64-key slices, merged across 11 workgroups
+    (128, 32, 8, 4096, 3216, 0),  # 128-key slices
     (32, 8, 2, 520, 300, 5),
     (16, 8, 1, 333, 333, 0),
     (128, 8, 8, 256, 200, 0),     # one query head per kv head
     (128, 16, 8, 512, 300, 0),    # two
     (64, 16, 2, 208, 150, 4),     # eight, head_dim 64
     (32, 4, 1, 1024, 1000, 64),   # many slices
-    (128, 32, 8, 4096, 256, 0),
-    (128, 32, 8, 4096, 257, 0),
+    (128, 32, 8, 4096, 256, 32),
+    (128, 32, 8, 4096, 257, 32),
     # waves with no tile in their slice skip their loads: one tile, one key past it, seven tiles
     # and a key, a last slice holding a single key, a last slice shorter than one tile
     (128, 32, 8, 4096, 32, 0),
     (128, 32, 8, 4096, 33, 0),
     (128, 32, 8, 4096, 225, 0),
+    (128, 32, 8, 4096, 225, 32),
     (128, 32, 8, 4096, 513, 2),
     (128, 32, 8, 4096, 1030, 4),
 ]

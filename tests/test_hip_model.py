@@ -1,8 +1,11 @@
 """Whole decode-step parity: HIP path (through the C-ABI) against the CPU oracle.
 
 Contract (reference -d cpu semantics): embedding gather and KV-cache indexing bit-exact; logits
-within rel-L2 1e-2 teacher-forced (fp32 accumulation on both sides; observed ~1e-6); the greedy
-token sequence identical for the first 32 generated tokens.
+within rel-L2 1e-2 teacher-forced (fp32 accumulation on both sides); the greedy token sequence
+identical for the first 32 generated tokens. Observed: ~1e-6 at the small shapes; at the Mistral-7B
+shape up to ~2e-4 at short context, where one K/V entry that fp32 summation order rounds to the
+other neighbouring fp16 on one side moves the following layers (the oracle itself is as far from a
+float64 evaluation there as the HIP path is from the oracle).
 """
 import numpy as np
 import pytest
@@ -25,12 +28,10 @@ def hip():
 # The ways a step can run: one launch per token (a dataflow of workgroups), the captured hipGraph
 # of per-op kernels (the default: attention and O share a launch up to 700 keys, beyond that the
 # attention's slice merge moves into the O launch), the same kernels launched directly, the graph
-# with the SIMT attention, the graph with attention (merge included) and O in separate launches, and
-# the graph with QKV, attention and O in one launch where the shape allows it (opt-in).
+# with the SIMT attention, and the graph with attention (merge included) and O in separate launches.
 PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
          "direct": dict(single_launch=0, graph=0), "graph_simt": dict(single_launch=0, graph=1, attn_mfma=0),
-         "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0),
-         "graph_qao": dict(single_launch=0, graph=1, qao=1)}
+         "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0)}
 
 
 def use_path(m, path):
@@ -38,19 +39,82 @@ def use_path(m, path):
         m.set_option(k, v)
 
 
-def require_launch(m, key):
-    """Turn on a launch that relies on the probed workgroup-to-XCD order (value 2 fails when this
-    GPU's order differs); the test is skipped, with the reason, where it is unavailable."""
-    try:
-        m.set_option(key, 2)
-    except hip().HipError as e:
-        pytest.skip(f"{key} unavailable on this GPU: {e}")
-
-
 def _models(cfg, tensors, path="single"):
     hm = hip().HipModel(cfg, tensors)
     use_path(hm, path)
     return O.OracleModel(cfg, tensors), hm
+
+
+def _written_masks(cfg, positions):
+    """Masks over one layer's K and V caches of the entries that steps at `positions` write: the
+    ring slot of each position (reference src/infer.cpp:300-305 in the layout of src/model.h:14-17)
+    and the two sink keys that every step past the context re-rotates (src/infer.cpp:307-325).
+    Also, per K entry, the position whose rotation angle it carries, and how many times it was
+    re-rotated as a sink key."""
+    nkv, hd, msl = cfg["n_kv_heads"], cfg["head_dim"], cfg["max_seq_len"]
+    km = np.zeros((nkv, hd // 16, msl, 16), bool)
+    vm = np.zeros((nkv, hd, msl), bool)
+    kpos = np.zeros((nkv, hd // 16, msl, 16), np.float64)
+    krot = np.zeros_like(kpos)
+    for pos in positions:
+        kv_sink, kv_pos, _ = O.positions(pos, msl)
+        km[:, :, kv_pos, :] = True
+        vm[:, :, kv_pos] = True
+        kpos[:, :, kv_pos, :] = pos
+        km[:, :, :kv_sink, :] = True
+        krot[:, :, :kv_sink, :] += 1
+    return km.reshape(-1), vm.reshape(-1), kpos.reshape(-1), krot.reshape(-1)
+
+
+# Written K/V entries: |hip - oracle| <= max(one fp16 ulp, noise x the written entries' RMS), the
+# noise 2e-4 in the first layer and 2e-3 deeper; for K plus the rotation term below. Both sides
+# round fp32 values to fp16; where fp32 summation order puts one entry on the other side of a
+# rounding boundary, the ulp it moves reaches the following layers as a ~1e-5..1e-4 relative change
+# (at the first positions of the Mistral-shape test the logits of the HIP path are 0.8..6e-5 from a
+# float64 evaluation, the oracle's 4..12e-5, and the deeper layers' K/V differ by up to ~5e-4 of
+# their RMS). A mis-slotted, zeroed or stale entry is off by O(RMS).
+KV_NOISE = (2e-4, 2e-3)
+# The RoPE angle pos * freq is an fp32 product of an fp32 frequency that the reference's fast-math
+# powf and ours may round an ulp apart (src/infer.cpp:205-206): the angle then differs by up to
+# ~pos * 2^-22 rad, which moves a rotated pair (k0, k1) by |(k0, k1)| times that (at position
+# 4096, 9.8e-4 rad). A re-rotated sink key may move by an ulp per rotation.
+ANGLE_REL = 2.0 ** -22
+
+
+def _check_kv_prefilled(om, hm, cfg, prefill, positions):
+    """Caches that started from the same host pre-fill: every entry no step wrote is bit-identical to
+    the pre-fill on both sides (no stray or mis-slotted write); every written entry is zero on both
+    sides or on neither (no flushed or dropped value) and within the noise bound of the oracle's."""
+    km, vm, kpos, krot = _written_masks(cfg, positions)
+    for layer, (kp, vp) in enumerate(prefill):
+        (kh, vh), (ko, vo) = hm.kv(layer), om.kv(layer)
+        for name, got, want, pre, m in (("K", kh, ko, kp, km), ("V", vh, vo, vp, vm)):
+            assert np.array_equal(got[~m], pre[~m]) and np.array_equal(want[~m], pre[~m]), (layer, name)
+            a, b = got[m], want[m]
+            assert np.array_equal((a & 0x7FFF) == 0, (b & 0x7FFF) == 0), (layer, name)
+            fa, fb = h2f(a).astype(np.float64), h2f(b).astype(np.float64)
+            with np.errstate(over="ignore"):  # the spacing above the largest finite fp16 is inf
+                ulp = np.spacing(np.abs(b.view(np.float16))).astype(np.float64)
+            bound = np.maximum(ulp, KV_NOISE[min(layer, 1)] * np.sqrt(np.mean(fb * fb)))
+            if name == "K":  # dims 2i and 2i + 1 (a rotation pair) are adjacent in the 16-tiled layout
+                full = h2f(want).astype(np.float64)
+                pair = np.repeat(np.sqrt(np.sum(full.reshape(-1, 2) ** 2, axis=1)), 2)[m]
+                bound = bound + pair * kpos[m] * ANGLE_REL + krot[m] * ulp
+            worst = int(np.argmax(np.abs(fa - fb) - bound))
+            assert np.abs(fa - fb)[worst] <= bound[worst], (layer, name, fa[worst], fb[worst], bound[worst])
+
+
+def _prefill_kv(om, hm, cfg, rng, k_scale=0.5):
+    """The same fp16 draws (K ~ N(0, k_scale), V ~ N(0, 1)) in every layer's caches on both sides."""
+    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
+    out = []
+    for layer in range(cfg["n_layers"]):
+        k = (rng.standard_normal(n, dtype=np.float32) * k_scale).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
+        om.set_kv(layer, k, v)
+        hm.set_kv(layer, k, v)
+        out.append((k, v))
+    return out
 
 
 def _check_kv(om, hm, n_layers):
@@ -86,7 +150,7 @@ def test_embedding_gather_bit_exact(path):
             assert np.array_equal(x, h2f(t["model.embed.weight"][tok]))
 
 
-@pytest.mark.parametrize("path", ["single", "graph", "direct", "graph_qao"])
+@pytest.mark.parametrize("path", ["single", "graph", "direct"])
 @pytest.mark.parametrize("shape", ["tiny", "mistral"])
 def test_embedding_gather_bit_exact_through_layer0(path, shape):
     # The production gather: layer 0's QKV matvec stages the fp16 embedding row and writes it to
@@ -188,7 +252,7 @@ def test_teacher_forced_logits_and_kv(cfg_name, path):
     hm.close()
 
 
-@pytest.mark.parametrize("path", ["single", "graph", "graph_sep", "graph_qao"])
+@pytest.mark.parametrize("path", ["single", "graph", "graph_sep"])
 def test_mistral_shape_two_layers(path):
     # The Mistral-7B layer shape (dim 4096, hidden 14336, 32/8 heads of 128) with two layers: the
     # instantiations the full model runs, checked teacher-forced against the oracle.
@@ -395,7 +459,8 @@ def test_kv_write_then_decode_long_context(path):
     hm.close()
 
 
-FUSE_SHAPES = {
+# Small attention shapes: head_dim 32/64/128 with 1, 2, 4 and 8 query heads per kv head.
+SMALL_ATTN_SHAPES = {
     "tiny": dict(TINY),  # head_dim 32, 4 q heads per kv head, dim 256
     "hd64_g2": dict(TINY, dim=256, head_dim=64, n_heads=4, n_kv_heads=2, rotary_dim=64, n_layers=2),
     "hd128_g8": dict(TINY, dim=1024, head_dim=128, n_heads=8, n_kv_heads=1, rotary_dim=128, n_layers=2),
@@ -403,69 +468,30 @@ FUSE_SHAPES = {
 }
 
 
-@pytest.mark.parametrize("path", ["graph", "direct"])
-@pytest.mark.parametrize("shape", list(FUSE_SHAPES))
-def test_attention_fused_into_qkv_matches_oracle(path, shape):
-    # Short contexts run the attention inside the QKV launch (the first workgroups to finish take
-    # the attention items once every q/K/V row is written); longer ones launch it separately. With
-    # the threshold at 200 tokens and slices of 64 the sequence crosses it, after running 1 to 4
-    # slices per kv head fused (their merge included).
-    cfg = FUSE_SHAPES[shape]
-    t = np_tensors(cfg, seed=55, std=0.02)
-    om, hm = _models(cfg, t, path)
-    ref = hip().HipModel(cfg, t)  # attention always in its own launch
-    use_path(ref, path)
-    ref.set_option("fuse_attn", 0)
-    ref.set_option("attn_o", 0)
-    hm.set_option("fuse_attn", 1)
-    hm.set_option("fuse_attn_max", 200)
-    hm.set_option("attn_min_slice", 64)
-    ref.set_option("attn_min_slice", 64)
-    rng = np.random.default_rng(56)
-    toks = rng.integers(0, cfg["vocab_size"], 230)
-    for pos, tok in enumerate(toks):
-        mode = 1 if (pos % 7 == 0 or pos > 190) else 0
-        lo = om.forward(int(tok), pos, mode)
-        lh = hm.forward(int(tok), pos, mode)
-        lr = ref.forward(int(tok), pos, mode)
-        if mode == 1:
-            assert npref.rel_l2(lh, lo) < 1e-4, pos
-            assert npref.rel_l2(lr, lo) < 1e-4, pos
-            assert npref.rel_l2(lh, lr) < 1e-4, pos
-    _check_kv(om, hm, cfg["n_layers"])
-    hm.close()
-    ref.close()
-
-
-ATTN_O_SHAPES = dict(FUSE_SHAPES, mistral=dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32,
-                                                n_kv_heads=8, max_seq_len=704, rotary_dim=128))
+ATTN_O_SHAPES = dict(SMALL_ATTN_SHAPES, mistral=dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2,
+                                                     n_heads=32, n_kv_heads=8, max_seq_len=704, rotary_dim=128))
 
 
 @pytest.mark.parametrize("path", ["graph", "direct"])
 @pytest.mark.parametrize("shape", list(ATTN_O_SHAPES))
 def test_attention_and_o_in_one_launch_matches_oracle(path, shape):
     # Attention and the O projection in one launch: every workgroup runs the whole-context
-    # attention of its kv head and adds its rows of Wo . attention into x with float atomics (the
-    # addition order varies, so the comparison is to tolerance). The threshold at 600 tokens puts
-    # positions with one and with several 32-key tiles per wave (8 waves: 256 keys a round) on the
-    # one-launch side and the rest on the separate kernels.
+    # attention of its kv head and combines its rows of Wo . attention with the other kv heads' in
+    # integer fixed-point words per row (bit-reproducible, tested below; the fixed point rounds each
+    # partial to 2^-32, so the comparison with the oracle is to tolerance). The threshold at 600
+    # tokens puts positions with one and with several 32-key tiles per wave (8 waves: 256 keys a
+    # round) on the one-launch side and the rest on the separate kernels.
     # At the Mistral shape the cache is pre-filled from the host (the same entries on both sides)
-    # and only the listed positions run, which keeps the oracle's share of the test short.
+    # and only the listed positions run, which keeps the oracle's share of the test short; the
+    # caches are then checked entry by entry against the pre-fill and the oracle.
     cfg = ATTN_O_SHAPES[shape]
     t = np_tensors(cfg, seed=57, std=0.02)
     om, hm = _models(cfg, t, path)
-    hm.set_option("qao", 0)  # the attention + O launch itself (the QKV + attention + O one is tested below)
     hm.set_option("attn_o", 1)
     hm.set_option("attn_o_max", 600)
     rng = np.random.default_rng(58)
     prefilled = shape == "mistral"
-    if prefilled:
-        n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-        for layer in range(cfg["n_layers"]):
-            k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
-            v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
-            om.set_kv(layer, k, v)
-            hm.set_kv(layer, k, v)
+    prefill = _prefill_kv(om, hm, cfg, rng) if prefilled else None
     n = min(700, cfg["max_seq_len"] - 10)
     toks = rng.integers(0, cfg["vocab_size"], n)
     checks = {0, 1, 31, 32, 33, 255, 256, 257, 511, 512, 513, 598, 599, 600, 601, n - 1}
@@ -476,8 +502,15 @@ def test_attention_and_o_in_one_launch_matches_oracle(path, shape):
         lo = om.forward(int(tok), pos, mode)
         lh = hm.forward(int(tok), pos, mode)
         if mode == 1:
-            assert npref.rel_l2(lh, lo) < 1e-4, pos
-    _check_kv(om, hm, cfg["n_layers"])
+            # fp32 summation order alone gives ~1e-6; at the first positions the attention output is
+            # one or a few fp16 V entries themselves, and a single entry whose fp32 value rounds to
+            # the neighbouring fp16 on one side (an ulp, ~1e-3 of it) moves these logits by up to
+            # ~1e-4 (the caches are checked entry by entry below)
+            assert npref.rel_l2(lh, lo) < 1e-3, pos
+    if prefilled:
+        _check_kv_prefilled(om, hm, cfg, prefill, sorted(checks))
+    else:
+        _check_kv(om, hm, cfg["n_layers"])
     hm.close()
 
 
@@ -500,23 +533,17 @@ def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
     cfg = SPLIT_O_SHAPES[shape]
     t = np_tensors(cfg, seed=61, std=0.02)
     om, hm = _models(cfg, t, path)
-    hm.set_option("slice_o", 0)  # the merge + O launch itself (the one-launch slices are tested below)
-    rng = np.random.default_rng(62)
-    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-    for layer in range(cfg["n_layers"]):
-        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
-        om.set_kv(layer, k, v)
-        hm.set_kv(layer, k, v)
+    prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(62))
     msl = cfg["max_seq_len"]
     tok = 3
-    for pos in (700, 701, 1023, 1024, 1536, 1537, 2047, 3216, msl - 1, msl, msl + 1, msl + 5):
-        if pos > msl + 5:
-            continue
+    ran = [pos for pos in (700, 701, 1023, 1024, 1536, 1537, 2047, 3216, msl - 1, msl, msl + 1, msl + 5)
+           if pos <= msl + 5]
+    for pos in ran:
         lo = om.forward(tok, pos)
         lh = hm.forward(tok, pos)
         assert npref.rel_l2(lh, lo) < 1e-4, pos
         tok = O.argmax(lo)
+    _check_kv_prefilled(om, hm, cfg, prefill, ran)
     hm.close()
 
 
@@ -530,7 +557,6 @@ def test_attention_and_o_in_one_launch_is_bit_reproducible():
     runs = []
     for ao in (1, 1, 0):
         with hip().HipModel(cfg, t) as m:
-            m.set_option("qao", 0)
             m.set_option("attn_o", ao)
             rng = np.random.default_rng(60)
             out = [m.forward(int(tok), pos, 1) for pos, tok in enumerate(rng.integers(0, cfg["vocab_size"], 24))]
@@ -542,65 +568,63 @@ def test_attention_and_o_in_one_launch_is_bit_reproducible():
     assert npref.rel_l2(la, ls) < 1e-5
 
 
-@pytest.mark.parametrize("path", ["graph", "direct"])
-def test_qkv_attention_and_o_in_one_launch_matches_oracle(path):
-    # QKV, attention and O in one launch at the Mistral shape: the workgroups of a kv head run on one
-    # XCD and hand q and this position's K/V to each other through its L2, then each repeats the kv
-    # head's attention over four waves before combining its Wo rows. Positions with one to six
-    # 32-key tiles per wave, the first (embedding residual) and second layer, against the oracle on
-    # a cache pre-filled from the host; qao = 2 fails unless this GPU's placement allows the launch.
-    cfg = ATTN_O_SHAPES["mistral"]
-    t = np_tensors(cfg, seed=71, std=0.02)
-    om, hm = _models(cfg, t, path)
-    require_launch(hm, "qao")
-    rng = np.random.default_rng(72)
+@pytest.mark.parametrize("variant", ["attn_o", "split_o"])
+def test_out_of_range_partials_reach_x_as_the_reference_gives_them(variant):
+    # The O launches (attention + O, and the slice merge + O) combine the kv heads' partial products
+    # in integer words; a partial outside their range (|p| >= 2^20 - 1, inf, NaN) goes through an fp32
+    # side sum instead of being clamped. Three caches, against the oracle's fp32 O projection
+    # (reference src/infer.cpp:218-250, 339-344):
+    #   - a Wo row of 60000s over positive V: that row's partials are ~6e7, x's row becomes ~1e8, and
+    #     the logits still match to fp32 rounding;
+    #   - an inf V entry: the attention output and everything after it are non-finite on both sides;
+    #   - a NaN V entry: the same.
+    cfg = dict(TINY, n_layers=1, max_seq_len=64)
+    t = np_tensors(cfg, seed=83, std=0.02)
+    wo = t["model.layers.0.attn.wo.weight"].copy()
+    wo[7] = np.float16(60000.0).view(np.uint16)
+    t["model.layers.0.attn.wo.weight"] = wo
+    rng = np.random.default_rng(84)
     n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-    for layer in range(cfg["n_layers"]):
-        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
-        om.set_kv(layer, k, v)
-        hm.set_kv(layer, k, v)
-    tok = 5
-    for pos in (0, 1, 2, 31, 32, 33, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 640, 699):
-        mode = 0 if pos in (1, 128) else 1
-        lo = om.forward(tok, pos, mode)
-        lh = hm.forward(tok, pos, mode)
-        if mode == 1:
-            assert npref.rel_l2(lh, lo) < 1e-4, pos
-        tok = O.argmax(lo) if mode == 1 else tok + 1
-    # the written entries within fp16 rounding of the oracle's (on a pre-filled cache a near-zero
-    # entry may round to zero on one side only, so no zero-pattern check here)
-    for layer in range(cfg["n_layers"]):
-        for a, b in zip(hm.kv(layer), om.kv(layer)):
-            fa, fb = h2f(a), h2f(b)
-            assert np.max(np.abs(fa - fb)) <= 2e-3 * np.max(np.abs(fb))
-            assert npref.rel_l2(fa, fb) < 1e-3
+    k = rng.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
+    v_pos = (np.abs(rng.standard_normal(n, dtype=np.float32)) * 10).astype(np.float16).view(np.uint16)
+    v_inf, v_nan = v_pos.copy(), v_pos.copy()
+    v_inf[3 * cfg["max_seq_len"] + 2] = 0x7C00  # kv head 0, dim 3, position 2: +inf
+    v_nan[(cfg["head_dim"] + 5) * cfg["max_seq_len"] + 1] = 0x7E00  # kv head 1, dim 5, position 1: NaN
+    for v, finite in ((v_pos, True), (v_inf, False), (v_nan, False)):
+        om, hm = _models(cfg, t, "graph")
+        if variant == "split_o":  # the split-KV attention and the merge + O launch at any length
+            hm.set_option("attn_o_max", 0)
+            hm.set_option("attn_splits", 24)  # the merge + O launch takes at most 32 slices per kv head
+        om.set_kv(0, k, v)
+        hm.set_kv(0, k, v)
+        assert hm.step_plan(5)[0] == (hip().STEP_ATTN_O if variant == "attn_o" else hip().STEP_SPLIT_O)
+        # the residual stream after the layer: a hydrate step (the oracle normalises x in place only
+        # when it goes on to the logits, src/infer.cpp:501-509), then the logits of the same step
+        om.forward(9, 5, 0)
+        hm.forward(9, 5, 0)
+        xh, xo = hm.debug_read(0, cfg["dim"]), om.x()
+        lo = om.forward(9, 5)
+        lh = hm.forward(9, 5)
+        if finite:
+            assert abs(float(xo[7])) > 1e7 and abs(float(xh[7]) - float(xo[7])) <= 1e-5 * abs(float(xo[7]))
+            assert npref.rel_l2(xh, xo) < 1e-5
+            assert np.all(np.isfinite(lh)) and npref.rel_l2(lh, lo) < 1e-4
+        else:
+            assert not np.any(np.isfinite(xo)) and not np.any(np.isfinite(xh))
+            assert not np.any(np.isfinite(lo)) and not np.any(np.isfinite(lh))
+        hm.close()
+    # the side sums are cleared: a finite step after the non-finite ones matches again
+    om, hm = _models(cfg, t, "graph")
+    if variant == "split_o":
+        hm.set_option("attn_o_max", 0)
+        hm.set_option("attn_splits", 24)
+    for v in (v_nan, v_pos):
+        om.set_kv(0, k, v)
+        hm.set_kv(0, k, v)
+        lo = om.forward(9, 5)
+        lh = hm.forward(9, 5)
+    assert np.all(np.isfinite(lh)) and npref.rel_l2(lh, lo) < 1e-4
     hm.close()
-
-
-def test_qkv_attention_and_o_in_one_launch_is_bit_reproducible():
-    # The one-launch step twice (bit for bit: the row words make x independent of arrival order),
-    # against the attention + O launch after a separate QKV launch (fp32 noise, growing along the
-    # 40 positions through fp16 cache roundings: the RMSNorm sum and the attention's merge run over
-    # eight waves in a different order).
-    cfg = ATTN_O_SHAPES["mistral"]
-    t = np_tensors(cfg, seed=73, std=0.02)
-    runs = []
-    for qao in (2, 2, 0):
-        with hip().HipModel(cfg, t) as m:
-            if qao == 2:
-                require_launch(m, "qao")
-            else:
-                m.set_option("qao", qao)
-            rng = np.random.default_rng(74)
-            toks = rng.integers(0, cfg["vocab_size"], 40)
-            out = [m.forward(int(tok), pos, 1) for pos, tok in enumerate(toks)]
-            runs.append((np.stack(out), [m.kv(layer) for layer in range(cfg["n_layers"])]))
-    (la, kva), (lb, kvb), (ls, kvs) = runs
-    assert np.array_equal(la, lb)
-    for (ka, va), (kb, vb) in zip(kva, kvb):
-        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
-    assert npref.rel_l2(la, ls) < 1e-4
 
 
 def test_slice_merge_in_the_o_launch_is_bit_reproducible():
@@ -611,69 +635,11 @@ def test_slice_merge_in_the_o_launch_is_bit_reproducible():
     outs = []
     for so in (1, 1, 0):
         with hip().HipModel(cfg, t) as m:
-            m.set_option("slice_o", 0)
             m.set_option("split_o", so)
             m.kv_fill_normal(3000, 64)
             outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
     assert np.array_equal(outs[0], outs[1])
     assert npref.rel_l2(outs[0], outs[2]) < 1e-5
-
-
-SLICE_O_SHAPES = {
-    "mistral": SPLIT_O_SHAPES["mistral"],
-    "hd64_g4_kv8": dict(TINY, dim=2048, head_dim=64, n_heads=32, n_kv_heads=8, rotary_dim=64, n_layers=2,
-                        max_seq_len=2048),
-}
-
-
-@pytest.mark.parametrize("path", ["graph", "direct"])
-@pytest.mark.parametrize("shape", list(SLICE_O_SHAPES))
-def test_attention_slices_and_o_in_one_launch_matches_oracle(path, shape):
-    # Beyond 700 keys with one kv head per XCD, the O launch's own workgroups take the split-KV
-    # slices (one per workgroup of the kv head), hand the partials to each other through the
-    # XCD's L2 and merge them before the Wo rows: positions from one 32-key slice per workgroup to
-    # the end of the context, then past it (sink mode falls back to the separate attention launch
-    # and the merge + O launch), against the oracle on a cache pre-filled from the host. slice_o = 2
-    # fails unless the launch is available on this GPU.
-    cfg = SLICE_O_SHAPES[shape]
-    t = np_tensors(cfg, seed=75, std=0.02)
-    om, hm = _models(cfg, t, path)
-    require_launch(hm, "slice_o")
-    rng = np.random.default_rng(76)
-    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-    for layer in range(cfg["n_layers"]):
-        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
-        om.set_kv(layer, k, v)
-        hm.set_kv(layer, k, v)
-    msl = cfg["max_seq_len"]
-    tok = 3
-    for pos in (700, 701, 1023, 1024, 1025, 2047, 3216, 4000, msl - 2, msl - 1, msl, msl + 1):
-        if pos > msl + 1:
-            continue
-        lo = om.forward(tok, pos)
-        lh = hm.forward(tok, pos)
-        assert npref.rel_l2(lh, lo) < 1e-4, pos
-        tok = O.argmax(lo)
-    hm.close()
-
-
-def test_attention_slices_and_o_in_one_launch_is_bit_reproducible():
-    # Twice bit for bit (the partials are merged in slice order and the rows meet in integer
-    # words), and within fp32 noise of the separate split-KV attention launch + merge + O launch.
-    cfg = SPLIT_O_SHAPES["mistral"]
-    t = np_tensors(cfg, seed=77, std=0.02)
-    outs = []
-    for so in (2, 2, 0):
-        with hip().HipModel(cfg, t) as m:
-            if so == 2:
-                require_launch(m, "slice_o")
-            else:
-                m.set_option("slice_o", so)
-            m.kv_fill_normal(3000, 64)
-            outs.append(np.stack([m.forward(7 + i, 3000 + i, 1) for i in range(6)]))
-    assert np.array_equal(outs[0], outs[1])
-    assert npref.rel_l2(outs[0], outs[2]) < 1e-4
 
 
 @pytest.mark.parametrize("path", ["graph", "direct"])
@@ -684,19 +650,62 @@ def test_mfma_attention_slice_rule_across_lengths(path):
     cfg = dict(MICRO, dim=128, head_dim=32, n_heads=4, n_kv_heads=1, rotary_dim=32, max_seq_len=5248)
     t = np_tensors(cfg, seed=44, std=0.1)
     om, hm = _models(cfg, t, path)
-    rng = np.random.default_rng(45)
-    n = cfg["n_kv_heads"] * cfg["head_dim"] * cfg["max_seq_len"]
-    for layer in range(cfg["n_layers"]):
-        k = (rng.standard_normal(n) * 0.5).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal(n).astype(np.float16).view(np.uint16)
-        om.set_kv(layer, k, v)
-        hm.set_kv(layer, k, v)
+    prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(45))
     tok = 3
-    for pos in (318, 320, 321, 700, 1023, 1024, 1536, 1537, 2400, 4095, 4096, 4500, 5119, 5120, 5121):
+    ran = (318, 320, 321, 700, 1023, 1024, 1536, 1537, 2400, 4095, 4096, 4500, 5119, 5120, 5121)
+    for pos in ran:
         lo = om.forward(tok, pos)
         lh = hm.forward(tok, pos)
         assert npref.rel_l2(lh, lo) < 1e-4, pos
         tok = O.argmax(lo)
+    _check_kv_prefilled(om, hm, cfg, prefill, ran)
+    hm.close()
+
+
+def test_attention_heavy_decode_step_at_16k_keys_matches_oracle():
+    # The attention-heavy workload's own decode step on a two-layer Mistral-shape model with a
+    # 16448-token context: every layer's K/V pre-filled with fp16 N(0, 1) draws on both sides
+    # (reference src/infer.cpp:300-305 layout), then steps at positions 16384 .. 16449 on the
+    # default options, greedy as in the workload. Each runs the split-KV attention with its slices
+    # stored (24 slices of 704 keys on a 256-CU part) and merged by the O launch (merge_o_kernel);
+    # the last two positions lie past the context (sink mode: the two sink keys re-rotated, ring
+    # slots 2 and 3).
+    # Two oracles: one rotating with the device's rotary frequencies (the correctly rounded fp32
+    # 1 / powf(theta, j / rotary_dim)), against which the logits agree to 1e-4 and the caches entry
+    # by entry; and the reference's own expression as its -ffast-math build rounds it (25 of the 64
+    # frequencies an ulp apart), whose angles at position 16384 differ by up to ~1e-3 rad in the
+    # fast pairs: that one within 2e-3 (contract 1e-2) (src/infer.cpp:202-250, 327-336).
+    cfg = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32, n_kv_heads=8,
+               max_seq_len=16448, rotary_dim=128)
+    t = np_tensors(cfg, seed=81, std=0.02)
+    om, hm = _models(cfg, t, "graph")
+    om.set_rope_freqs(hm.debug_read(5, cfg["head_dim"] // 2))
+    ref = O.OracleModel(cfg, t)  # the reference's frequency expression
+    prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(16384), k_scale=1.0)
+    for layer, (k, v) in enumerate(prefill):
+        ref.set_kv(layer, k, v)
+    H = hip()
+    positions = list(range(16384, 16450))
+    tok = int(np.random.default_rng(16385).integers(0, cfg["vocab_size"]))
+    worst = worst_ref = 0.0
+    for pos in positions:
+        variant, slices, slice_len = hm.step_plan(pos)
+        assert variant == H.STEP_SPLIT_O and 2 <= slices <= 32, (pos, variant, slices, slice_len)
+        assert slices * slice_len >= min(pos + 1, cfg["max_seq_len"]) > (slices - 1) * slice_len
+        lo = om.forward(tok, pos)
+        lh = hm.forward(tok, pos)
+        lr = ref.forward(tok, pos)
+        rel, rel_ref = npref.rel_l2(lh, lo), npref.rel_l2(lh, lr)
+        worst, worst_ref = max(worst, rel), max(worst_ref, rel_ref)
+        assert rel < 1e-4, (pos, rel)
+        assert rel_ref < 2e-3, (pos, rel_ref)
+        tok = O.argmax(lo)
+        top2 = np.sort(lo)[-2:]
+        if top2[1] - top2[0] > 1e-3 * np.max(np.abs(lo)):  # a clear maximum: the same greedy token
+            assert int(np.argmax(lh)) == tok, pos
+    print(f"16K-key steps: plan {hm.step_plan(positions[0])}, worst logits rel-L2 {worst:.2e} "
+          f"(reference frequency expression: {worst_ref:.2e})")
+    _check_kv_prefilled(om, hm, cfg, prefill, positions)
     hm.close()
 
 

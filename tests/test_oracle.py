@@ -290,3 +290,26 @@ def test_forward_rejects_bad_token():
     om = O.OracleModel(cfg, np_tensors(cfg, seed=15))
     with pytest.raises(ValueError):
         om.forward(cfg["vocab_size"], 0)
+
+
+def test_rope_frequency_hook_zero_frequencies_equal_no_rotation():
+    # oracle_set_rope_freqs (the test hook that lets the oracle rotate with a given frequency table):
+    # all-zero frequencies make every rotation the identity, as rotary_dim 0 does through the
+    # reference's own expression (src/infer.cpp:205: freq = 0 for j >= rotary_dim); setting no table
+    # restores the reference's expression.
+    from tests.util import MICRO, np_tensors
+    cfg = dict(MICRO)
+    t = np_tensors(cfg, seed=91)
+    m = O.OracleModel(cfg, t)
+    m.set_rope_freqs(np.zeros(cfg["head_dim"] // 2, np.float32))
+    norot = O.OracleModel(dict(cfg, rotary_dim=0), t)
+    plain = O.OracleModel(cfg, t)
+    for pos, tok in enumerate((3, 77, 5, 300)):
+        assert np.array_equal(m.forward(tok, pos), norot.forward(tok, pos))
+    m2 = O.OracleModel(cfg, t)
+    m2.set_rope_freqs(np.zeros(cfg["head_dim"] // 2, np.float32))
+    m2.set_rope_freqs(None)
+    for pos, tok in enumerate((3, 77, 5, 300)):
+        assert np.array_equal(m2.forward(tok, pos), plain.forward(tok, pos))
+    with pytest.raises(ValueError):
+        m.set_rope_freqs(np.zeros(3, np.float32))

@@ -23,23 +23,17 @@ def hip():
     return H
 
 
-# (LDS stages, k-step, workgroup rows, large-tile k-step schedule interleaved); 0 stages = the
-# register-staged kernel
-GEMM_VARIANTS = [(-1, 32, 128, -1), (4, 32, 128, -1), (2, 64, 128, -1), (3, 64, 128, -1), (2, 64, 256, -1),
-                 (3, 64, 256, -1), (1, 64, 256, 1), (1, 32, 256, 1), (1, 64, 256, 2), (1, 32, 256, 2),
-                 (1, 64, 256, 0), (1, 32, 256, 0), (0, 32, 128, -1),
-                 (5, 64, 256, -1), (6, 64, 256, -1)]
-# -1: chosen per shape; 1: the 256 x 256 kernel; 5: the same, stream-K; 6: the eight-wave 256 x 256
-# kernel (K % 64 == 0; otherwise it falls back to the 32-deep four-wave one)
+# (LDS stages, k-step, workgroup rows): -1 = chosen per shape; 2..4 = the LDS pipeline; 6 = the
+# eight-wave 256 x 256 kernel (K % 64 == 0; otherwise it falls back to the 32-deep LDS pipeline)
+GEMM_VARIANTS = [(-1, 32, 128), (4, 32, 128), (2, 64, 128), (3, 64, 128), (2, 64, 256), (3, 64, 256),
+                 (6, 64, 256)]
 
 
-@pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}i{i}" for s, k, m, i in GEMM_VARIANTS])
+@pytest.fixture(params=GEMM_VARIANTS, ids=[f"s{s}k{k}m{m}" for s, k, m in GEMM_VARIANTS])
 def gemm_variant(request):
-    hip().set_gemm_stages(*request.param[:3])
-    hip().set_gemm_interleave(request.param[3])
+    hip().set_gemm_stages(*request.param)
     yield request.param
     hip().set_gemm_stages(-1)
-    hip().set_gemm_interleave(-1)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 32), (200, 384, 256), (37, 64, 96), (300, 256, 4096),
@@ -292,15 +286,11 @@ def test_gemm_eight_wave_split_round(M, N, K, mode):
         assert npref.rel_l2(got.astype(np.float64), whole.astype(np.float64)) < 1e-6
 
 
-@pytest.mark.parametrize("variant", ["auto", "stream_k"])
 @pytest.mark.parametrize("mode,N,K", [(2, 14336, 4096), (1, 4096, 14336), (0, 6144, 4096), (1, 4096, 4096)])
-def test_gemm_production_shapes_at_3200_rows(mode, N, K, variant):
-    # The Mistral-7B prefill GEMMs at M = 3200 with the auto-selected variants (and forced stream-K
-    # large tiles), against a float64 product on sampled rows and columns (tile edges of both tile
-    # sizes included).
+def test_gemm_production_shapes_at_3200_rows(mode, N, K):
+    # The Mistral-7B prefill GEMMs at M = 3200 with the auto-selected variants, against a float64
+    # product on sampled rows and columns (tile edges of both tile sizes included).
     H = hip()
-    if variant == "stream_k":
-        H.set_gemm_stages(5, 64, 256)
     M = 3200
     rng = np.random.default_rng(N + K + mode)
     a = f16(rng.standard_normal((M, K), dtype=np.float32))

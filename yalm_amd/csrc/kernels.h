@@ -250,9 +250,6 @@ struct MatvecArgs {
   // row-loop statistics for the lm_head: running (max, index) of the outputs, tie rule of
   // src/sampler.cpp:27-38, kept per wave (argmax fused into the last matvec)
   int track_max;
-  // QKV epilogue: 1 = q and the K/V of this position are written through to memory (agent-scope
-  // stores), for a later workgroup of the same launch that reads them (the fused attention)
-  int coh_store;
 };
 
 // Loads of one row segment for this lane: chunk c = lane + 64*u, u < KC (KC = K/512 when > 0).
@@ -344,7 +341,7 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
     }
     if (!store) return;
     if (i < a.q_dim) {
-      if (COH || a.coh_store) {
+      if (COH) {
         store_shared(a.out + i, v0);
         store_shared(a.out + i + 1, v1);
       } else {
@@ -361,16 +358,7 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
       const uint16_t h1 = __builtin_bit_cast(uint16_t, (f16)v1);
       if constexpr (COH)  // the same launch's attention reads this position from the side buffer
         store_shared_u32(a.kvcur + (is_k ? 0 : a.kv_dim / 2) + ik / 2, (uint32_t)h0 | ((uint32_t)h1 << 16));
-      if (a.coh_store) {  // dims j, j + 1 (j even) are adjacent in K's 16-dim chunk: one word
-        if (is_k)
-          store_shared_u32(reinterpret_cast<uint32_t*>(a.kcache + head + k_cache_idx(j, ps.kv_pos, a.msl)),
-                           (uint32_t)h0 | ((uint32_t)h1 << 16));
-        else {
-          __hip_atomic_store(a.vcache + head + (long)j * a.msl + ps.kv_pos, h0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(a.vcache + head + (long)(j + 1) * a.msl + ps.kv_pos, h1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else if (is_k) {
+      if (is_k) {
         a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = h0;
         a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = h1;
       } else {
@@ -909,25 +897,6 @@ __global__ void rope_table_kernel(const float* inv_freq, float* rope_cs, int hal
 // In sink mode (pos >= msl) slice 0 first re-rotates the two sink keys by one position
 // (reference src/infer.cpp:307-325).
 // ------------------------------------------------------------------------------------------
-// Weight prefetch riding on the attention launch. Attention waits on latency and leaves HBM idle,
-// so extra workgroups read the weights the next kernels will stream (O, then the first rows of
-// W1/W3) and leave them in the caches. Range r is split into chunks of `chunk` 16-byte units; worker
-// j reads chunks j, j + blocks, ... so that with `blocks` and the attention grid multiples of 8 a
-// chunk lands on the same XCD (and L2) as the consumer workgroup with the chunk's index.
-// The loaded words are folded into one value per thread that is stored to `sink` only if it equals
-// `magic` (keeps the loads alive; in practice never written).
-struct PrefetchRange {
-  const u32x4* p = nullptr;
-  long units = 0;  // 16-byte units
-  int chunk = 1;   // 16-byte units per chunk
-};
-struct AttnPrefetch {
-  PrefetchRange r[3];
-  int blocks = 0;  // worker workgroups (0: no prefetch)
-  unsigned magic = 0;
-  unsigned* sink = nullptr;  // one word per thread of the launch's workgroups
-};
-
 struct AttnArgs {
   const float* q;        // [nh][hd]
   uint16_t* kcache;      // layer base
@@ -941,7 +910,6 @@ struct AttnArgs {
                           // merged by the next launch (merge_o_kernel) instead of the last slice
   const float* inv_freq;  // [head_dim / 2] rotary frequencies (sink re-rotation by one position)
   const StepParams* params;
-  AttnPrefetch pf;
 };
 
 constexpr int kMaxGroup = 8;
@@ -1396,38 +1364,9 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
   attn_merge_slices<HD, G, NT, COH>(a, g, active, tid, sm.mrg, &sm.red[0][0][0], sm.last_flag);
 }
 
-// One prefetch worker of NT threads: 16 loads of 16 bytes per thread in flight per round.
-template <int NT>
-__device__ __forceinline__ void prefetch_worker(const AttnPrefetch& pf, int j) {
-  constexpr int U = 16;
-  unsigned fold = 0;
-#pragma unroll 1
-  for (int ri = 0; ri < 3; ++ri) {
-    const PrefetchRange r = pf.r[ri];
-    const long nch = (r.units + r.chunk - 1) / r.chunk;
-    for (long c = j; c < nch; c += pf.blocks) {
-      const long end = min((c + 1) * r.chunk, r.units);
-      for (long i0 = c * r.chunk + threadIdx.x; i0 < end; i0 += (long)NT * U) {
-        u32x4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = r.p[min(i0 + (long)u * NT, end - 1)];
-#pragma unroll
-        for (int u = 0; u < U; ++u) fold ^= v[u][0] ^ v[u][3];
-      }
-    }
-  }
-  if (fold == pf.magic) pf.sink[threadIdx.x] = fold;
-}
-
-// Split-KV attention as its own launch: grid (n_kv_heads, nsplit + prefetch rows) of 256-thread
-// workgroups; the rows beyond nsplit are prefetch workers.
+// Split-KV attention as its own launch: grid (n_kv_heads, nsplit) of 256-thread workgroups.
 template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
-  if ((int)blockIdx.y >= a.nsplit) {
-    const int j = ((int)blockIdx.y - a.nsplit) * (int)gridDim.x + (int)blockIdx.x;
-    if (j < a.pf.blocks) prefetch_worker<kBlock>(a.pf, j);
-    return;
-  }
   __shared__ AttnSmem<HD, G, kBlock> sm;
   attn_run<HD, G, kBlock, false, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
 }

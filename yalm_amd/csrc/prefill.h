@@ -60,12 +60,10 @@ __device__ __forceinline__ float max16(const f32x16& s) {
 
 // ------------------------------------------------------------------------------------------
 // GEMM C[M][N] = A[M][K] . B[N][K]^T, A and B fp16 row-major (both K-contiguous, as activations
-// and .yalm weights are). Block tile 128 x 128 x 32, four waves in 2 x 2, each a 64 x 64 tile of
-// four 32x32 MFMA tiles; A and B tiles double-buffered through LDS (rows padded to 40 halves so
-// the fragment reads are conflict-free). Rows past M and columns past N are clamped on load and
-// masked on store. K must be a multiple of 32.
-// Epilogues: STORE C = acc; RESID C += acc; SWIGLU: the block's 128 B rows are 64 rows of W1 and
-// the same 64 rows of W3, interleaved by 32, so each lane holds act(w1) and w3 of one output;
+// and .yalm weights are), on 32x32x16 MFMA tiles. Rows past M and columns past N are clamped on
+// load and masked on store. K must be a multiple of 32.
+// Epilogues: STORE C = acc; RESID C += acc; SWIGLU: a tile's B rows are rows of W1 and the same
+// rows of W3, interleaved by 32, so each lane holds act(w1) and w3 of one output;
 // H[m][j] = fp16(act(w1) * w3) with N counting output columns.
 // ------------------------------------------------------------------------------------------
 enum GemmEpi : int { kGemmStore = 0, kGemmResid = 1, kGemmSwiGLU = 2 };
@@ -97,123 +95,17 @@ struct GemmArgs {
   float* P;
   long p_floats;  // capacity of P
   int ksplit;     // 0 or 1: no split
-  // Stream-K large tiles: one flag per workgroup slot (kSkFlagStride words apart, zeroed once) and
-  // the word a timed-out wait sets.
+  // Split last round of the eight-wave kernel: one flag per partial slot (kSkFlagStride words
+  // apart, zeroed once) and the word a timed-out wait sets.
   unsigned* sk_flags;
   unsigned* abort_flag;
-  int interleave;  // large tiles: the interleaved k-step schedule (BigTile::mainloop<true>)
 };
 
-constexpr int kGBM = 128, kGBN = 128, kGBK = 32, kGLds = kGBK + 8;
-
-// At most 128 VGPRs (four waves per SIMD) so four workgroups fit on a CU: 1024 slots on the GPU,
-// which holds the 800 tiles of a 3200 x 4096 output in one round (with 768 slots the last 32
-// tiles would run as a second round of full length).
-template <int EPI>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) gemm_nt_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kGBM * kGLds];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGBN * kGLds];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kGBM;
-  // SwiGLU: this block's 64 output columns j0..j0+63
-  const int n0 = EPI == kGemmSwiGLU ? blockIdx.x * (kGBN / 2) : blockIdx.x * kGBN;
-
-  // global -> LDS: 128 rows x 4 chunks of 8 halves per operand; thread t moves chunks t, t + 256
-  const uint16_t* arow[2];
-  const uint16_t* brow[2];
-  int lofs[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + 256 * i, row = c >> 2, kc = c & 3;
-    lofs[i] = row * kGLds + kc * 8;
-    arow[i] = g.A + (long)min(m0 + row, g.M - 1) * g.lda + kc * 8;
-    if constexpr (EPI == kGemmSwiGLU) {
-      // B tile row r: W1 for (r/32) even, W3 for odd; output column n0 + (r/64)*32 + r%32
-      const int col = n0 + (row >> 6) * 32 + (row & 31);
-      const uint16_t* base = ((row >> 5) & 1) ? g.B3 : g.B;
-      brow[i] = base + (long)min(col, g.N - 1) * g.ldb + kc * 8;
-    } else {
-      brow[i] = g.B + (long)min(n0 + row, g.N - 1) * g.ldb + kc * 8;
-    }
-  }
-  u32x4 ra[2], rb[2];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
-      rb[i] = *reinterpret_cast<const u32x4*>(brow[i] + k0);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<u32x4*>(&As[buf][lofs[i]]) = ra[i];
-      *reinterpret_cast<u32x4*>(&Bs[buf][lofs[i]]) = rb[i];
-    }
-  };
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  const int nk = g.K / kGBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kGBK);
-#pragma unroll
-    for (int ks = 0; ks < kGBK / 16; ++ks) {
-      const int kofs = ks * 16 + 8 * (lane >> 5);
-      u32x4 fa[2], fb[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        fa[t] = *reinterpret_cast<const u32x4*>(&As[buf][(wm * 64 + t * 32 + (lane & 31)) * kGLds + kofs]);
-        fb[t] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wn * 64 + t * 32 + (lane & 31)) * kGLds + kofs]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
-    }
-    if (kt + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 64 + i * 32 + acc_row(r, lane);
-      if (m >= g.M) continue;
-      if constexpr (EPI == kGemmSwiGLU) {
-        const int j = n0 + wn * 32 + (lane & 31);
-        if (j < g.N) {
-          const float a1 = acc[i][0][r], a3 = acc[i][1][r];
-          const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
-          g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-          if (n >= g.N) continue;
-          float* cp = g.C + (long)m * g.ldc + n;
-          if constexpr (EPI == kGemmResid) *cp += acc[i][j][r];
-          else *cp = acc[i][j][r];
-        }
-      }
-    }
-  }
-}
+constexpr int kGBM = 128, kGBN = 128, kGBK = 32;
 
 // ------------------------------------------------------------------------------------------
-// The same GEMM with an S-stage LDS pipeline fed by direct-to-LDS loads (global_load_lds_dwordx4:
+// 128-row tiles (BM 128 with four waves in 2 x 2, or 256 with eight), each wave a 64 x 64 block of
+// four 32x32 MFMA tiles, in an S-stage LDS pipeline fed by direct-to-LDS loads (global_load_lds_dwordx4:
 // lane l of a wave instruction writes 16 bytes at the instruction's LDS address + 16 l). A stage
 // holds one BK-deep k-step of both operands, 128 rows x 2 BK bytes each, with the 16-byte k-chunk
 // c of row r stored at position c ^ ((r / RPW) % CPR) (CPR = BK / 8 chunks per row, RPW = rows per
@@ -221,7 +113,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) g
 // (a 256-byte period), and the swizzle puts the 16 rows of each pass in distinct banks (measured:
 // no LDS bank conflicts). S - 1 k-steps are in flight while one is used; nothing passes through
 // registers on the way to LDS, and each 16-deep slice's fragments are read while the previous
-// slice's MFMAs run. Same tiles, waves and epilogues as gemm_nt_kernel.
+// slice's MFMAs run.
 // ------------------------------------------------------------------------------------------
 // Tile order of the pipelined GEMMs (one-dimensional grid of 8 * ceil(tiles / 8) workgroups).
 // Workgroups are handed to the eight XCDs in turn (workgroup b runs on XCD b % 8), and each XCD
@@ -438,233 +330,15 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs g) {
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Large-tile GEMM: 256 x 256 per workgroup, four waves in 2 x 2 each computing 128 x 128 (4 x 4
-// tiles of 32 x 32; the 256 fp32 accumulators live in the accumulation registers), BK-deep
-// k-steps in an S-stage LDS pipeline (S x BK x 1 KB) filled by direct-to-LDS loads with the same
-// swizzle as gemm_lds_kernel, one workgroup per CU. A wave issues 2 MFMAs per fragment read; the
-// loads are latency-bound, so the pipeline keeps S - 1 stages in flight (measured: with one
-// 64 KB stage in flight the loads alone take 70% of the GEMM's time).
-// SwiGLU: the 256 B rows are 128 rows of W1 and the same 128 rows of W3 interleaved by 32, so a
-// wave's tiles 2q and 2q + 1 hold W1 and W3 of the same 32 output columns.
-// ------------------------------------------------------------------------------------------
 constexpr int kBigM = 256, kBigN = 256;
 
-// One 256 x 256 output tile of the large-tile GEMM, shared by the data-parallel kernel (one tile per
-// workgroup) and the stream-K kernel (ranges of k-steps over tiles).
-template <int EPI, int S, int BK>
-struct BigTile {
-  static constexpr int CPR = BK / 8, RPI = 1024 / (2 * BK), RPW = 256 / (2 * BK);
-  static constexpr int ATILE = kBigM * BK, BTILE = kBigN * BK;
-  static constexpr int IA = kBigM / RPI / 4, IB = kBigN / RPI / 4;  // load instructions per wave per stage
-  static constexpr int LPS = IA + IB;
-  static constexpr int KK = BK / 16;
-  static constexpr int NC = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;  // output columns per tile
-  static constexpr int STAGE = ATILE + BTILE;                        // halves per LDS stage
-  static __device__ __forceinline__ int swz(int r) { return (r / RPW) % CPR; }
-
-  // acc += A[m0 .. m0 + 256) . B[n0 ...]^T over k-steps [kt0, kt1), through the S-stage LDS
-  // pipeline; every wave of the workgroup takes part (the LDS stages are reused afterwards).
-  // tid = threadIdx.x (a persistent caller passes an opaque copy so its per-lane indexing is not
-  // hoisted out of the tile loop and kept live across it).
-  // IL: every k-step issues its copy unconditionally (a stage past the end re-reads the last k-step
-  // into a slot nobody reads) so that the step is one basic block, and the copies and the next
-  // fragments' LDS reads are interleaved with the MFMAs (scheduling groups) instead of bunched
-  // after the barrier.
-  template <int IL = 0>
-  static __device__ __forceinline__ void mainloop(const GemmArgs& g, uint16_t* smem, int m0, int n0, int kt0, int kt1,
-                                                  f32x16 (&acc)[4][4], int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const uint16_t* arow[IA];
-    const uint16_t* brow[IB];
-#pragma unroll
-    for (int j = 0; j < IA; ++j) {
-      const int r = RPI * (wave + 4 * j) + lane / CPR;
-      arow[j] = g.A + (long)min(m0 + r, g.M - 1) * g.lda + 8 * ((lane % CPR) ^ swz(r));
-    }
-#pragma unroll
-    for (int j = 0; j < IB; ++j) {
-      const int r = RPI * (wave + 4 * j) + lane / CPR;
-      const int c = (lane % CPR) ^ swz(r);
-      if constexpr (EPI == kGemmSwiGLU) {
-        const int col = n0 + (r >> 6) * 32 + (r & 31);
-        const uint16_t* base = ((r >> 5) & 1) ? g.B3 : g.B;
-        brow[j] = base + (long)min(col, g.N - 1) * g.ldb + 8 * c;
-      } else {
-        brow[j] = g.B + (long)min(n0 + r, g.N - 1) * g.ldb + 8 * c;
-      }
-    }
-    // the stage's copies j0 .. j1 - 1 (A pieces first, then B)
-    auto issue_part = [&](int kt, int kdata, int j0, int j1) {
-      uint16_t* st = smem + ((kt - kt0) % S) * STAGE;
-      const int k0 = kdata * BK;
-#pragma unroll
-      for (int j = 0; j < IA + IB; ++j) {
-        if (j < j0 || j >= j1) continue;
-        if (j < IA) load_lds16(arow[j] + k0, st + (wave + 4 * j) * 512);
-        else load_lds16(brow[j - IA] + k0, st + ATILE + (wave + 4 * (j - IA)) * 512);
-      }
-    };
-    auto issue = [&](int kt, int kdata) { issue_part(kt, kdata, 0, IA + IB); };
-    auto read_frags = [&](const uint16_t* As, const uint16_t* Bs, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-      const int c = 2 * kk + (lane >> 5);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int ra = wm * 128 + t * 32 + (lane & 31);
-        const int rb = wn * 128 + t * 32 + (lane & 31);
-        fa[t] = *reinterpret_cast<const u32x4*>(As + ra * BK + 8 * (c ^ swz(ra)));
-        fb[t] = *reinterpret_cast<const u32x4*>(Bs + rb * BK + 8 * (c ^ swz(rb)));
-      }
-    };
-#pragma unroll
-    for (int kt = kt0; kt < kt0 + S - 1; ++kt)
-      if (IL != 0 || kt < kt1) issue(kt, min(kt, kt1 - 1));
-    for (int kt = kt0; kt < kt1; ++kt) {
-      // k-step kt has landed once at most S - 2 later stages are outstanding
-      if (IL != 0 || kt + S - 2 < kt1) wait_vmcnt<LPS * (S - 2)>();
-      else wait_vmcnt<0>();
-      __asm__ volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();  // stage kt is in for every wave; stage kt - 1 is no longer read
-      __asm__ volatile("" ::: "memory");
-      const uint16_t* As = smem + ((kt - kt0) % S) * STAGE;
-      const uint16_t* Bs = As + ATILE;
-      u32x4 fa[2][4], fb[2][4];
-      if constexpr (IL == 2) {
-        // fenced phases: phase kk issues the reads of kk + 1 and a quarter of the next stage's
-        // copies, then its 16 MFMAs; the fences keep each phase's reads ahead of its MFMAs, so the
-        // wait before phase kk + 1 finds them done
-        constexpr int VPK = (LPS + KK - 1) / KK;
-        const int kn = min(kt + S - 1, kt1 - 1);
-        read_frags(As, Bs, 0, fa[0], fb[0]);
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-          issue_part(kt + S - 1, kn, kk * VPK, (kk + 1) * VPK);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        continue;
-      }
-      if constexpr (IL == 1) {
-        read_frags(As, Bs, 0, fa[0], fb[0]);
-        __builtin_amdgcn_sched_barrier(0);
-        issue(kt + S - 1, min(kt + S - 1, kt1 - 1));
-      } else {
-        if (kt + S - 1 < kt1) issue(kt + S - 1, kt + S - 1);
-        read_frags(As, Bs, 0, fa[0], fb[0]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        if (kk + 1 < KK) read_frags(As, Bs, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
-      }
-      if constexpr (IL == 1) {
-        // per 16 MFMAs of a kk step: one LDS read of the next step's fragments after every other
-        // MFMA (8), one copy after every fourth (LPS over the k-step)
-        constexpr int VPK = (LPS + KK - 1) / KK;  // copies per kk step
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (kk + 1 < KK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i < VPK) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          }
-      }
-    }
-    if constexpr (IL != 0) wait_vmcnt<0>();  // the copies past the end land before the stages are reused
-    // the next tile's loads reuse the stages: every wave is done reading them
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-  }
-
-  // The epilogue of row block i (32 rows of this wave): v[j] = its four 32 x 32 accumulator tiles.
-  static __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, int m0, int n0, int i, const f32x16 (&v)[4],
-                                                       int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 128 + i * 32 + acc_row(r, lane);
-      if (m >= g.M) continue;
-      if constexpr (EPI == kGemmSwiGLU) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int j = n0 + wn * 64 + q * 32 + (lane & 31);
-          if (j < g.N) {
-            const float a1 = v[2 * q][r], a3 = v[2 * q + 1][r];
-            const float h = g.act == 1 ? silu_fast(a1) : gelu(a1);
-            g.H[(long)m * g.ldh + j] = __builtin_bit_cast(uint16_t, (f16)(h * a3));
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = n0 + wn * 128 + j * 32 + (lane & 31);
-          if (n >= g.N) continue;
-          float* cp = g.C + (long)m * g.ldc + n;
-          if constexpr (EPI == kGemmResid) *cp += v[j][r];
-          else *cp = v[j][r];
-        }
-      }
-    }
-  }
-
-  static __device__ __forceinline__ void epilogue(const GemmArgs& g, int m0, int n0, const f32x16 (&acc)[4][4],
-                                                  int tid) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) epilogue_rows(g, m0, n0, i, acc[i], tid);
-  }
-};
-
-// Large-tile GEMM: 256 x 256 per workgroup, four waves in 2 x 2 each computing 128 x 128 (4 x 4
-// tiles of 32 x 32; the 256 fp32 accumulators live in the accumulation registers), BK-deep
-// k-steps in an S-stage LDS pipeline (S x BK x 1 KB) filled by direct-to-LDS loads with the same
-// swizzle as gemm_lds_kernel, one workgroup per CU. A wave issues 2 MFMAs per fragment read; the
-// loads are latency-bound, so the pipeline keeps S - 1 stages in flight (measured: with one
-// 64 KB stage in flight the loads alone take 70% of the GEMM's time).
-// SwiGLU: the 256 B rows are 128 rows of W1 and the same 128 rows of W3 interleaved by 32, so a
-// wave's tiles 2q and 2q + 1 hold W1 and W3 of the same 32 output columns.
-template <int EPI, int S, int BK>
-__global__ void __launch_bounds__(256) gemm_big_kernel(GemmArgs g) {
-  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
-  using T = BigTile<EPI, S, BK>;
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * T::STAGE];
-  int tm, tn;
-  if (!gemm_tile((g.M + kBigM - 1) / kBigM, (g.N + T::NC - 1) / T::NC, tm, tn)) return;
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  if (g.interleave == 2)
-    T::template mainloop<2>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
-  else if (g.interleave)
-    T::template mainloop<1>(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
-  else
-    T::mainloop(g, smem, tm * kBigM, tn * T::NC, 0, g.K / BK, acc, threadIdx.x);
-  T::epilogue(g, tm * kBigM, tn * T::NC, acc, threadIdx.x);
-}
-
-// Partial slots and flags of the split large-tile GEMMs (stream-K and the eight-wave kernel's split
-// round): a slot holds one 256 x 256 fp32 tile, flags are kSkFlagStride words apart.
+// Partial slots and flags of the eight-wave kernel's split round: a slot holds one 256 x 256 fp32
+// tile, flags are kSkFlagStride words apart.
 constexpr int kSkSlotFloats = kBigM * kBigN;
 constexpr int kSkFlagStride = 64;
 
 // ------------------------------------------------------------------------------------------
-// Eight-wave large-tile GEMM ("ping-pong"): 256 x 256 per workgroup as in gemm_big_kernel, but two
-// waves per SIMD. Each wave owns a 128 x 64 block of the tile (2 x 4 layout, accumulators 4 x 2
+// Eight-wave large-tile GEMM ("ping-pong"): 256 x 256 per workgroup, two waves per SIMD. Each wave owns a 128 x 64 block of the tile (2 x 4 layout, accumulators 4 x 2
 // tiles of 32 x 32) and alternates a memory phase (the LDS fragment reads of its next 32-deep
 // half-step, then copies) with a compute phase (that half-step's 16 MFMAs on registers only). Waves
 // 0-3 and 4-7 form two groups; group 1 runs one phase behind group 0 and a workgroup barrier ends
@@ -683,8 +357,8 @@ constexpr int kSkFlagStride = 64;
 // last memory phase), before the barrier after which group 0 reads stage s + 1.
 // Copies past the last k-step re-read it into a slot that is not read again, so every phase has
 // the same shape.
-// SwiGLU: the B rows of a tile are W1 and W3 interleaved by 32 as in gemm_big_kernel, so a wave's
-// two column tiles are W1 and W3 of the same 32 outputs.
+// SwiGLU: the B rows of a tile are 128 rows of W1 and the same 128 rows of W3 interleaved by 32, so
+// a wave's two column tiles are W1 and W3 of the same 32 outputs.
 // ------------------------------------------------------------------------------------------
 template <int EPI>
 struct PPTile {
@@ -947,111 +621,6 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmArgs g, PPSplit sp, un
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Stream-K variant of the large-tile GEMM: one workgroup per CU, and the grid's k-steps (tiles x
-// K / BK, tiles M-fastest) dealt out evenly as contiguous ranges, so no CU idles when the tile
-// count is not a multiple of the CU count (a 3200 x 4096 output has 208 tiles of 256 x 256). The
-// ranges of XCD x (workgroups b with b % 8 == x) are contiguous, so each XCD walks its own run of
-// tiles and reuses the weight panels from its L2.
-// A workgroup walks the tiles of its range from the last to the first. When its range ends inside
-// a tile, that part comes first and is stored as an fp32 partial (written through to memory, in
-// the accumulators' own lane order) to the workgroup's slot, then the slot's flag is set to this
-// launch's epoch. The workgroup that holds a tile's last k-step handles that tile last: it adds the
-// partials of the earlier ranges (in range order: deterministic) once their flags show the epoch,
-// and applies the epilogue. Waits are bounded: a time-out sets *abort_flag (the host reports an
-// error) and the tile's result is then wrong, never hung.
-// P: gridDim.x slots of 65536 floats; flags: gridDim.x words, 64 apart, below the epoch on entry.
-// ------------------------------------------------------------------------------------------
-
-template <int EPI, int S, int BK>
-__global__ void __launch_bounds__(256) gemm_sk_kernel(GemmArgs g, unsigned* flags, unsigned epoch,
-                                                      unsigned* abort_flag) {
-  static_assert(S >= 2 && (BK == 32 || BK == 64), "stages and k-step");
-  using T = BigTile<EPI, S, BK>;
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * T::STAGE];
-  const int mt = (g.M + kBigM - 1) / kBigM, nt = (g.N + T::NC - 1) / T::NC;
-  const int KI = g.K / BK;
-  const long total = (long)mt * nt * KI;
-  const int P = gridDim.x;
-  // range index: XCD-contiguous (workgroup b runs on XCD b % 8)
-  const int per_x = P / 8;
-  const int ri = (P % 8 == 0) ? ((int)blockIdx.x % 8) * per_x + (int)blockIdx.x / 8 : (int)blockIdx.x;
-  auto range_begin = [&](int r) { return (long)r * total / P; };
-  const long b = range_begin(ri), e = range_begin(ri + 1);
-  if (b >= e) return;
-  // accumulator tile (i, j) of this thread <-> slot floats ((wave * 16 + 4 i + j) * 64 + lane) * 16 + [0, 16):
-  // 64 contiguous bytes per lane, moved as four 16-byte agent-coherent accesses
-
-  long it = e;
-  while (it > b) {
-    // the last tile of [b, it): its k-steps [k0, k1) within this range
-    const long t = (it - 1) / KI;
-    const long tile_start = t * KI;
-    const int k0 = (int)(max(b, tile_start) - tile_start), k1 = (int)(it - tile_start);
-    it = max(b, tile_start);
-    const int m0 = (int)(t % mt) * kBigM, n0 = (int)(t / mt) * T::NC;
-    // per-lane indexing is recomputed for every tile rather than held across the loop
-    int tid = threadIdx.x;
-    __asm__ volatile("" : "+v"(tid));
-    const int lane = tid & 63, wave = tid >> 6;
-    auto slot_byte = [&](int i, int j) { return (((wave * 16 + 4 * i + j) * 64 + lane) * 16) * (int)sizeof(float); };
-    f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-    if (k0 > 0 && k1 == KI) {
-      // this workgroup finishes a tile that earlier ranges started: their partials seed the
-      // accumulators, added in range order. The tile is the last one of this reverse walk and the
-      // first of theirs, so the partials are normally published long before.
-      int first = ri;  // the first range that reaches into this tile
-      while (first > 0 && range_begin(first) > tile_start) --first;
-      for (int q = first; q < ri; ++q) {
-        if (range_begin(q) == range_begin(q + 1)) continue;  // an empty range (fewer k-steps than workgroups)
-        wait_flag(flags + (long)q * kSkFlagStride, epoch, abort_flag);
-        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-            g.P + (long)q * kSkSlotFloats, 0, kSkSlotFloats * (int)sizeof(float), kBufferConfig);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-              const f32x4 v = load_shared4(sr, slot_byte(i, j) + 16 * r4);
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[i][j][4 * r4 + r] += v[r];
-            }
-      }
-    }
-    if (g.interleave == 2)
-      T::template mainloop<2>(g, smem, m0, n0, k0, k1, acc, tid);
-    else if (g.interleave)
-      T::template mainloop<1>(g, smem, m0, n0, k0, k1, acc, tid);
-    else
-      T::mainloop(g, smem, m0, n0, k0, k1, acc, tid);
-    if (k1 < KI) {
-      // a partial: a later range finishes this tile
-      const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-          g.P + (long)ri * kSkSlotFloats, 0, kSkSlotFloats * (int)sizeof(float), kBufferConfig);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const f32x4 v = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), sr, slot_byte(i, j) + 16 * r4, 0,
-                                                   kCpolSc1);
-          }
-      publish();
-      __syncthreads();
-      if (tid == 0)
-        __hip_atomic_store(flags + (long)ri * kSkFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      T::epilogue(g, m0, n0, acc, tid);
-    }
-  }
-}
 
 // ------------------------------------------------------------------------------------------
 // Row kernels of the prefill (one workgroup per row).

@@ -37,14 +37,13 @@ bool g_attn_mfma = true;  // attention kernel of the kernel-level entry points (
 // 1 = copies and fragment reads placed between the MFMAs by scheduling groups, 2 = fenced phases;
 // -1 (default) = per shape: 2 for K >= 8192, else 1. Same box, 3200 rows (us): W1/W3 962 / 890 /
 // 905, W2 510 / 488 / 463.
-int g_gemm_il = -1;
 int g_gemm_ppsplit = 1;   // eight-wave prefill GEMM: split the last, partial round of tiles along K
-int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth (0 = the register-staged kernel)
+int g_gemm_stages = 4;    // prefill GEMM: LDS pipeline depth 2..4, or 6 = the eight-wave kernel
 int g_gemm_bk = 32;       // prefill GEMM: k-step of the LDS pipeline (32 or 64)
 int g_gemm_bm = 128;      // prefill GEMM: rows of A per workgroup with the 64-deep k-step (128 or 256)
 bool g_gemm_auto = true;  // prefill GEMM variant chosen per shape (cleared by forcing one)
 int g_gemm_ksplit = 0;    // prefill GEMM K splits on the LDS-pipeline kernel (0 = chosen per shape)
-std::atomic<unsigned> g_sk_epoch{0};  // stream-K GEMM launches so far (each launch's flag value)
+std::atomic<unsigned> g_sk_epoch{0};  // split-round GEMM launches so far (each launch's flag value)
 int g_upload_stage_mb = 64;  // weight upload: pinned staging chunk in MB (0 = direct pageable copies)
 int g_upload_threads = 8;    // weight upload: host threads filling a staging chunk
 
@@ -63,15 +62,11 @@ struct LayerW {
 // reference src/infer.cpp:205-208), written before each step so that a captured graph stays static.
 // It also zeroes the packed key the fused lm_head argmax posts to.
 __global__ void set_params_kernel(StepParams* p, int token, int pos, const float* inv_freq, float* rope_cs, int half,
-                                  unsigned long long* argmax_key, unsigned* qkv_done, int n_layers) {
+                                  unsigned long long* argmax_key) {
   if (threadIdx.x == 0) {
     p->token = token;
     p->pos = pos;
     *argmax_key = 0ull;
-  }
-  for (int i = threadIdx.x; i < n_layers * kQkvDoneParts; i += blockDim.x) {  // 32- or 64-bit counters
-    qkv_done[kQkvDoneStride * i] = 0u;
-    qkv_done[kQkvDoneStride * i + 1] = 0u;
   }
   fill_rope_table(inv_freq, rope_cs, half, pos);
 }
@@ -125,29 +120,10 @@ struct yhip_ctx {
   int mv_bpc[5] = {0, 0, 0, 0, 0};
   int attn_splits = 32;
   int attn_min_slice = 0;  // 0: the kernel's own default (attn_min_slice_for)
-  // weight prefetch on the attention launch: O (prefetch_o), the first prefetch_w13_mb MB of each
-  // of W1 and W3, over prefetch_blocks worker workgroups
-  int prefetch_o = 0, prefetch_w13_mb = 0, prefetch_blocks = 256;
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
-  unsigned* pf_sink = nullptr;
-  // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepQkvAttn,
-  // kStepAttnO, kStepSplitO, kStepQao, kStepSliceO]
-  hipGraphExec_t graph[3][6] = {};
-  // xcd_rr: a probe launch found workgroup b of a launch on XCD (s + b) % 8 for b < kXcdProbeGrid
-  // (checked when there are 8 kv heads: then every kv head's workgroups of attn_o's grid share one)
-  bool xcd_rr = false;
-  // split-KV attention, slice merge and O in one launch (slice_o_kernel) beyond attn_o_max where
-  // the kv heads' workgroups share an XCD
-  // (opt-in: measured no faster than the split-KV attention launch followed by merge_o)
-  bool slice_o = false;
-  // QKV, attention and O in one launch (qao_kernel) where attn_o applies and the shape has one kv
-  // head per XCD (opt-in: measured slower than the QKV launch followed by attn_o, see the design
-  // notes); qao_ok: a probe launch found the dispatcher's workgroup-to-XCD order it needs
-  bool qao = false;
-  bool qao_ok = false;
-  std::string qao_note;  // why not, when qao_ok is false
-  int qao_max = 700;     // most cached tokens of a step that runs it
-  int qao_wo_after = 2;  // barriers of its workgroups before the Wo loads go out
+  // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepAttnO,
+  // kStepSplitO]
+  hipGraphExec_t graph[3][3] = {};
 
   // attention and the O projection in one launch (attn_o_kernel) for contexts up to attn_o_max
   // tokens: 108-119 us less per token than the separate launches up to 350 keys, 60 at 500, 17 at
@@ -157,13 +133,9 @@ struct yhip_ctx {
   // beyond that, the split-KV attention leaves its slice merge to merge_o_kernel, which merges and
   // runs the O projection in one launch
   bool split_o = true;
-  // decode attention fused into the QKV launch for contexts up to fuse_attn_max tokens (opt-in:
-  // measured slower than the separate launch on MI355X, see the design notes)
-  bool fuse_attn = false;
-  int fuse_attn_max = 1024;
-  unsigned* qkv_done = nullptr;    // per layer: kQkvDoneParts counters of QKV workgroups done (zeroed every step)
-  unsigned* step_abort = nullptr;  // a bounded wait of a fused launch timed out
+  unsigned* step_abort = nullptr;  // a bounded wait of the prefill GEMM's split round timed out
   unsigned long long* rowacc = nullptr;  // [dim] attn_o_kernel's per-row combining words (zero between launches)
+  float* rowovf = nullptr;               // [dim] their fp32 side sums of out-of-range partials (zero between launches)
 
   // single-launch decode (decode_flow.h)
   const void* flow_fn = nullptr;  // instantiation for this shape, or null when the shape has none
@@ -272,6 +244,13 @@ void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
 
 int device_cus();  // compute units of the current device (defined with the test hooks)
 
+// KV slices per kv head of the decode attention: three quarters of a workgroup per CU over all kv
+// heads (swept on MI355X at 1K-16K keys: fewer partials to merge beat one more tile per wave; more
+// than one workgroup per CU does not fit), clamped to [1, 64].
+int default_attn_splits(int cus, int n_kv_heads) {
+  return std::max(1, std::min(64, 3 * cus / (4 * std::max(1, n_kv_heads))));
+}
+
 // Split-K workspace bound: tiles x splits never exceed one workgroup per CU, and a 128 x 128 tile
 // (or 128 x 64 of W1 and of W3) holds 16384 partial sums; the stream-K GEMM keeps one 256 x 256
 // fp32 slot per CU.
@@ -320,8 +299,7 @@ constexpr int kAttnWaves = 8;
 
 template <int HD>
 bool launch_attention_hd(const AttnArgs& a, bool mfma, hipStream_t s) {
-  const int pf_rows = a.pf.blocks > 0 ? (a.pf.blocks + a.n_kv_heads - 1) / a.n_kv_heads : 0;
-  const dim3 grid(a.n_kv_heads, a.nsplit + pf_rows);
+  const dim3 grid(a.n_kv_heads, a.nsplit);
   if constexpr (HD % 32 == 0) {
     if (mfma && a.msl % 32 == 0) {
       switch (a.n_heads / a.n_kv_heads) {
@@ -377,68 +355,6 @@ int check_attn_shape(yhip_ctx* ctx, int hd, int nh, int nkv) {
   const int G = nh / nkv;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(ctx, YHIP_EINVAL, "query heads per kv head must be 1, 2, 4 or 8");
-  return YHIP_OK;
-}
-
-// ---- QKV with the attention fused in ----------------------------------------------------------
-// Attention items (kv head x KV slice) of a step at position pos, as the kernel counts them.
-int attn_items_at(const yhip_ctx* ctx, int pos) {
-  const int kv_len = std::min(pos + 1, ctx->c.max_seq_len);
-  const int chunk = attn_mfma_chunk(kv_len, ctx->attn_splits, attn_min_slice_for(ctx, true));
-  return ctx->c.n_kv_heads * ((kv_len + chunk - 1) / chunk);
-}
-
-int qkv_blocks(const yhip_ctx* ctx) {
-  const int groups = (ctx->q_dim() + 2 * ctx->kv_dim()) / 2;
-  const int bpc = ctx->mv_bpc[0] > 0 ? ctx->mv_bpc[0] : default_bpc(ctx->c.dim, kEpiQkvRope);
-  return std::max(1, std::min((groups + kWavesPerBlock - 1) / kWavesPerBlock, ctx->num_cus * bpc));
-}
-
-bool fused_attention_shape(const yhip_config& c) {
-  const int G = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
-  return (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-         (16 + (size_t)c.dim + c.head_dim) * sizeof(float) <= 65536;
-}
-
-// The step at pos runs the fused launch when the option is on, the MFMA attention applies, there is
-// no sink rotation (pos < max_seq_len), the context is short, and every attention item finds a QKV
-// workgroup.
-bool fused_attention_at(const yhip_ctx* ctx, int pos) {
-  return ctx->fuse_attn && attn_uses_mfma(ctx) && fused_attention_shape(ctx->c) && pos < ctx->c.max_seq_len &&
-         pos + 1 <= ctx->fuse_attn_max && attn_items_at(ctx, pos) <= qkv_blocks(ctx);
-}
-
-template <int KC, int HD, int G>
-void go_qkv_attn(const MatvecArgs& a, const AttnArgs& t, unsigned* done, unsigned* abort_flag, int blocks,
-                 hipStream_t s) {
-  const size_t lds = (16 + (size_t)a.K + a.head_dim) * sizeof(float);
-  hipLaunchKernelGGL((qkv_attn_kernel<KC, HD, G>), dim3(blocks), dim3(kBlock), lds, s, a, t, done, abort_flag);
-}
-
-int launch_qkv_attn(yhip_ctx* ctx, const MatvecArgs& a, const AttnArgs& t, unsigned* done, hipStream_t s) {
-  const int blocks = qkv_blocks(ctx), G = t.n_heads / t.n_kv_heads;
-  unsigned* ab = ctx->step_abort;
-  if (a.K == 4096 && t.head_dim == 128 && G == 4) {
-    go_qkv_attn<8, 128, 4>(a, t, done, ab, blocks, s);
-  } else {
-    switch (t.head_dim * 16 + G) {
-      case 32 * 16 + 1: go_qkv_attn<0, 32, 1>(a, t, done, ab, blocks, s); break;
-      case 32 * 16 + 2: go_qkv_attn<0, 32, 2>(a, t, done, ab, blocks, s); break;
-      case 32 * 16 + 4: go_qkv_attn<0, 32, 4>(a, t, done, ab, blocks, s); break;
-      case 32 * 16 + 8: go_qkv_attn<0, 32, 8>(a, t, done, ab, blocks, s); break;
-      case 64 * 16 + 1: go_qkv_attn<0, 64, 1>(a, t, done, ab, blocks, s); break;
-      case 64 * 16 + 2: go_qkv_attn<0, 64, 2>(a, t, done, ab, blocks, s); break;
-      case 64 * 16 + 4: go_qkv_attn<0, 64, 4>(a, t, done, ab, blocks, s); break;
-      case 64 * 16 + 8: go_qkv_attn<0, 64, 8>(a, t, done, ab, blocks, s); break;
-      case 128 * 16 + 1: go_qkv_attn<0, 128, 1>(a, t, done, ab, blocks, s); break;
-      case 128 * 16 + 2: go_qkv_attn<0, 128, 2>(a, t, done, ab, blocks, s); break;
-      case 128 * 16 + 4: go_qkv_attn<0, 128, 4>(a, t, done, ab, blocks, s); break;
-      case 128 * 16 + 8: go_qkv_attn<0, 128, 8>(a, t, done, ab, blocks, s); break;
-      default: return fail(ctx, YHIP_EINVAL, "fused attention: unsupported shape");
-    }
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("fused QKV + attention launch: ") + hipGetErrorString(e));
   return YHIP_OK;
 }
 
@@ -515,138 +431,18 @@ int launch_attn_o(yhip_ctx* ctx, const AttnArgs& t, const AttnOArgs& o, hipStrea
   return YHIP_OK;
 }
 
-// ---- QKV + attention + O projection in one launch ----------------------------------------------
-// The shape qao_kernel is built for: head_dim 128, 4 query heads per kv head, 8 kv heads (one per
-// XCD), dim = q_dim = 4096 (32 Wo row blocks of 128 rows per kv head, 12 row pairs of [Wq;Wk;Wv]
-// per workgroup), and a grid of one workgroup per CU at most.
-constexpr int kQaoRowsPerBlock = AttnOGeom<128, 4, kQaoWoWaves, kQaoWoLoads>::RB;
-bool qao_shape(const yhip_config& c, int num_cus) {
-  const int G = c.n_kv_heads > 0 ? c.n_heads / c.n_kv_heads : 0;
-  if (c.head_dim != 128 || G != 4 || c.n_kv_heads != kQaoXcds || c.dim != 4096 || c.n_heads * c.head_dim != 4096)
-    return false;
-  const int bph = c.dim / kQaoRowsPerBlock;
-  const int pairs = (G + 2) * c.head_dim / 2;
-  return (pairs + bph - 1) / bph <= kQaoPairsPerWave * kQaoRowWaves && bph < 64 && c.n_kv_heads * bph <= num_cus;
-}
-
-// The probe launch: workgroup b of a launch must run on XCD (s + b) % 8 for one s, for every b below
-// kXcdProbeGrid (the launches that rely on it have at most that many workgroups). Returns an empty
-// string when it does, else what was found.
-constexpr int kXcdProbeGrid = 1024;
-std::string xcd_probe(yhip_ctx* ctx) {
-  const int grid = kXcdProbeGrid;
-  unsigned* d = nullptr;
-  std::vector<unsigned> h(grid, 0xffffffffu);
-  (void)hipGetLastError();  // an earlier call's error is not this launch's
-  if (hipMalloc(&d, grid * sizeof(unsigned)) != hipSuccess) return "probe: out of device memory";
-  hipLaunchKernelGGL(xcc_probe_kernel, dim3(grid), dim3(512), 0, ctx->stream, d);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = hipMemcpyAsync(h.data(), d, grid * sizeof(unsigned), hipMemcpyDeviceToHost, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  hipFree(d);
-  if (e != hipSuccess) return std::string("probe launch: ") + hipGetErrorString(e);
-  for (int b = 0; b < grid; ++b)
-    if (h[b] != (h[0] + b) % kQaoXcds)
-      return "probe: workgroup 0 ran on XCD " + std::to_string(h[0]) + ", workgroup " + std::to_string(b) + " on " +
-             std::to_string(h[b]);
-  return "";
-}
-
-// The step at pos runs QKV, attention and O in one launch where attn_o would run and the shape and
-// the probed placement allow it.
-bool qao_at(const yhip_ctx* ctx, int pos) {
-  return ctx->qao && ctx->qao_ok && attn_o_at(ctx, pos) && pos + 1 <= ctx->qao_max && qao_shape(ctx->c, ctx->num_cus);
-}
-
-int launch_qao(yhip_ctx* ctx, const MatvecArgs& m, const AttnArgs& t, const AttnOArgs& o, int layer, hipStream_t s) {
-  const yhip_config& c = ctx->c;
-  QaoArgs z;
-  z.done = ctx->qkv_done + (size_t)layer * kQkvDoneParts * kQkvDoneStride;
-  z.abort_flag = ctx->step_abort;
-  z.blocks_per_head = c.dim / kQaoRowsPerBlock;
-  z.wo_after = ctx->qao_wo_after;
-  hipLaunchKernelGGL((qao_kernel<128, 4>), dim3(c.n_kv_heads * z.blocks_per_head),
-                     dim3(64 * (kQaoRowWaves + kQaoWoWaves)), 0, s, m, t, o, z);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("QKV + attention + O launch: ") + hipGetErrorString(e));
-  return YHIP_OK;
-}
-
-// ---- split-KV attention + slice merge + O projection in one launch ----------------------------
-// attn_o's grid (kv head b % nkv, 32 Wo row blocks of 128 rows per kv head at the Mistral shape),
-// each workgroup also taking one KV slice of its kv head.
-template <int HD, int G>
-int slice_o_slices(const yhip_config& c) {
-  return attn_o_blocks<HD, G>(c) / c.n_kv_heads;
-}
-// Shapes whose partial block fits LDS (G * HD <= 512).
-int slice_o_slices_for(const yhip_config& c) {
-  switch (c.head_dim * 16 + c.n_heads / std::max(1, c.n_kv_heads)) {
-#define YK_SS(HD, G) case HD * 16 + G: return slice_o_slices<HD, G>(c);
-    YK_SS(32, 1) YK_SS(32, 2) YK_SS(32, 4) YK_SS(32, 8) YK_SS(64, 1) YK_SS(64, 2) YK_SS(64, 4) YK_SS(64, 8)
-    YK_SS(128, 1) YK_SS(128, 2) YK_SS(128, 4)
-#undef YK_SS
-    default: return 0;
-  }
-}
-
-// The step at pos runs it where attn_o would not (more than attn_o_max cached tokens, below
-// max_seq_len), with 8 kv heads on the probed round-robin order, the matrix-core attention's
-// shapes and a grid of one workgroup per CU at most.
-bool slice_o_at(const yhip_ctx* ctx, int pos) {
-  const yhip_config& c = ctx->c;
-  if (!ctx->slice_o || !ctx->xcd_rr || !attn_uses_mfma(ctx) || !attn_o_shape(c) || c.n_kv_heads != kQaoXcds ||
-      pos >= c.max_seq_len || pos + 1 <= ctx->attn_o_max)
-    return false;
-  const int ns = slice_o_slices_for(c);
-  return ns > 0 && ns <= kSliceOMaxSlices && c.n_kv_heads * ns <= std::min(ctx->num_cus, kXcdProbeGrid);
-}
-
-template <int HD, int G>
-void go_slice_o(const yhip_config& c, const AttnArgs& t, const AttnOArgs& o, const SliceOArgs& z, hipStream_t s) {
-  hipLaunchKernelGGL((slice_o_kernel<HD, G, kAttnOWaves, attn_o_loads<HD, G>()>), dim3(attn_o_blocks<HD, G>(c)),
-                     dim3(64 * kAttnOWaves), 0, s, t, o, z);
-}
-
-int launch_slice_o(yhip_ctx* ctx, AttnArgs t, const AttnOArgs& o, int layer, hipStream_t s) {
-  const yhip_config& c = ctx->c;
-  SliceOArgs z;
-  z.done = ctx->qkv_done + (size_t)layer * kQkvDoneParts * kQkvDoneStride;
-  z.abort_flag = ctx->step_abort;
-  z.slices = slice_o_slices_for(c);
-  t.nsplit = z.slices;  // the partial buffer's rows per head for this launch
-  switch (t.head_dim * 16 + t.n_heads / t.n_kv_heads) {
-#define YK_SO(HD, G) case HD * 16 + G: go_slice_o<HD, G>(c, t, o, z, s); break;
-    YK_SO(32, 1) YK_SO(32, 2) YK_SO(32, 4) YK_SO(32, 8) YK_SO(64, 1) YK_SO(64, 2) YK_SO(64, 4) YK_SO(64, 8)
-    YK_SO(128, 1) YK_SO(128, 2) YK_SO(128, 4)
-#undef YK_SO
-    default: return fail(ctx, YHIP_EINVAL, "attention slices + O: unsupported shape");
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("attention slices + O launch: ") + hipGetErrorString(e));
-  return YHIP_OK;
-}
-
 // ---- one decode step ------------------------------------------------------------------------
 // mode: 0 hydrate, 1 logits (device logits + D2H copy into the pinned buffer), 2 argmax.
-// variant: kStepSeparate (every kernel its own launch), kStepQkvAttn (the attention runs inside
-// the QKV launch, fused_attention_at), kStepAttnO (attention and O in one launch, attn_o_at) or
-// kStepSplitO (split-KV attention, then slice merge and O in one launch, split_o_at).
-// kStepQao: QKV, attention and O in one launch (qao_at).
-// kStepSliceO: split-KV attention, slice merge and O in one launch (slice_o_at).
-enum StepVariant : int {
-  kStepSeparate = 0, kStepQkvAttn = 1, kStepAttnO = 2, kStepSplitO = 3, kStepQao = 4, kStepSliceO = 5
-};
+// variant: kStepSeparate (every kernel its own launch), kStepAttnO (attention and O in one launch,
+// attn_o_at) or kStepSplitO (split-KV attention, then slice merge and O in one launch, split_o_at);
+// the values are the header's YHIP_STEP_* codes.
+enum StepVariant : int { kStepSeparate = YHIP_STEP_SEPARATE, kStepAttnO = YHIP_STEP_ATTN_O, kStepSplitO = YHIP_STEP_SPLIT_O };
 int step_variant(const yhip_ctx* ctx, int pos) {
-  if (fused_attention_at(ctx, pos)) return kStepQkvAttn;  // opt-in, so it takes precedence
-  if (qao_at(ctx, pos)) return kStepQao;
   if (attn_o_at(ctx, pos)) return kStepAttnO;
-  if (slice_o_at(ctx, pos)) return kStepSliceO;
   return split_o_at(ctx, pos) ? kStepSplitO : kStepSeparate;
 }
 
 int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
-  const bool fused = variant == kStepQkvAttn;
   const yhip_config& c = ctx->c;
   hipStream_t s = ctx->stream;
   const int qd = ctx->q_dim(), kvd = ctx->kv_dim();
@@ -693,71 +489,34 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
     t.min_slice = attn_min_slice_for(ctx, attn_uses_mfma(ctx));
     t.inv_freq = ctx->inv_freq;
     t.params = ctx->params;
-    if (variant == kStepQao) {
-      // 1 + 2 + 3 in one launch; in the first layer the residual stream is read from the embedding
-      // row by the workgroups that complete x's rows, and nothing writes x before them
-      AttnOArgs o;
-      o.wo = L.wo;
-      o.x = ctx->x;
-      o.rowacc = ctx->rowacc;
-      o.dim = c.dim;
-      o.q_dim = qd;
-      if (l == 0) {
-        a.emb_out = nullptr;
-        o.emb = ctx->embed;
-        o.params = ctx->params;
-      }
-      if ((rc = launch_qao(ctx, a, t, o, l, s))) return rc;
-    } else if (fused) {
-      a.coh_store = 1;
-      if ((rc = launch_qkv_attn(ctx, a, t, ctx->qkv_done + (size_t)l * kQkvDoneParts * kQkvDoneStride, s))) return rc;
-    } else {
-      if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
-    }
-    if (variant == kStepSeparate && (ctx->prefetch_o || ctx->prefetch_w13_mb)) {
-      // O is read by its matvec in 64 KB pieces (8 rows of q_dim halves per workgroup for q_dim
-      // 4096), W1/W3 in 32 KB pieces per matrix; chunk i of a range feeds consumer workgroup i.
-      const long o_units = (long)c.dim * qd * 2 / 16;
-      const long w_units = std::min((long)c.hidden_dim * c.dim * 2, (long)ctx->prefetch_w13_mb << 20) / 16;
-      if (ctx->prefetch_o) t.pf.r[0] = PrefetchRange{reinterpret_cast<const u32x4*>(L.wo), o_units, 4096};
-      if (w_units > 0) {
-        t.pf.r[1] = PrefetchRange{reinterpret_cast<const u32x4*>(L.w1), w_units, 2048};
-        t.pf.r[2] = PrefetchRange{reinterpret_cast<const u32x4*>(L.w3), w_units, 2048};
-      }
-      t.pf.blocks = ctx->prefetch_blocks;
-      t.pf.magic = 0x9E3779B9u;
-      t.pf.sink = ctx->pf_sink;
-    }
+    if ((rc = launch_matvec(ctx, a, kEpiQkvRope, 2, ctx->num_cus, s, ctx->mv_bpc[0]))) return rc;
     if (variant == kStepSplitO) {  // 2. attention, its slices merged by the O launch
       t.defer_merge = 1;
       if ((rc = launch_attention(ctx, t, s))) return rc;
     }
-    if (variant == kStepAttnO || variant == kStepSplitO || variant == kStepSliceO) {
+    if (variant == kStepAttnO || variant == kStepSplitO) {
       // 2 + 3. attention (or its slice merge) and O-proj + residual in one launch
       AttnOArgs o;
       o.wo = L.wo;
       o.x = ctx->x;
       o.rowacc = ctx->rowacc;
+      o.ovf = ctx->rowovf;
       o.dim = c.dim;
       o.q_dim = qd;
-      if (variant == kStepSliceO) {
-        if ((rc = launch_slice_o(ctx, t, o, l, s))) return rc;
-      } else if ((rc = launch_attn_o(ctx, t, o, s, variant == kStepSplitO))) {
-        return rc;
-      }
+      if ((rc = launch_attn_o(ctx, t, o, s, variant == kStepSplitO))) return rc;
     }
     if (variant == kStepSeparate && (rc = launch_attention(ctx, t, s))) return rc;
     // 3. O-proj + residual
-    if (variant != kStepAttnO && variant != kStepSplitO && variant != kStepQao && variant != kStepSliceO) {
-    a = mv_base();
-    a.w0 = L.wo;
-    a.row_step = 2L * qd;
-    a.r_step = qd;
-    a.groups = c.dim / 2;
-    a.K = qd;
-    a.x = ctx->att;
-    a.out = ctx->x;
-    if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s, ctx->mv_bpc[1]))) return rc;
+    if (variant == kStepSeparate) {
+      a = mv_base();
+      a.w0 = L.wo;
+      a.row_step = 2L * qd;
+      a.r_step = qd;
+      a.groups = c.dim / 2;
+      a.K = qd;
+      a.x = ctx->att;
+      a.out = ctx->x;
+      if ((rc = launch_matvec(ctx, a, kEpiResidual, 2, ctx->num_cus, s, ctx->mv_bpc[1]))) return rc;
     }
     // 4. rmsnorm + W1/W3 + SwiGLU
     a = mv_base();
@@ -816,8 +575,6 @@ int enqueue_step(yhip_ctx* ctx, int mode, int variant) {
       hipLaunchKernelGGL(lm_head_argmax_kernel<0>, dim3(blocks), dim3(kBlock), lds, s, a, ctx->argmax_key);
     HIP_TRY(ctx, hipGetLastError());
   }
-  if (fused || variant == kStepQao || variant == kStepSliceO)  // a wait's time-out flag, checked after the caller's synchronisation
-    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (mode == 1) {
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
@@ -930,14 +687,14 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   return YHIP_OK;
 }
 
-// After a synchronised step: a wait of a fused launch that timed out poisons it (in the QKV +
-// attention + O launch also the sign of a kv head whose workgroups were not all on one XCD).
+// After a synchronised prefill: a bounded wait of a prefill GEMM's split round that timed out
+// poisons the result.
 int check_step_abort(yhip_ctx* ctx) {
   if (ctx->argmax_host[4] == 0) return YHIP_OK;
   ctx->argmax_host[4] = 0;
   hipMemsetAsync(ctx->step_abort, 0, sizeof(unsigned), ctx->stream);
   hipStreamSynchronize(ctx->stream);
-  return fail(ctx, YHIP_EDEVICE, "fused QKV + attention launch: a dependency wait timed out");
+  return fail(ctx, YHIP_EDEVICE, "prefill GEMM: a wait for a partial tile timed out");
 }
 
 // After a synchronised single-launch step: a wait that timed out poisons the step.
@@ -984,8 +741,7 @@ int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode) {
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   if (ctx->use_flow) return launch_flow_step(ctx, token, pos, mode);
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->params, token, pos,
-                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key, ctx->qkv_done,
-                     c.n_layers);
+                     (const float*)ctx->inv_freq, ctx->rope_cs, c.head_dim / 2, ctx->argmax_key);
   HIP_TRY(ctx, hipGetLastError());
   const int variant = step_variant(ctx, pos);
   if (!ctx->use_graph) return enqueue_step(ctx, mode, variant);
@@ -1079,34 +835,33 @@ void gemm_choice(int epi, int M, int N, int K, int cus, int& stages, int& bk, in
   if (big_rows && K % 64 == 0 && M >= (epi == kGemmSwiGLU ? 192 : 1536)) bm = 256;
 }
 
+// The variant launch_gemm runs: gemm_choice, then the kernels' own limits. The eight-wave kernel
+// needs K % 64 == 0; the LDS pipeline exists with 4 stages of 32-deep k-steps on 128 rows, or 2..3
+// stages of 64-deep ones on 128 or 256 rows (a forced eight-wave kernel with K % 64 != 0 lands there).
+void gemm_resolve(int epi, int M, int N, int K, int cus, int& stages, int& bk, int& bm) {
+  gemm_choice(epi, M, N, K, cus, stages, bk, bm);
+  if (stages == 6 && K % 64 == 0) {
+    bk = 64;
+    bm = kBigM;
+    return;
+  }
+  if (K % 64 != 0) bk = 32;
+  if (bk != 64) {
+    bm = 128;
+    stages = 4;
+  } else {
+    stages = std::min(std::max(stages, 2), 3);
+  }
+}
+
 // Prefill GEMM launch. The variant is chosen per shape (gemm_choice) unless forced with the
 // process-wide options.
 template <int EPI>
 int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.K % kGBK != 0 || g.M <= 0 || g.N <= 0) return fail(ctx, YHIP_EINVAL, "gemm: K must be a multiple of 32");
   int stages, bk, bm;
-  gemm_choice(EPI, g.M, g.N, g.K, ctx ? ctx->num_cus : device_cus(), stages, bk, bm);
-  // one-dimensional grids of 8 * ceil(tiles / 8) workgroups (gemm_tile)
-  auto tiles8 = [&](int tm, int nc) {
-    const int t = ((g.M + tm - 1) / tm) * ((g.N + nc - 1) / nc);
-    return dim3(8 * ((t + 7) / 8));
-  };
-  if (stages == 5) {  // 256 x 256 tiles, stream-K over all CUs
-    const int P = ctx ? ctx->num_cus : device_cus();
-    if (!g.P || !g.sk_flags || !g.abort_flag || g.p_floats < (long)P * kSkSlotFloats)
-      return fail(ctx, YHIP_EINVAL, "gemm: stream-K needs a partial slot and a flag per CU");
-    const unsigned epoch = ++g_sk_epoch;
-    GemmArgs gi = g;
-    gi.interleave = g_gemm_il >= 0 ? g_gemm_il : (g.K >= 8192 ? 2 : 1);
-    if (g.K % 64 == 0)
-      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 2, 64>), dim3(P), dim3(256), 0, s, gi, g.sk_flags, epoch, g.abort_flag);
-    else
-      hipLaunchKernelGGL((gemm_sk_kernel<EPI, 4, 32>), dim3(P), dim3(256), 0, s, gi, g.sk_flags, epoch, g.abort_flag);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
-    return YHIP_OK;
-  }
-  if (stages == 6 && g.K % 64 == 0) {  // 256 x 256 tiles, eight waves in two alternating groups
+  gemm_resolve(EPI, g.M, g.N, g.K, ctx ? ctx->num_cus : device_cus(), stages, bk, bm);
+  if (stages == 6) {  // 256 x 256 tiles, eight waves in two alternating groups
     const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
     const int P = ctx ? ctx->num_cus : device_cus();
     const PPSplit sp = pp_split_plan((long)((g.M + kBigM - 1) / kBigM) * ((g.N + nc - 1) / nc), g.K / 64, P,
@@ -1117,22 +872,7 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
     return YHIP_OK;
   }
-  if (stages == 6) stages = 1;  // a 64-deep k-step needs K % 64 == 0: the 32-deep large-tile kernel
-  if (stages == 1) {  // 256 x 256 tiles
-    const int nc = EPI == kGemmSwiGLU ? kBigN / 2 : kBigN;
-    GemmArgs gi = g;
-    gi.interleave = g_gemm_il >= 0 ? g_gemm_il : (g.K >= 8192 ? 2 : 1);
-    if (bk == 64 && g.K % 64 == 0)
-      hipLaunchKernelGGL((gemm_big_kernel<EPI, 2, 64>), tiles8(kBigM, nc), dim3(256), 0, s, gi);
-    else
-      hipLaunchKernelGGL((gemm_big_kernel<EPI, 4, 32>), tiles8(kBigM, nc), dim3(256), 0, s, gi);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(ctx, YHIP_EDEVICE, std::string("gemm launch: ") + hipGetErrorString(e));
-    return YHIP_OK;
-  }
   const int ncols = EPI == kGemmSwiGLU ? kGBN / 2 : kGBN;
-  if (g.K % 64 != 0) bk = 32;  // a 64-deep k-step needs K % 64 == 0
-  if (bk != 64) bm = 128;
   // Split-K when the output has too few tiles to fill the GPU (short prompts): the largest power of
   // two that keeps tiles x splits within one workgroup per CU, divides the k-steps and leaves each
   // split at least two of them; the partials go to the caller's workspace (none: no split).
@@ -1161,10 +901,7 @@ int launch_gemm(yhip_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     case 3 * 10000 + 8000 + 128: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 128>), grid, dim3(256), 0, s, ga); break;
     case 2 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 2, 64, 256>), grid, dim3(512), 0, s, ga); break;
     case 3 * 10000 + 8000 + 256: hipLaunchKernelGGL((gemm_lds_kernel<EPI, 3, 64, 256>), grid, dim3(512), 0, s, ga); break;
-    default:
-      ga.ksplit = 1;
-      hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((g.N + ncols - 1) / ncols, (g.M + kGBM - 1) / kGBM), dim3(256), 0, s, ga);
-      break;
+    default: return fail(ctx, YHIP_EINVAL, "gemm: no LDS-pipeline kernel for this variant");
   }
   if (ga.ksplit > 1) {
     const long total = (long)g.M * g.N;
@@ -1397,16 +1134,9 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device_ordinal) == hipSuccess && prop.multiProcessorCount > 0)
     ctx->num_cus = prop.multiProcessorCount;
-  // KV slices per kv head: one attention workgroup per CU over all kv heads at long context
-  // KV slices per kv head: three quarters of a workgroup per CU (swept on MI355X at 1K-16K keys:
-  // fewer partials to merge beat one more tile per wave; more than one workgroup per CU does not fit)
-  ctx->attn_splits = std::max(1, std::min(64, 3 * ctx->num_cus / (4 * std::max(1, c.n_kv_heads))));
+  ctx->attn_splits = default_attn_splits(ctx->num_cus, c.n_kv_heads);
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(nullptr, YHIP_EDEVICE, "stream create failed"));
-  const std::string probe = c.n_kv_heads == kQaoXcds ? xcd_probe(ctx) : std::string("kv heads");
-  ctx->xcd_rr = probe.empty();
-  ctx->qao_note = qao_shape(c, ctx->num_cus) ? probe : std::string("shape");
-  ctx->qao_ok = ctx->qao_note.empty();
 
   // Weights: one allocation, 256-byte aligned sub-buffers.
   const size_t dim = c.dim, hid = c.hidden_dim, qd = ctx->q_dim(), kvd = ctx->kv_dim(), V = c.vocab_size;
@@ -1458,9 +1188,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
                a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
                a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
                a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
-               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_pfs = atake(1024 * 4),
-               a_qd = atake((size_t)std::max(1, c.n_layers) * kQkvDoneParts * kQkvDoneStride * sizeof(unsigned)),
-               a_sa = atake(256), a_racc = atake(dim * sizeof(unsigned long long));
+               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_sa = atake(256), a_racc = atake(dim * sizeof(unsigned long long)),
+               a_ovf = atake(dim * sizeof(float));
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
   ctx->x = (float*)(ctx->abase + a_x);
@@ -1479,10 +1208,9 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->kvcur = (uint32_t*)(ctx->abase + a_kvc);
   ctx->best_v = (float*)(ctx->abase + a_bv);
   ctx->best_i = (int*)(ctx->abase + a_bi);
-  ctx->pf_sink = (unsigned*)(ctx->abase + a_pfs);
-  ctx->qkv_done = (unsigned*)(ctx->abase + a_qd);
   ctx->step_abort = (unsigned*)(ctx->abase + a_sa);
   ctx->rowacc = (unsigned long long*)(ctx->abase + a_racc);
+  ctx->rowovf = (float*)(ctx->abase + a_ovf);
   {
     const std::vector<float> f = make_inv_freq(c.head_dim, c.rotary_dim, c.rope_theta);
     if (hipMemcpy(ctx->inv_freq, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -1770,20 +1498,15 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
       g_attn_mfma = value != 0;
       return YHIP_OK;
     }
-    if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 0 register-staged; 1 large tile; 2..4 LDS stages;
-                                        // 5 large tiles, stream-K; 6 eight-wave large tiles
-      if (value < -1 || value > 6) return fail(nullptr, YHIP_EINVAL, "gemm_stages must be in [-1, 6]");
+    if (!strcmp(key, "gemm_stages")) {  // -1: chosen per shape; 2..4 LDS stages; 6 eight-wave large tiles
+      if (value < -1 || (value >= 0 && value < 2) || value == 5 || value > 6)
+        return fail(nullptr, YHIP_EINVAL, "gemm_stages must be -1, 2, 3, 4 or 6");
       g_gemm_auto = value < 0;
       if (value >= 0) g_gemm_stages = value;
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_ppsplit")) {
       g_gemm_ppsplit = value != 0;
-      return YHIP_OK;
-    }
-    if (!strcmp(key, "gemm_il")) {
-      if (value < -1 || value > 2) return fail(nullptr, YHIP_EINVAL, "gemm_il must be -1 (per shape), 0, 1 or 2");
-      g_gemm_il = value;
       return YHIP_OK;
     }
     if (!strcmp(key, "gemm_bk")) {
@@ -1845,38 +1568,6 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "attn_o_max")) {
     if (value < 0) return fail(ctx, YHIP_EINVAL, "attn_o_max must be >= 0");
     ctx->attn_o_max = value;
-  } else if (!strcmp(key, "slice_o")) {
-    if (value == 2) {
-      const yhip_config& c = ctx->c;
-      const int ns = slice_o_slices_for(c);
-      if (!ctx->xcd_rr || !attn_uses_mfma(ctx) || !attn_o_shape(c) || c.n_kv_heads != kQaoXcds || ns <= 0 ||
-          ns > kSliceOMaxSlices || c.n_kv_heads * ns > std::min(ctx->num_cus, kXcdProbeGrid))
-        return fail(ctx, YHIP_EINVAL, "slice_o: no attention slices + O launch for this context");
-    }
-    ctx->slice_o = value != 0;
-  } else if (!strcmp(key, "qao")) {
-    if (value == 2 && !ctx->qao_ok)
-      return fail(ctx, YHIP_EINVAL, "qao: no QKV + attention + O launch for this context (" + ctx->qao_note + ")");
-    ctx->qao = value != 0;
-  } else if (!strcmp(key, "qao_wo_after")) {
-    if (value < 0 || value > 5) return fail(ctx, YHIP_EINVAL, "qao_wo_after must be in [0, 5]");
-    ctx->qao_wo_after = value;
-  } else if (!strcmp(key, "qao_max")) {
-    if (value < 0) return fail(ctx, YHIP_EINVAL, "qao_max must be >= 0");
-    ctx->qao_max = value;
-  } else if (!strcmp(key, "fuse_attn")) {
-    ctx->fuse_attn = value != 0;
-  } else if (!strcmp(key, "fuse_attn_max")) {
-    if (value < 0) return fail(ctx, YHIP_EINVAL, "fuse_attn_max must be >= 0");
-    ctx->fuse_attn_max = value;
-  } else if (!strcmp(key, "prefetch_o")) {
-    ctx->prefetch_o = value != 0;
-  } else if (!strcmp(key, "prefetch_w13_mb")) {
-    if (value < 0 || value > 4096) return fail(ctx, YHIP_EINVAL, "prefetch_w13_mb must be in [0, 4096]");
-    ctx->prefetch_w13_mb = value;
-  } else if (!strcmp(key, "prefetch_blocks")) {
-    if (value < 8 || value > 4096 || value % 8) return fail(ctx, YHIP_EINVAL, "prefetch_blocks must be a multiple of 8 in [8, 4096]");
-    ctx->prefetch_blocks = value;
   } else if (!strncmp(key, "bpc_", 4)) {
     static const char* names[5] = {"bpc_qkv", "bpc_o", "bpc_w13", "bpc_w2", "bpc_lm"};
     int i = 0;
@@ -1905,12 +1596,32 @@ extern "C" int yhip_debug_read(yhip_ctx* ctx, int which, float* host, size_t n) 
     case 2: src = ctx->att; cap = ctx->q_dim(); break;
     case 3: src = ctx->hb; cap = c.hidden_dim; break;
     case 4: src = ctx->logits; cap = c.vocab_size; break;
+    case 5: src = ctx->inv_freq; cap = (size_t)c.head_dim / 2; break;
     default: return fail(ctx, YHIP_EINVAL, "unknown buffer");
   }
   if (n > cap) return fail(ctx, YHIP_EINVAL, "read larger than buffer");
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   HIP_TRY(ctx, hipMemcpyAsync(host, src, n * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return YHIP_OK;
+}
+
+extern "C" int yhip_step_plan(yhip_ctx* ctx, int pos, int* variant, int* slices, int* slice_len) {
+  if (!ctx) return fail(nullptr, YHIP_EINVAL, "null context");
+  if (pos < 0) return fail(ctx, YHIP_EINVAL, "negative position");
+  const int kv_len = std::min(pos + 1, ctx->c.max_seq_len);
+  int v = ctx->use_flow ? YHIP_STEP_SINGLE : step_variant(ctx, pos);
+  int ns = 1, len = kv_len;
+  if (v != YHIP_STEP_ATTN_O) {
+    // the same rules the launches apply: the single launch and the SIMT kernel in 64-key granules
+    const bool mfma = !ctx->use_flow && attn_uses_mfma(ctx);
+    const int ms = attn_min_slice_for(ctx, mfma);
+    len = mfma ? attn_mfma_chunk(kv_len, ctx->attn_splits, ms) : attn_chunk(kv_len, ctx->attn_splits, ms);
+    ns = (kv_len + len - 1) / len;
+  }
+  if (variant) *variant = v;
+  if (slices) *slices = ns;
+  if (slice_len) *slice_len = len;
   return YHIP_OK;
 }
 
@@ -1948,11 +1659,29 @@ struct DevBufs {
 };
 
 int device_cus() {
+  static std::atomic<int> cached[64] = {};  // per device, looked up once
   int dev = 0;
   hipGetDevice(&dev);
+  if (dev >= 0 && dev < 64 && cached[dev].load(std::memory_order_relaxed) > 0)
+    return cached[dev].load(std::memory_order_relaxed);
+  int cus = 256;
   hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0) return prop.multiProcessorCount;
-  return 256;
+  if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0) cus = prop.multiProcessorCount;
+  if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// The attention hooks' slice plan. nsplit 0: the decode step's own (default_attn_splits slices per
+// kv head; the matrix-core kernel picks the slice length from the context length, attn_mfma_chunk;
+// the SIMT kernel takes slices of at least 64 keys). nsplit > 0: that many slices of at least 64.
+void hook_slice_plan(int head_dim, int max_seq_len, int n_kv_heads, int& nsplit, int& min_slice) {
+  const bool mfma = g_attn_mfma && head_dim % 32 == 0 && max_seq_len % 32 == 0;
+  if (nsplit <= 0) {
+    nsplit = default_attn_splits(device_cus(), n_kv_heads);
+    min_slice = mfma ? 0 : 64;
+  } else {
+    min_slice = 64;
+  }
 }
 
 #define TRY_ALLOC(p) \
@@ -2042,7 +1771,8 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   if (!q || !kcache || !vcache || !att_out || pos < 0 || max_seq_len <= kKvSinks)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
-  if (nsplit <= 0) nsplit = std::max(1, std::min(64, 256 / n_kv_heads));
+  int min_slice = 64;
+  hook_slice_plan(head_dim, max_seq_len, n_kv_heads, nsplit, min_slice);
   if (nsplit > 64) return fail(nullptr, YHIP_EINVAL, "nsplit must be at most 64");
   const size_t kv = (size_t)n_kv_heads * head_dim * max_seq_len;
   DevBufs b;
@@ -2076,7 +1806,7 @@ extern "C" int yhip_test_attention(const float* q, uint16_t* kcache, const uint1
   t.n_kv_heads = n_kv_heads;
   t.msl = max_seq_len;
   t.nsplit = nsplit;
-  t.min_slice = 64;
+  t.min_slice = min_slice;
   t.inv_freq = dfreq;
   t.params = dp;
   if (int rc = launch_attention(nullptr, t, nullptr)) return rc;
@@ -2154,7 +1884,8 @@ extern "C" int yhip_attention_noalloc(const float* q, uint16_t* kcache, const ui
       rotary_dim > head_dim)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
-  if (nsplit <= 0) nsplit = std::max(1, std::min(64, 256 / n_kv_heads));  // as yhip_test_attention
+  int min_slice = 64;
+  hook_slice_plan(head_dim, max_seq_len, n_kv_heads, nsplit, min_slice);  // as yhip_test_attention
   if (nsplit > 64) return fail(nullptr, YHIP_EINVAL, "nsplit must be at most 64");
   const size_t part_bytes = (size_t)n_heads * nsplit * (head_dim + 2) * sizeof(float);
   if (part_bytes > kNaPartialBytes)
@@ -2180,7 +1911,7 @@ extern "C" int yhip_attention_noalloc(const float* q, uint16_t* kcache, const ui
   t.n_kv_heads = n_kv_heads;
   t.msl = max_seq_len;
   t.nsplit = nsplit;
-  t.min_slice = 64;  // as yhip_test_attention
+  t.min_slice = min_slice;
   t.inv_freq = reinterpret_cast<const float*>(base + 512);
   t.params = reinterpret_cast<const StepParams*>(base + 256);
   return launch_attention(nullptr, t, s);
@@ -2310,17 +2041,10 @@ extern "C" int yhip_gemm_variant(int M, int N, int K, int mode, int* stages, int
   if (!stages || !bk || !bm || M <= 0 || N <= 0 || K <= 0 || mode < 0 || mode > 2)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   int s = 0, k = 0, m = 0;
-  gemm_choice(mode, M, N, K, device_cus(), s, k, m);
-  if (s == 6 && K % 64 != 0) s = 1;  // launch_gemm's fallback
-  const bool big = s == 1 || s == 5 || s == 6;
-  if (!big) {  // the LDS pipeline's own limits (launch_gemm)
-    if (K % 64 != 0) k = 32;
-    if (k != 64) m = 128;
-  }
-  if (s == 6) k = 64;
+  gemm_resolve(mode, M, N, K, device_cus(), s, k, m);
   *stages = s;
   *bk = k;
-  *bm = big ? kBigM : m;
+  *bm = m;
   return YHIP_OK;
 }
 

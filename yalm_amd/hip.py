@@ -20,6 +20,9 @@ _ip = ctypes.POINTER(ctypes.c_int)
 MODE_HYDRATE = 0
 MODE_LOGITS = 1
 
+# Launch structure of a decode step (yhip_step_plan), as include/yalm_hip.h's YHIP_STEP_*.
+STEP_SEPARATE, STEP_ATTN_O, STEP_SPLIT_O, STEP_SINGLE = 0, 1, 2, 3
+
 # Every symbol include/yalm_hip.h declares.
 EXPORTS = (
     "yhip_create", "yhip_destroy", "yhip_upload_layer", "yhip_upload_globals", "yhip_forward",
@@ -27,6 +30,7 @@ EXPORTS = (
     "yhip_debug_read", "yhip_last_error", "yhip_step_stats", "yhip_test_matvec", "yhip_test_ffn", "yhip_test_attention",
     "yhip_test_qkv", "yhip_test_gemm", "yhip_test_argmax", "yhip_bench_kernel", "yhip_bench_attention",
     "yhip_bench_gemm", "yhip_gemm_variant", "yhip_attention_noalloc", "yhip_kv_fill_normal", "yhip_bench_stream",
+    "yhip_step_plan",
 )
 
 
@@ -69,6 +73,7 @@ def lib():
         "yhip_debug_read": (ctypes.c_int, [vp, ctypes.c_int, _f32p, ctypes.c_size_t]),
         "yhip_last_error": (ctypes.c_char_p, [vp]),
         "yhip_step_stats": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_double), _ip]),
+        "yhip_step_plan": (ctypes.c_int, [vp, ctypes.c_int, _ip, _ip, _ip]),
         "yhip_test_matvec": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, ctypes.c_int, ctypes.c_int,
                                             _f32p, _f32p]),
         "yhip_test_ffn": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, _u16p, _u16p, _u16p, ctypes.c_int,
@@ -207,6 +212,13 @@ class HipModel:
     def set_option(self, key, value):
         _check(lib().yhip_set_option(self.h, key.encode(), int(value)), self.h)
 
+    def step_plan(self, pos):
+        """(variant, slices per kv head holding keys, keys per slice) of the decode step at pos under
+        the current options; variant is one of STEP_*."""
+        out = [ctypes.c_int() for _ in range(3)]
+        _check(lib().yhip_step_plan(self.h, int(pos), *[ctypes.byref(o) for o in out]), self.h)
+        return tuple(o.value for o in out)
+
     def step_stats(self):
         """(device microseconds, steps) timed since set_option("stats", 1)."""
         us = ctypes.c_double()
@@ -244,19 +256,12 @@ def set_test_bpc(n):
 
 
 def set_gemm_stages(n, bk=32, bm=128):
-    """Prefill GEMM variant: -1 = chosen per shape (default); 0 = register-staged kernel; 1 = large
-    tiles (k-step bk); 2..4 = LDS pipeline stages with k-step bk and workgroup rows bm; 5 = large
-    tiles, stream-K over all CUs."""
+    """Prefill GEMM variant: -1 = chosen per shape (default); 2..4 = LDS pipeline stages with k-step
+    bk and workgroup rows bm (4 stages with 32-deep k-steps, 2 or 3 with 64-deep ones); 6 = the
+    eight-wave 256 x 256 kernel (64-deep k-steps, K % 64 == 0)."""
     _check(lib().yhip_set_option(None, b"gemm_stages", int(n)))
     _check(lib().yhip_set_option(None, b"gemm_bk", int(bk)))
     _check(lib().yhip_set_option(None, b"gemm_bm", int(bm)))
-
-
-def set_gemm_interleave(mode=-1):
-    """Large-tile prefill GEMM k-step schedule: -1 = per shape (default), 0 = the compiler's own
-    order, 1 = copies and fragment reads interleaved with the MFMAs by scheduling groups, 2 = fenced
-    phases."""
-    _check(lib().yhip_set_option(None, b"gemm_il", int(mode)))
 
 
 def set_gemm_ppsplit(on=True):
@@ -272,8 +277,8 @@ def set_gemm_ksplit(n=0):
 
 def gemm_variant(M, N, K, mode):
     """(stages, k-step, workgroup rows) of the prefill GEMM yhip_prefill runs for this shape and mode
-    under the current process-wide options (stages 6 = the eight-wave 256 x 256 kernel, 1 = the
-    four-wave one, 5 = the same with stream-K, 2..4 = the 128-row LDS pipeline's depth)."""
+    under the current process-wide options (stages 6 = the eight-wave 256 x 256 kernel, 2..4 = the
+    LDS pipeline's depth)."""
     out = [ctypes.c_int() for _ in range(3)]
     _check(lib().yhip_gemm_variant(M, N, K, mode, *[ctypes.byref(o) for o in out]))
     return tuple(o.value for o in out)
