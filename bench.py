@@ -428,7 +428,7 @@ def main():
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_of("decode_step_traffic.json"),
                     "traffic_kind": "recorded (profiles/decode_step_traffic.json), not measured in this run",
-                    "kernel": "decode_flow_kernel<128,4> (the whole token, one launch)",
+                    "kernel": "decode_step_kernel<128,4,8,14> (the whole token, one cooperative launch)",
                     "bytes_per_launch": int(step_bytes), "us_per_launch": round(step_us, 3)}
     else:
         roofline = w13

@@ -104,10 +104,12 @@ int yhip_kv_write(yhip_ctx* ctx, int layer, const uint16_t* k_host, const uint16
  * attention-heavy workload (a KV cache pre-filled to 16384 positions). No reference counterpart. */
 int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed);
 
-/* Options: "single_launch" (1 = the whole step as one launch, a dataflow of workgroups, where the
- * kernel has an instantiation: head_dim 128 with 4 q heads per kv head, and the test shapes;
- * 0 = per-op kernels, the default), "flow_bpc" / "flow_bpc_w2" (workgroups per CU of the single
- * launch's matvec phases / of its W2 phase, defaults 2 / 1), "graph" (per-op kernels: 1 = replay
+/* Options: "single_launch" (1 = the whole step as one cooperative launch, one workgroup per CU
+ * walking the step's phases with a grid barrier between them, where the kernel has an
+ * instantiation: head_dim 128 with 4 q heads per kv head, and the test shapes, on at most 256 CUs;
+ * 0 = per-op kernels, the default), "step_atto_max" (single launch: attention and the O projection
+ * as one phase for steps with at most this many cached tokens, below max_seq_len, default 192;
+ * 0 = always two phases), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
  * kv head, default 3/4 of compute units / n_kv_heads clamped to [1,64]),
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for

@@ -21,7 +21,14 @@
 //     range and split into hi/lo columns like q (undone at the end);
 //   - the waves' (m, l, o) are merged in LDS; slices of one kv head are merged by the last one
 //     to finish (attn_merge_slices).
-// Needs head_dim % 32 == 0 and max_seq_len % 32 == 0.
+// Needs head_dim % 16 == 0 (head_dim 16: the k-step's upper 16 dims of K lie past the head's K
+// region and read as zero, those of q are masked to zero) and max_seq_len % 8 == 0 (16-byte V
+// reads; keys past the context are read clamped and masked). The per-op launches keep to
+// max_seq_len % 32 == 0.
+//
+// COH (the single-launch decode, where q and the current position's K/V were written by other
+// workgroups of the same launch with write-through stores): q, K and V are read with the
+// agent-coherence bit (sc1), so no line this XCD's L2 may still hold is used.
 #pragma once
 
 #include "kernels.h"
@@ -38,19 +45,23 @@ __device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, c
 
 // K and V fragments of one wave for one 32-key tile starting at t0 (lane = 16 q + m).
 template <int HD>
+constexpr int kKSteps = (HD + 31) / 32;  // 32-dim k-steps of the score product
+
+template <int HD>
 struct KvFrag {
-  u32x4 k[2][HD / 32];  // group j, k step ks: key t0 + 8 (m / 4) + 4 j + m % 4, dims 32 ks + 8 q .. +7
+  u32x4 k[2][kKSteps<HD>];  // group j, k step ks: key t0 + 8 (m / 4) + 4 j + m % 4, dims 32 ks + 8 q .. +7
   u32x4 v[HD / 16];     // dim 16 dt + m, keys t0 + 8 q .. +7
 };
 
 // Buffer loads: the K/V regions of the kv head are addressed by a descriptor in scalar registers,
 // so each load takes one 32-bit lane offset plus a wave-uniform scalar offset (the dims / k-step
 // strides) instead of a 64-bit address per load; reads past the region return zero.
+template <bool COH = false>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, COH ? kCpolSc1 : 0));
 }
 
-template <int HD>
+template <int HD, bool COH = false>
 __device__ __forceinline__ void load_kv_frag(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int msl, int t0,
                                              int m, int q, KvFrag<HD>& f) {
   // K byte offset: (2 ks + q / 2) * 16 msl * 2 + key * 32 + 16 (q % 2)
@@ -59,12 +70,12 @@ __device__ __forceinline__ void load_kv_frag(__amdgpu_buffer_rsrc_t kr, __amdgpu
     const int tk = min(t0 + 8 * (m >> 2) + 4 * j + (m & 3), msl - 1);
     const int vo = (q >> 1) * 32 * msl + tk * 32 + 16 * (q & 1);
 #pragma unroll
-    for (int ks = 0; ks < HD / 32; ++ks) f.k[j][ks] = buffer_load16(kr, vo, ks * 64 * msl);
+    for (int ks = 0; ks < kKSteps<HD>; ++ks) f.k[j][ks] = buffer_load16<COH>(kr, vo, ks * 64 * msl);
   }
   // V byte offset: (16 dt + m) * msl * 2 + key * 2
   const int vo = m * 2 * msl + 2 * min(t0 + 8 * q, msl - 8);
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) f.v[dt] = buffer_load16(vr, vo, dt * 32 * msl);
+  for (int dt = 0; dt < HD / 16; ++dt) f.v[dt] = buffer_load16<COH>(vr, vo, dt * 32 * msl);
 }
 
 template <int HD, int G, int NW>
@@ -85,19 +96,21 @@ struct AttnMfmaSmem {
 // K/V tile and its q loads are issued (at once in a wave without a tile): loads it issues are
 // younger than those, and loads retire in issue order, so waiting for the tile and q does not wait
 // for them.
-template <int HD, int G, int NW, int NB, class Issue>
+// COH: coherent q, K and V loads (see the file comment).
+template <int HD, int G, int NW, int NB, bool COH = false, class Issue>
 __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_begin, int t_end,
                                                 AttnMfmaSmem<HD, G, NW>& sm, Issue issue) {
-  static_assert(HD % 32 == 0 && G >= 1 && G <= 8, "head_dim % 32, 1..8 query heads per kv head");
+  static_assert(HD % 16 == 0 && G >= 1 && G <= 8, "head_dim % 16, 1..8 query heads per kv head");
   static_assert(NB == 1 || NB == 2, "tile buffers per wave");
-  constexpr int KS = HD / 32, DT = HD / 16;
+  constexpr int KS = kKSteps<HD>, DT = HD / 16;
   constexpr int TS = 32;  // keys per wave tile
   auto& om = sm.om;
   auto& oml = sm.oml;
 
   // the wave index in a scalar register: per-wave tile bounds and loop exits are then uniform
   // branches rather than exec-masked ones
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // (tid opaque: the lane's offsets are computed here, where they are used; see opaque_v)
+  const int tid = opaque_v(threadIdx.x), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const long head_off = (long)g * HD * a.msl;
   const int head_bytes = HD * a.msl * 2;
@@ -117,7 +130,7 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
     // first tile in flight before q is read
     KvFrag<HD> cur;
     [[maybe_unused]] KvFrag<HD> nxt;
-    load_kv_frag<HD>(kr, vr, a.msl, t0, col, grp, cur);
+    load_kv_frag<HD, COH>(kr, vr, a.msl, t0, col, grp, cur);
 
     // q as the B operand: column col is head col (hi part) or head col - G (lo part); others zero
     u32x4 qf[KS];
@@ -126,12 +139,28 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
       const bool used = col < 2 * G;
       const bool lo = col >= G;
       const int h = used ? (lo ? col - G : col) : 0;
-      const float* qp = a.q + (long)(g * G + h) * HD + 8 * grp;
       f32x4 q4[KS][2];
+      if constexpr (COH) {  // the kv head's G query rows through one descriptor; dims past HD are zero
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.q + (long)g * G * HD), 0, G * HD * (int)sizeof(float), kBufferConfig);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
-        q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
+        for (int ks = 0; ks < KS; ++ks) {
+          const int d = 32 * ks + 8 * grp;
+          const int off = 4 * (h * HD + (d < HD ? d : 0));
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const f32x4 v = load_shared4(qr, off + 16 * hf);
+            q4[ks][hf] = d < HD ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      } else {
+        static_assert(COH || HD % 32 == 0, "head_dim 16 only with coherent (masked) q loads");
+        const float* qp = a.q + (long)(g * G + h) * HD + 8 * grp;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          q4[ks][0] = *reinterpret_cast<const f32x4*>(qp + 32 * ks);
+          q4[ks][1] = *reinterpret_cast<const f32x4*>(qp + 32 * ks + 4);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       issue();
@@ -212,7 +241,7 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
         tile(cur, t0);
         t0 += TS * NW;
         if (t0 >= t_end) break;
-        load_kv_frag<HD>(kr, vr, a.msl, t0, col, grp, cur);
+        load_kv_frag<HD, COH>(kr, vr, a.msl, t0, col, grp, cur);
       }
     } else for (;;) {
       int tn = t0 + TS * NW;
@@ -221,7 +250,7 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
         break;
       }
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
-      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, nxt);
+      load_kv_frag<HD, COH>(kr, vr, a.msl, tn, col, grp, nxt);
       __builtin_amdgcn_sched_barrier(0);
       tile(cur, t0);
       t0 = tn;
@@ -231,7 +260,7 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
         break;
       }
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      load_kv_frag<HD>(kr, vr, a.msl, tn, col, grp, cur);
+      load_kv_frag<HD, COH>(kr, vr, a.msl, tn, col, grp, cur);
       __builtin_amdgcn_sched_barrier(0);
       tile(nxt, t0);
       t0 = tn;
@@ -261,12 +290,12 @@ __device__ __forceinline__ void attn_mfma_waves(const AttnArgs& a, int g, int t_
 }
 
 // One workgroup of NW waves: kv head g, KV slice `split`, all G query heads of g (NB as
-// attn_mfma_waves).
-template <int HD, int G, int NW, int NB = 2>
+// attn_mfma_waves; COH: coherent loads, and the output and the sink keys written through).
+template <int HD, int G, int NW, int NB = 2, bool COH = false>
 __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int split, const Positions& pss,
                                                AttnMfmaSmem<HD, G, NW>& sm) {
   constexpr int NT = 64 * NW;
-  const int tid = threadIdx.x;
+  const int tid = opaque_v(threadIdx.x);
   const int kv_len = pss.kv_len;
   const int chunk = attn_mfma_chunk(kv_len, a.nsplit, a.min_slice);
   const int active = (kv_len + chunk - 1) / chunk;
@@ -274,10 +303,10 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
   const int t_begin = split * chunk;
   const int t_end = min(kv_len, t_begin + chunk);
   if (pss.kv_sink > 0 && split == 0) {
-    rotate_sinks<HD, NT>(a, a.kcache + (long)g * HD * a.msl, pss.kv_sink, tid);
+    rotate_sinks<HD, NT, COH>(a, a.kcache + (long)g * HD * a.msl, pss.kv_sink, tid);
     __syncthreads();
   }
-  attn_mfma_waves<HD, G, NW, NB>(a, g, t_begin, t_end, sm, [] {});
+  attn_mfma_waves<HD, G, NW, NB, COH>(a, g, t_begin, t_end, sm, [] {});
   auto& om = sm.om;
   auto& oml = sm.oml;
 
@@ -296,7 +325,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
       L = fmaf(oml[w][h][1], wt, L);
     }
     if (active == 1 && !a.defer_merge) {
-      a.out[(long)(g * G + h) * HD + d] = O / L;
+      st_act<COH>(a.out + (long)(g * G + h) * HD + d, O / L);
     } else {
       float* dst = a.partial + ((long)(g * G + h) * a.nsplit + split) * stride;
       store_shared(dst + d, O);
@@ -307,7 +336,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnArgs& a, int g, int spl
     }
   }
   if (active == 1 || a.defer_merge) return;
-  attn_merge_slices<HD, G, NT, false>(a, g, active, tid, sm.mrg, sm.Ls, sm.last_flag);
+  attn_merge_slices<HD, G, NT, COH>(a, g, active, tid, sm.mrg, sm.Ls, sm.last_flag);
 }
 
 template <int HD, int G, int NW, int NB = 2>

@@ -150,26 +150,22 @@ __device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ void publish() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait gives up (about a second)
-
-// Thread 0 polls until *c >= target (bounded; a time-out sets the abort flag, after which every
-// wait returns at once and the host reports the error); the workgroup waits at the barrier.
-__device__ __forceinline__ void wait_count(const unsigned* c, unsigned target, unsigned* abort_flag) {
-  if (threadIdx.x == 0) {
-    unsigned spins = 0;
-    while (__hip_atomic_load(const_cast<unsigned*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if ((++spins & 255u) == 0 &&
-          (spins >= kSpinLimit || __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
+// The value, opaque to the compiler: whatever is computed from it is computed where it is used. In
+// the single-launch decode (one loop over the layers) this keeps per-use address arithmetic from
+// being hoisted out of the loop and held, in registers or scratch, across every phase.
+__device__ __forceinline__ int opaque_v(int v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ int opaque_s(int v) {
+  __asm__ volatile("" : "+s"(v));
+  return v;
 }
 
-// Thread 0 polls until *f == value (bounded, as wait_count); the workgroup waits at the barrier.
+constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait gives up (about a second)
+
+// Thread 0 polls until *f == value (bounded: a time-out sets the abort flag, after which every
+// wait returns at once and the host reports the error); the workgroup waits at the barrier.
 __device__ __forceinline__ void wait_flag(const unsigned* f, unsigned value, unsigned* abort_flag) {
   if (threadIdx.x == 0) {
     unsigned spins = 0;
@@ -195,13 +191,8 @@ __device__ __forceinline__ f32x4 load_shared4(__amdgpu_buffer_rsrc_t r, int byte
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
 
-// Activation accesses: plain, or agent-coherent (COH) when a later workgroup of the same launch
+// An activation store: plain, or agent-coherent (COH) when a later workgroup of the same launch
 // consumes the value.
-template <bool COH>
-__device__ __forceinline__ float ld_act(const float* p) {
-  if constexpr (COH) return load_shared(p);
-  else return *p;
-}
 template <bool COH>
 __device__ __forceinline__ void st_act(float* p, float v) {
   if constexpr (COH) store_shared(p, v);
@@ -242,11 +233,9 @@ struct MatvecArgs {
   float qkv_clip;
   uint16_t* kcache;
   uint16_t* vcache;
-  uint32_t* kvcur;       // coherent copy of this position's K/V (fp16 pairs), single-launch decode only
   const StepParams* params;
   int pos;               // position, or -1 to read params->pos
-  const float* rope_cs;  // [head_dim]: (cos, sin) per rotary pair at this step's position, or
-  const float* inv_freq; // [head_dim / 2]: compute that table from the rotary frequencies
+  const float* rope_cs;  // [head_dim]: (cos, sin) per rotary pair at this step's position
   // row-loop statistics for the lm_head: running (max, index) of the outputs, tie rule of
   // src/sampler.cpp:27-38, kept per wave (argmax fused into the last matvec)
   int track_max;
@@ -303,29 +292,29 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 // flow simple.
 // Operands an epilogue needs from memory, loaded together with the group's weights so that their
 // latency is not paid at the end of the group.
-template <int R, EpiKind EPI, bool COH>
+template <int R, EpiKind EPI>
 __device__ __forceinline__ void epilogue_prefetch(const MatvecArgs& a, int p, float (&pre)[R]) {
   if constexpr (EPI == kEpiResidual) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) pre[r] = ld_act<COH>(a.out + (long)p * R + r);
+    for (int r = 0; r < R; ++r) pre[r] = a.out[(long)p * R + r];
   }
 }
 
-template <int R, EpiKind EPI, bool COH>
+template <int R, EpiKind EPI>
 __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float (&acc)[R], const float (&pre)[R],
                                          int pos, const float* rope_cs, bool store) {
   if constexpr (EPI == kEpiStore) {
     if (store)
 #pragma unroll
-      for (int r = 0; r < R; ++r) st_act<COH>(a.out + (long)p * R + r, acc[r]);
+      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = acc[r];
   } else if constexpr (EPI == kEpiResidual) {
     if (store)
 #pragma unroll
-      for (int r = 0; r < R; ++r) st_act<COH>(a.out + (long)p * R + r, pre[r] + acc[r]);
+      for (int r = 0; r < R; ++r) a.out[(long)p * R + r] = pre[r] + acc[r];
   } else if constexpr (EPI == kEpiSwiGLU) {
     const float h = a.act == 1 ? silu(acc[0]) : gelu(acc[0]);
     const float v = h * acc[R - 1];
-    if (store) st_act<COH>(a.out + p, v);
+    if (store) a.out[p] = v;
   } else {  // kEpiQkvRope: rows i = 2p, 2p+1 of [Wq; Wk; Wv]  (reference src/infer.cpp:279-305)
     const int i = 2 * p;
     float v0 = clipf(acc[0], a.qkv_clip);
@@ -341,13 +330,8 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
     }
     if (!store) return;
     if (i < a.q_dim) {
-      if (COH) {
-        store_shared(a.out + i, v0);
-        store_shared(a.out + i + 1, v1);
-      } else {
-        a.out[i] = v0;
-        a.out[i + 1] = v1;
-      }
+      a.out[i] = v0;
+      a.out[i + 1] = v1;
     } else {
       const Positions ps = positions(pos, a.msl);
       const bool is_k = i < a.q_dim + a.kv_dim;
@@ -356,8 +340,6 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
       const long head = (long)g * a.head_dim * a.msl;
       const uint16_t h0 = __builtin_bit_cast(uint16_t, (f16)v0);  // RNE, as _cvtss_sh(x, 0)
       const uint16_t h1 = __builtin_bit_cast(uint16_t, (f16)v1);
-      if constexpr (COH)  // the same launch's attention reads this position from the side buffer
-        store_shared_u32(a.kvcur + (is_k ? 0 : a.kv_dim / 2) + ik / 2, (uint32_t)h0 | ((uint32_t)h1 << 16));
       if (is_k) {
         a.kcache[head + k_cache_idx(j, ps.kv_pos, a.msl)] = h0;
         a.kcache[head + k_cache_idx(j + 1, ps.kv_pos, a.msl)] = h1;
@@ -369,101 +351,45 @@ __device__ __forceinline__ void epilogue(const MatvecArgs& a, int p, const float
   }
 }
 
-template <bool COH>
-__device__ __forceinline__ float stage_src(const MatvecArgs& a, const uint16_t* x16, int i) {
-  if (x16) return (float)__builtin_bit_cast(f16, x16[i]);
-  return ld_act<COH>(a.x + i);
-}
-
 // Stage the (optionally RMS-normalised) input vector into LDS: xs[i] = x[i] * inv * g[i] with
-// inv = 1/sqrt(mean(x^2) + eps) (reference src/infer.cpp:136-146). NPT > 0: K == 1024*NPT, i.e.
-// exactly NPT float4 per thread, all loads issued before the first use; NPT == 0: any K % 4 == 0.
-// The step's RoPE table (head_dim floats) goes to LDS right after the vector.
-template <int NPT, bool COH>
-__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red, int pos, const uint16_t* x16) {
-  if (a.rope_cs) {
+// inv = 1/sqrt(mean(x^2) + eps) (reference src/infer.cpp:136-146), for any K % 4 == 0 (the
+// unrolled kernels stage through stage_load / stage_store below). x16: the fp16 embedding row as
+// the input instead of x. The step's RoPE table (head_dim floats) goes to LDS right after the vector.
+__device__ __forceinline__ void stage_input(const MatvecArgs& a, float* xs, float* red, const uint16_t* x16) {
+  if (a.rope_cs)
     for (int i = threadIdx.x; i < a.head_dim; i += kBlock) xs[a.K + i] = a.rope_cs[i];
-  } else if (a.inv_freq) {  // reference src/infer.cpp:205-208
-    for (int k = threadIdx.x; k < a.head_dim / 2; k += kBlock) {
-      const float ang = (float)pos * a.inv_freq[k];
-      xs[a.K + 2 * k] = cosf(ang);
-      xs[a.K + 2 * k + 1] = sinf(ang);
-    }
-  }
   f32x4* o4 = reinterpret_cast<f32x4*>(xs);
-  if constexpr (NPT > 0) {
-    f32x4 xv[NPT], gv[NPT];
-    if (!COH && !x16) {
-      const f32x4* x4 = reinterpret_cast<const f32x4*>(a.x);
-#pragma unroll
-      for (int k = 0; k < NPT; ++k) xv[k] = x4[threadIdx.x + kBlock * k];
-    } else if (!x16) {
-      const __amdgpu_buffer_rsrc_t xr =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, a.K * (int)sizeof(float), kBufferConfig);
-#pragma unroll
-      for (int k = 0; k < NPT; ++k) xv[k] = load_shared4(xr, 16 * (threadIdx.x + kBlock * k));
+  const int n4 = a.K >> 2;
+  auto src4 = [&](int i) {
+    f32x4 v;
+    if (!x16) {
+      v = reinterpret_cast<const f32x4*>(a.x)[i];
     } else {
 #pragma unroll
-      for (int k = 0; k < NPT; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xv[k][e] = stage_src<COH>(a, x16, 4 * (threadIdx.x + kBlock * k) + e);
+      for (int e = 0; e < 4; ++e) v[e] = (float)__builtin_bit_cast(f16, x16[4 * i + e]);
     }
-    if (a.gain) {
-      const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
-#pragma unroll
-      for (int k = 0; k < NPT; ++k) gv[k] = g4[threadIdx.x + kBlock * k];
-      float ss = 0.f;
-#pragma unroll
-      for (int k = 0; k < NPT; ++k)
-        ss += xv[k][0] * xv[k][0] + xv[k][1] * xv[k][1] + xv[k][2] * xv[k][2] + xv[k][3] * xv[k][3];
-      ss = block_sum(ss, red);
-      const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-#pragma unroll
-      for (int k = 0; k < NPT; ++k) {
-        f32x4 o;
-        o[0] = xv[k][0] * inv * gv[k][0];
-        o[1] = xv[k][1] * inv * gv[k][1];
-        o[2] = xv[k][2] * inv * gv[k][2];
-        o[3] = xv[k][3] * inv * gv[k][3];
-        o4[threadIdx.x + kBlock * k] = o;
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < NPT; ++k) o4[threadIdx.x + kBlock * k] = xv[k];
+    return v;
+  };
+  if (a.gain) {
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+      f32x4 v = src4(i);
+      ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+      f32x4 v = src4(i), g = g4[i];
+      f32x4 o;
+      o[0] = v[0] * inv * g[0];
+      o[1] = v[1] * inv * g[1];
+      o[2] = v[2] * inv * g[2];
+      o[3] = v[3] * inv * g[3];
+      o4[i] = o;
     }
   } else {
-    const int n4 = a.K >> 2;
-    auto src4 = [&](int i) {
-      f32x4 v;
-      if (!COH && !x16) {
-        v = reinterpret_cast<const f32x4*>(a.x)[i];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = stage_src<COH>(a, x16, 4 * i + e);
-      }
-      return v;
-    };
-    if (a.gain) {
-      const f32x4* g4 = reinterpret_cast<const f32x4*>(a.gain);
-      float ss = 0.f;
-      for (int i = threadIdx.x; i < n4; i += kBlock) {
-        f32x4 v = src4(i);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-      }
-      ss = block_sum(ss, red);
-      const float inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-      for (int i = threadIdx.x; i < n4; i += kBlock) {
-        f32x4 v = src4(i), g = g4[i];
-        f32x4 o;
-        o[0] = v[0] * inv * g[0];
-        o[1] = v[1] * inv * g[1];
-        o[2] = v[2] * inv * g[2];
-        o[3] = v[3] * inv * g[3];
-        o4[i] = o;
-      }
-    } else {
-      for (int i = threadIdx.x; i < n4; i += kBlock) o4[i] = src4(i);
-    }
+    for (int i = threadIdx.x; i < n4; i += kBlock) o4[i] = src4(i);
   }
   __syncthreads();
 }
@@ -511,8 +437,6 @@ __device__ __forceinline__ void stage_load(const MatvecArgs& a, StagedInput<NPT,
 template <int NPT, bool GAIN, bool EMB>
 __device__ __forceinline__ void stage_store(const MatvecArgs& a, StagedInput<NPT, GAIN, EMB>& st, float* xs, float* red,
                                             int pos, const uint16_t* x16) {
-  // the RoPE table comes precomputed (rope_cs); the per-launch cos/sin form (inv_freq) belongs to
-  // the single-launch path, which stages through stage_input
   if (a.rope_cs && (int)threadIdx.x < a.head_dim) xs[a.K + threadIdx.x] = st.rc;
   if (EMB && x16) {
 #pragma unroll
@@ -561,13 +485,11 @@ __device__ __forceinline__ void track_rows(const MatvecArgs& a, int p, const flo
   }
 }
 
-// The fused matvec over groups p = blk*4 + wave + k*(nblk*4). `wait()` runs after the first
-// group's weight loads are issued and before anything that reads activations (the single-launch
-// decode waits there for the producing phase); COH selects coherent activation accesses.
+// The fused matvec over groups p = blk*4 + wave + k*(nblk*4).
 // KC > 0: K == 512*KC*H, fully unrolled row streaming. KC == 0: any K % 8 == 0.
 // H == 2 (R == 1 only): each row is streamed as two pieces of K/2 (see below).
-template <int KC, int R, EpiKind EPI, bool COH, int H = 1, class Wait>
-__device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int nblk, float* lds, Wait wait) {
+template <int KC, int R, EpiKind EPI, int H = 1>
+__device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int nblk, float* lds) {
   float* red = lds;      // kWavesPerBlock floats (padded to 16)
   float* xs = lds + 16;  // K floats (+ the RoPE table)
   const int lane = threadIdx.x & (kWave - 1);
@@ -580,10 +502,10 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
   if (a.emb) {
     x16 = a.emb + (long)(a.token >= 0 ? a.token : a.params->token) * a.K;
     if (a.emb_out && blk == 0)
-      for (int i = threadIdx.x; i < a.K; i += kBlock) st_act<COH>(a.emb_out + i, (float)__builtin_bit_cast(f16, x16[i]));
+      for (int i = threadIdx.x; i < a.K; i += kBlock) a.emb_out[i] = (float)__builtin_bit_cast(f16, x16[i]);
   }
 
-  static_assert(H == 1 || (H == 2 && R == 1 && KC > 0 && !COH), "two-piece rows: one row per group, unrolled");
+  static_assert(H == 1 || (H == 2 && R == 1 && KC > 0), "two-piece rows: one row per group, unrolled");
   if constexpr (H == 2) {
     // Long rows (W2: 28 KB) in two pieces through the two register buffers: piece 0 of a group in
     // wa, piece 1 in wb, so each buffer holds half a row and the pair fits the register file with
@@ -602,13 +524,12 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       group_rows<1>(a, valid ? p0 + i * wave_stride : 0, rows);
       rows[0] += piece * half;
       load_group_uniform<KC, 1>(wv, rows, lane, valid);
-      if (piece == 1) epilogue_prefetch<1, EPI, COH>(a, p0 + i * wave_stride, pre);
+      if (piece == 1) epilogue_prefetch<1, EPI>(a, p0 + i * wave_stride, pre);
     };
     StagedInput<KC, kEpiGain<EPI>, kEpiEmb<EPI>> st;  // K = 1024*KC -> KC float4 per thread
     stage_load(a, st, x16);
     __builtin_amdgcn_sched_barrier(0);
     issue(wa, 0, 0, n > 0);  // unconditional: a branch here would make the staging wait for it
-    wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
     stage_store(a, st, xs, red, pos, x16);
     float carry = 0.f;
@@ -626,7 +547,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       }
       float accs[1] = {wave_sum(carry + acc)};
       const int pg = p0 + i * wave_stride;
-      epilogue<1, EPI, COH>(a, pg, accs, pre, pos, xs + a.K, lane == 0);
+      epilogue<1, EPI>(a, pg, accs, pre, pos, xs + a.K, lane == 0);
       track_rows<1, EPI>(a, pg, accs, mx);
     };
     int i = 0;
@@ -644,7 +565,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       use(wa, i, 0);
       use(wb, i, 1);
     }
-  } else if constexpr (KC > 0 && !COH) {
+  } else if constexpr (KC > 0) {
     // Two register buffers, one group in flight: group i + 1's loads are issued as soon as group
     // i's have landed and before group i's dot products, reduction and epilogue, so a wave's
     // arithmetic overlaps its next memory round trip. (Two groups in flight per wave measured
@@ -661,13 +582,12 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       const int g = valid ? p0 + i * wave_stride : 0;
       group_rows<R>(a, g, rows);
       load_group_uniform<KC, R>(wv, rows, lane, valid);
-      epilogue_prefetch<R, EPI, COH>(a, g, pre);
+      epilogue_prefetch<R, EPI>(a, g, pre);
     };
     StagedInput<KC / 2, kEpiGain<EPI>, kEpiEmb<EPI>> st;  // K = 512*KC -> KC/2 float4 per thread
     stage_load(a, st, x16);
     __builtin_amdgcn_sched_barrier(0);
     issue(wa, prea, 0, n > 0);  // unconditional: a branch here would make the staging wait for it
-    wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
     stage_store(a, st, xs, red, pos, x16);
     auto use = [&](const u32x4 (&wv)[R][KC], const float (&pre)[R], int i) {
@@ -683,7 +603,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      epilogue<R, EPI, COH>(a, pg, acc, pre, pos, xs + a.K, lane == 0);
+      epilogue<R, EPI>(a, pg, acc, pre, pos, xs + a.K, lane == 0);
       track_rows<R, EPI>(a, pg, acc, mx);
     };
     int i = 0;
@@ -703,56 +623,15 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
     } else if (i + 1 == n) {
       use(wa, prea, i);
     }
-  } else if constexpr (KC > 0) {
-    // One register buffer: the first group's loads are in flight while the workgroup stages x
-    // (every wave takes part in the staging barrier); each later group is loaded at the end of
-    // the previous iteration, after its registers are dead.
-    u32x4 wv[R][KC];
-    float pre[R];
-    if (p < a.groups) {
-      const uint16_t* rows[R];
-      group_rows<R>(a, p, rows);
-      load_group<KC, R>(wv, rows, lane);
-      if (!COH) epilogue_prefetch<R, EPI, COH>(a, p, pre);
-    }
-    wait();
-    const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
-    if (COH && p < a.groups) epilogue_prefetch<R, EPI, COH>(a, p, pre);
-    stage_input<KC / 2, COH>(a, xs, red, pos, x16);  // K = 512*KC -> K/4/256 = KC/2 float4 per thread
-    while (p < a.groups) {
-      float acc[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = 0.f;
-#pragma unroll
-      for (int u = 0; u < KC; ++u) {
-        // one 8-float slice of x serves all R rows; a scheduling fence every 4 slices bounds how
-        // many LDS reads the compiler hoists (each hoisted slice costs 8 VGPRs)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = dot8(wv[r][u], xs + 8 * (lane + kWave * u), acc[r]);
-        if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      epilogue<R, EPI, COH>(a, p, acc, pre, pos, xs + a.K, lane == 0);
-      track_rows<R, EPI>(a, p, acc, mx);
-      p += wave_stride;
-      if (p < a.groups) {
-        const uint16_t* rows[R];
-        group_rows<R>(a, p, rows);
-        load_group<KC, R>(wv, rows, lane);
-        epilogue_prefetch<R, EPI, COH>(a, p, pre);
-      }
-    }
   } else {
-    wait();
     const int pos = EPI == kEpiQkvRope ? (a.pos >= 0 ? a.pos : a.params->pos) : 0;
-    stage_input<0, COH>(a, xs, red, pos, x16);
+    stage_input(a, xs, red, x16);
     const int nch = a.K >> 3;
     for (; p < a.groups; p += wave_stride) {
       const uint16_t* rows[R];
       group_rows<R>(a, p, rows);
       float pre[R];
-      epilogue_prefetch<R, EPI, COH>(a, p, pre);
+      epilogue_prefetch<R, EPI>(a, p, pre);
       float acc[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -765,7 +644,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-      epilogue<R, EPI, COH>(a, p, acc, pre, pos, xs + a.K, lane == 0);
+      epilogue<R, EPI>(a, p, acc, pre, pos, xs + a.K, lane == 0);
       track_rows<R, EPI>(a, p, acc, mx);
     }
   }
@@ -775,59 +654,7 @@ __device__ __forceinline__ RowMax matvec_body(const MatvecArgs& a, int blk, int 
 template <int KC, int R, EpiKind EPI, int H = 1>
 __global__ void __launch_bounds__(kBlock) matvec_kernel(MatvecArgs a) {
   extern __shared__ float lds[];
-  matvec_body<KC, R, EPI, false, H>(a, blockIdx.x, gridDim.x, lds, [] {});
-}
-
-// (max, index) over the lanes of a wave, then over the waves of the workgroup; tie rule of
-// reference src/sampler.cpp:27-38 (first index of the maximum). Every thread gets the result.
-__device__ __forceinline__ RowMax block_best(RowMax m, float* sv, int* si) {
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(m.v, o, kWave);
-    const int oi = __shfl_xor(m.i, o, kWave);
-    better(m.v, m.i, ov, oi);
-  }
-  if (lane == 0) {
-    sv[wave] = m.v;
-    si[wave] = m.i;
-  }
-  __syncthreads();
-  RowMax r;
-  r.v = sv[0];
-  r.i = si[0];
-  for (int w = 1; w < kWavesPerBlock; ++w) better(r.v, r.i, sv[w], si[w]);
-  __syncthreads();
-  return r;
-}
-
-// Per-workgroup (max, index) of a matvec's outputs combined into the argmax: workgroup `slot` of
-// `nslots` posts its best, the last to post (ticket) reduces all of them and zeroes the ticket for
-// the next launch.
-__device__ __forceinline__ void argmax_finish(RowMax mx, int slot, int nslots, float* best_v, int* best_i,
-                                              unsigned* ticket, int* result) {
-  __shared__ float sv[kWavesPerBlock];
-  __shared__ int si[kWavesPerBlock];
-  __shared__ unsigned last;
-  const int tid = threadIdx.x;
-  const RowMax b = block_best(mx, sv, si);
-  if (tid == 0) {
-    store_shared(best_v + slot, b.v);
-    __hip_atomic_store(best_i + slot, b.i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    publish();
-    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = t == (unsigned)(nslots - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last) return;
-  RowMax m;
-  for (int s = tid; s < nslots; s += kBlock)
-    better(m.v, m.i, load_shared(best_v + s), __hip_atomic_load(best_i + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  const RowMax r = block_best(m, sv, si);
-  if (tid == 0) {
-    result[0] = r.i == 0x7fffffff ? 0 : r.i;
-    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  matvec_body<KC, R, EPI, H>(a, blockIdx.x, gridDim.x, lds);
 }
 
 // Packed (logit, index) whose unsigned order is the argmax order with the reference's tie rule
@@ -863,7 +690,7 @@ __device__ __forceinline__ void argmax_post(RowMax mx, unsigned long long* key) 
 template <int KC>
 __global__ void __launch_bounds__(kBlock) lm_head_argmax_kernel(MatvecArgs a, unsigned long long* key) {
   extern __shared__ float lds[];
-  const RowMax mx = matvec_body<KC, 2, kEpiStore, false>(a, blockIdx.x, gridDim.x, lds, [] {});
+  const RowMax mx = matvec_body<KC, 2, kEpiStore>(a, blockIdx.x, gridDim.x, lds);
   argmax_post(mx, key);
 }
 
@@ -977,8 +804,7 @@ struct AttnGeom {
   static_assert(DPT >= 1 && NDG * DPT == HD && LPD <= kWave, "attention tile layout");
 };
 
-// LDS of one attention workgroup. kcur/vcur hold the current token's fp16 K and V of the head
-// (used by the single-launch decode, which reads them from a coherent side buffer).
+// LDS of one attention workgroup.
 constexpr int kMaxSplits = 64;  // KV slices per kv head (the partial buffer holds this many)
 
 template <int HD, int G, int NT>
@@ -987,8 +813,6 @@ struct AttnSmem {
   __attribute__((aligned(16))) float ps[G][AttnGeom<HD, NT>::TT];
   float red[2][G][NT / kWave];
   float mrg[G][kMaxSplits][2];  // merge: per slice (weight, sum), then 1/L per head in red
-  __attribute__((aligned(16))) uint32_t kcur[HD / 2];
-  uint32_t vcur[HD / 2];
   unsigned last_flag;
 };
 
@@ -1002,6 +826,7 @@ template <int HD, int G, int NT, bool COH>
 __device__ __forceinline__ void attn_merge_slices(const AttnArgs& a, int g, int active, int tid,
                                                   float (&mrg)[G][kMaxSplits][2], float* Ls, unsigned& last_flag) {
   const int stride = HD + 2;
+  tid = opaque_v(tid);
   publish();
   __syncthreads();
   if (tid == 0) {
@@ -1089,8 +914,10 @@ __device__ __forceinline__ void attn_merge_slices(const AttnArgs& a, int g, int 
 }
 
 // Re-rotates the K of the sink tokens r < kv_sink by angle freq*1 in place, fp16 round trip as
-// the reference (src/infer.cpp:307-325); kh is the kv head's K cache.
-template <int HD, int NT>
+// the reference (src/infer.cpp:307-325); kh is the kv head's K cache. COH: the entries are read
+// and written with agent-coherent accesses and written through before the function returns (the
+// caller's coherent K loads then see them).
+template <int HD, int NT, bool COH = false>
 __device__ __forceinline__ void rotate_sinks(const AttnArgs& a, uint16_t* kh, int kv_sink, int tid) {
   for (int e = tid; e < kv_sink * (HD / 2); e += NT) {
     const int r = e / (HD / 2);
@@ -1099,10 +926,26 @@ __device__ __forceinline__ void rotate_sinks(const AttnArgs& a, uint16_t* kh, in
     const float c = cosf(freq), s = sinf(freq);
     uint16_t* p0 = kh + k_cache_idx(j, r, a.msl);
     uint16_t* p1 = kh + k_cache_idx(j + 1, r, a.msl);
-    const float v0 = (float)__builtin_bit_cast(f16, *p0), v1 = (float)__builtin_bit_cast(f16, *p1);
-    *p0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
-    *p1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
+    uint16_t h0, h1;
+    if constexpr (COH) {
+      h0 = __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      h1 = __hip_atomic_load(p1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      h0 = *p0;
+      h1 = *p1;
+    }
+    const float v0 = (float)__builtin_bit_cast(f16, h0), v1 = (float)__builtin_bit_cast(f16, h1);
+    const uint16_t r0 = __builtin_bit_cast(uint16_t, (f16)(v0 * c - v1 * s));
+    const uint16_t r1 = __builtin_bit_cast(uint16_t, (f16)(v0 * s + v1 * c));
+    if constexpr (COH) {
+      __hip_atomic_store(p0, r0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p1, r1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      *p0 = r0;
+      *p1 = r1;
+    }
   }
+  if constexpr (COH) publish();
 }
 
 // K and V registers for one tile of one thread (loaded one tile ahead of use).
@@ -1115,16 +958,11 @@ struct AttnTileRegs {
 // One attention workgroup: kv head g, KV slice `split`, all G query heads of g; tid is the thread
 // index (passed in so that a caller's loop can keep lane-derived values from being hoisted).
 // HD: head_dim; G: query heads per kv head; NT: threads.
-// COH: q is read and the output written with agent-coherent accesses (a later workgroup of the
-// same launch consumes it). SIDE_KV: the current token's K/V (position kv_pos, written by other
-// workgroups of the same launch) is taken from `kvcur` ([K pairs | V pairs] as packed fp16x2,
-// coherent) instead of the cache.
 // Partial sums stay per lane and are reduced over the LPD lanes once, after the last tile. Every
 // tile issues the same loads (addresses clamped into the cache, results masked), so the compiler
 // waits only for the tile it is about to use.
-template <int HD, int G, int NT, bool COH, bool SIDE_KV>
-__device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, int pos, AttnSmem<HD, G, NT>& sm,
-                                         const uint32_t* kvcur, int tid) {
+template <int HD, int G, int NT>
+__device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, int pos, AttnSmem<HD, G, NT>& sm, int tid) {
   using Geo = AttnGeom<HD, NT>;
   constexpr int LPT = Geo::LPT, CPL = Geo::CPL, TT = Geo::TT, LPD = Geo::LPD, NDG = Geo::NDG, DPT = Geo::DPT;
   constexpr int NW = Geo::NW;
@@ -1150,8 +988,6 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
   const int oct = tid % LPD, dgrp = tid / LPD;
   const bool vec_ok = (a.msl & 7) == 0;
   const int vmax = vec_ok ? a.msl - 8 : 0;
-  const int kvp = pss.kv_pos;
-  const uint16_t* vcur_h = reinterpret_cast<const uint16_t*>(sm.vcur);
 
   auto load_tile = [&](int t0, AttnTileRegs<CPL, DPT>& r) {
     const int tok = min(t0 + tok_l, a.msl - 1);
@@ -1179,19 +1015,11 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
       const int e = min(tid + i * NT, G * HD - 1);
-      if constexpr (COH) qv[i] = load_shared(a.q + (long)g * G * HD + e);
-      else qv[i] = a.q[(long)g * G * HD + e];
+      qv[i] = a.q[(long)g * G * HD + e];
     }
 #pragma unroll
     for (int i = 0; i < QPT; ++i)
       if (tid + i * NT < G * HD) sm.qs[tid + i * NT] = qv[i];
-  }
-  if constexpr (SIDE_KV) {
-    for (int e = tid; e < HD / 2; e += NT) {
-      sm.kcur[e] = __hip_atomic_load(kvcur + g * (HD / 2) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm.vcur[e] = __hip_atomic_load(kvcur + (a.n_kv_heads + g) * (HD / 2) + e, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-    }
   }
   float m_run[G], l_run[G], acc[DPT][G];
 #pragma unroll
@@ -1209,28 +1037,6 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
     const int tok = t0 + tok_l;
     const bool valid = tok < t_end;
     const int tv = t0 + 8 * oct;
-    if constexpr (SIDE_KV) {
-      if (kvp >= t0 && kvp < t0 + TT) {  // this tile holds the current token: take it from the side buffer
-        if (tok == kvp) {
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(sm.kcur + (sub * CPL + cc) * 8);
-            cur.k[cc][0] = src[0];
-            cur.k[cc][1] = src[1];
-          }
-        }
-        if (kvp >= tv && kvp < tv + 8) {
-#pragma unroll
-          for (int m = 0; m < DPT; ++m) {
-            f16x8 v8 = __builtin_bit_cast(f16x8, cur.v[m]);
-            const f16 vc = __builtin_bit_cast(f16, vcur_h[dgrp + NDG * m]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v8[e] = (kvp - tv == e) ? vc : v8[e];  // no dynamic register index
-            cur.v[m] = __builtin_bit_cast(u32x4, v8);
-          }
-        }
-      }
-    }
     // scores: partial dots over this lane's chunks, then summed over the LPT lanes of the token
     float s[G];
 #pragma unroll
@@ -1312,10 +1118,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
 #pragma unroll
           for (int m = 0; m < DPT; ++m) {
             const int d = dgrp + NDG * m;
-            float v = (float)__builtin_bit_cast(f16, vh[(long)d * a.msl + t]);
-            if constexpr (SIDE_KV) {
-              if (t == kvp) v = (float)__builtin_bit_cast(f16, vcur_h[d]);
-            }
+            const float v = (float)__builtin_bit_cast(f16, vh[(long)d * a.msl + t]);
 #pragma unroll
             for (int h = 0; h < G; ++h) acc[m][h] = fmaf(sm.ps[h][8 * oct + e], v, acc[m][h]);
           }
@@ -1338,9 +1141,7 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
       for (int m = 0; m < DPT; ++m)
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          float* o = a.out + (long)(g * G + h) * HD + dgrp + NDG * m;
-          if constexpr (COH) store_shared(o, acc[m][h] / l_run[h]);
-          else *o = acc[m][h] / l_run[h];
+          a.out[(long)(g * G + h) * HD + dgrp + NDG * m] = acc[m][h] / l_run[h];
         }
     return;
   }
@@ -1361,14 +1162,14 @@ __device__ __forceinline__ void attn_run(const AttnArgs& a, int g, int split, in
         store_shared(dst + HD + 1, l_run[h]);
       }
   }
-  attn_merge_slices<HD, G, NT, COH>(a, g, active, tid, sm.mrg, &sm.red[0][0][0], sm.last_flag);
+  attn_merge_slices<HD, G, NT, false>(a, g, active, tid, sm.mrg, &sm.red[0][0][0], sm.last_flag);
 }
 
 // Split-KV attention as its own launch: grid (n_kv_heads, nsplit) of 256-thread workgroups.
 template <int HD, int G>
 __global__ void __launch_bounds__(kBlock) attention_kernel(AttnArgs a) {
   __shared__ AttnSmem<HD, G, kBlock> sm;
-  attn_run<HD, G, kBlock, false, false>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, nullptr, threadIdx.x);
+  attn_run<HD, G, kBlock>(a, blockIdx.x, blockIdx.y, a.params->pos, sm, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------

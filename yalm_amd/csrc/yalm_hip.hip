@@ -138,16 +138,16 @@ struct yhip_ctx {
   float* rowovf = nullptr;               // [dim] their fp32 side sums of out-of-range partials (zero between launches)
 
   // single-launch decode (decode_flow.h)
-  const void* flow_fn = nullptr;  // instantiation for this shape, or null when the shape has none
-  size_t flow_lds = 0;
+  const void* step_fn = nullptr;       // instantiation for this shape (attention and O as two phases), or null
+  const void* step_fn_atto = nullptr;  // the same with attention and O as one phase (short contexts)
   bool use_flow = false;
-  unsigned flow_launches = 0;
-  int flow_bpc = 2, flow_bpc_w2 = 1;  // workgroups per CU of the matvec phases (W2 separately)
+  unsigned step_launches = 0;
+  unsigned step_base = 0;  // arrival-flag value before the next launch (flags count up across launches)
   LayerLayout layout{};       // weight and KV addresses of every layer
-  unsigned* sync = nullptr;   // flow_sync_words(n_layers)
-  uint32_t* kvcur = nullptr;  // current position's K/V as fp16 pairs
-  float* best_v = nullptr;
-  int* best_i = nullptr;
+  unsigned* sync = nullptr;   // kSyncWords: abort word, arrival flags
+  unsigned long long* step_keys = nullptr;  // [2] packed argmax keys (by launch parity)
+  // attention and the O projection as one phase of the single launch up to this many keys (0: never)
+  int step_atto_max = 192;
 
   // batched prefill workspace (grown on demand, prefill.h)
   int pf_cap = 0;
@@ -226,7 +226,7 @@ int default_bpc(int K, int kind = -1) {
 template <int KC, int R, EpiKind EPI, int H = 1>
 void launch_mv(const MatvecArgs& a, int blocks, hipStream_t s) {
   // reduction scratch + input vector (+ the RoPE table for the QKV epilogue)
-  const size_t lds = (16 + (size_t)a.K + (a.rope_cs || a.inv_freq ? (size_t)a.head_dim : 0)) * sizeof(float);
+  const size_t lds = (16 + (size_t)a.K + (a.rope_cs ? (size_t)a.head_dim : 0)) * sizeof(float);
   hipLaunchKernelGGL((matvec_kernel<KC, R, EPI, H>), dim3(blocks), dim3(kBlock), lds, s, a);
 }
 
@@ -265,7 +265,7 @@ int launch_matvec(yhip_ctx* ctx, MatvecArgs a, int kind, int R, int num_cus, hip
   if (R != 1 && R != 2) return fail(ctx, YHIP_EINVAL, "matvec: R must be 1 or 2");
   if (kind == kEpiResidual && (a.gain || a.emb)) return fail(ctx, YHIP_EINVAL, "matvec: the residual epilogue takes no gain or embedding input");
   if (kind == kEpiSwiGLU && a.emb) return fail(ctx, YHIP_EINVAL, "matvec: the SwiGLU epilogue takes no embedding input");
-  if (a.inv_freq && !a.rope_cs) return fail(ctx, YHIP_EINVAL, "matvec: the RoPE epilogue takes a precomputed table (rope_cs)");
+  if (kind == kEpiQkvRope && !a.rope_cs) return fail(ctx, YHIP_EINVAL, "matvec: the RoPE epilogue takes a precomputed table (rope_cs)");
   if (bpc <= 0) bpc = default_bpc(a.K, kind);
   int blocks = (a.groups + kWavesPerBlock - 1) / kWavesPerBlock;
   blocks = std::max(1, std::min(blocks, num_cus * bpc));
@@ -595,34 +595,40 @@ void drop_graphs(yhip_ctx* ctx) {
 }
 
 // ---- single-launch decode ---------------------------------------------------------------------
-// Instantiations of decode_flow_kernel (head_dim, query heads per kv head): the Mistral-7B shape
-// and the small test shapes; other shapes run the per-op kernels.
-const void* select_flow_kernel(const yhip_config& c) {
-  if (c.vocab_size % 2 || c.n_kv_heads <= 0) return nullptr;
+// Instantiations of decode_step_kernel (head_dim, query heads per kv head, 1 KB loads per piece of
+// a dim-long row and of half a hidden-long row): the Mistral-7B shape and the small test shapes;
+// other shapes run the per-op kernels.
+const void* select_step_kernel(const yhip_config& c, int q_dim, bool atto) {
+  // the MFMA attention's 16-byte V reads need max_seq_len % 8 == 0 (keys past the context are read
+  // clamped and masked, so 32-key tiles need no further alignment)
+  if (c.vocab_size % 2 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.max_seq_len % 8 || c.dim % 8 ||
+      c.hidden_dim % 16 || q_dim % 8 || c.n_layers * kPhasesPerLayer + 1 >= kStepPhaseStride)
+    return nullptr;
   const int G = c.n_heads / c.n_kv_heads;
-  if (c.head_dim == 128 && G == 4) return reinterpret_cast<const void*>(&decode_flow_kernel<128, 4>);
-  if (c.head_dim == 32 && G == 4) return reinterpret_cast<const void*>(&decode_flow_kernel<32, 4>);
-  if (c.head_dim == 16 && G == 2) return reinterpret_cast<const void*>(&decode_flow_kernel<16, 2>);
+  const int pld = (2 * std::max(c.dim, q_dim) + 1023) / 1024, plh = (c.hidden_dim + 1023) / 1024;
+#define YK_STEP_KERNEL(HD, G, PLD, PLH)                                                                    \
+  (atto ? reinterpret_cast<const void*>(&decode_step_kernel<HD, G, PLD, PLH, true>)                           \
+        : reinterpret_cast<const void*>(&decode_step_kernel<HD, G, PLD, PLH, false>))
+  if (c.head_dim == 128 && G == 4 && pld == 8 && plh == 14) return YK_STEP_KERNEL(128, 4, 8, 14);
+  if (c.head_dim == 32 && G == 4 && pld == 1 && plh == 1) return YK_STEP_KERNEL(32, 4, 1, 1);
+  if (c.head_dim == 16 && G == 2 && pld == 1 && plh == 1) return YK_STEP_KERNEL(16, 2, 1, 1);
+#undef YK_STEP_KERNEL
   return nullptr;
 }
 
-size_t attn_smem_bytes(int hd, int G) {
-  switch (hd * 16 + G) {
-    case 128 * 16 + 4: return sizeof(AttnSmem<128, 4, kBlock>);
-    case 32 * 16 + 4: return sizeof(AttnSmem<32, 4, kBlock>);
-    case 16 * 16 + 2: return sizeof(AttnSmem<16, 2, kBlock>);
-    default: return 0;
-  }
-}
-
-// Workgroups of a matvec phase: the per-op kernels' grid for the same rows (`bpc` per CU).
-int phase_blocks(int groups, int num_cus, int bpc) {
-  return std::max(1, std::min((groups + kWavesPerBlock - 1) / kWavesPerBlock, num_cus * bpc));
+// Arrival flags and argmax keys back to zero (context creation, and after an aborted launch).
+int reset_step_sync(yhip_ctx* ctx) {
+  HIP_TRY(ctx, hipMemsetAsync(ctx->sync, 0, (size_t)kSyncWords * sizeof(unsigned), ctx->stream));
+  HIP_TRY(ctx, hipMemsetAsync(ctx->step_keys, 0, 2 * sizeof(unsigned long long), ctx->stream));
+  ctx->step_base = 0;
+  return YHIP_OK;
 }
 
 int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   const yhip_config& c = ctx->c;
-  FlowArgs d;
+  if (ctx->step_base > 0x7fffffffu - 2u * kStepPhaseStride)  // flag values stay far from wrapping
+    if (int rc = reset_step_sync(ctx)) return rc;
+  StepArgs d;
   memset(&d, 0, sizeof(d));
   d.layers = ctx->layout;
   d.embed = ctx->embed;
@@ -636,17 +642,15 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.logits = ctx->logits;
   d.partial = ctx->partial;
   d.tickets = ctx->tickets;
-  d.kvcur = ctx->kvcur;
+  d.rowacc = ctx->rowacc;
+  d.rowovf = ctx->rowovf;
   d.sync = ctx->sync;
-  d.best_v = ctx->best_v;
-  d.best_i = ctx->best_i;
-  d.result = ctx->argmax_dev;
+  d.keys = ctx->step_keys;
   d.n_layers = c.n_layers;
   d.dim = c.dim;
   d.hidden = c.hidden_dim;
   d.q_dim = ctx->q_dim();
   d.kv_dim = ctx->kv_dim();
-  d.head_dim = c.head_dim;
   d.n_heads = c.n_heads;
   d.n_kv_heads = c.n_kv_heads;
   d.vocab = c.vocab_size;
@@ -654,34 +658,31 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.token = token;
   d.pos = pos;
   d.mode = mode;
-  d.nsplit = ctx->attn_splits;
-  d.min_slice = attn_min_slice_for(ctx, false);  // the single launch runs the SIMT attention
+  const int nb = ctx->num_cus;
+  // KV slices per kv head: every (kv head, slice) pair needs a workgroup of the grid
+  d.nsplit = std::max(1, std::min({ctx->attn_splits, nb / c.n_kv_heads, kMaxSplits}));
+  // fused attention + O phase: every (kv head, 128-row block) needs a workgroup; the row words hold
+  // up to kRowAccMaxTerms kv heads; no sink rotation
+  const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
+  const bool atto = ctx->step_fn_atto && pos < c.max_seq_len && kv_len <= ctx->step_atto_max &&
+                    c.n_kv_heads <= kRowAccMaxTerms && c.n_kv_heads * ((c.dim + kAttORows - 1) / kAttORows) <= nb;
   d.act = c.act;
   d.eps = c.norm_eps;
   d.qkv_clip = c.qkv_clip;
-  d.launch = ctx->flow_launches++;
-  // attention workgroups: the active KV slices at this position (same rule as attn_run)
-  const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
-  const int chunk = attn_chunk(kv_len, ctx->attn_splits, d.min_slice);
-  const int active = (kv_len + chunk - 1) / chunk;
-  const int cus = ctx->num_cus;
-  d.nb[kPhQkv] = phase_blocks((d.q_dim + 2 * d.kv_dim) / 2, cus, ctx->flow_bpc);
-  d.nb[kPhAtt] = c.n_kv_heads * active;
-  d.nb[kPhO] = phase_blocks(c.dim / 2, cus, ctx->flow_bpc);
-  d.nb[kPhW13] = phase_blocks(c.hidden_dim, cus, ctx->flow_bpc);
-  d.nb[kPhW2] = phase_blocks(c.dim, cus, ctx->flow_bpc_w2);
-  d.nb[kPhLm] = phase_blocks(c.vocab_size / 2, cus, ctx->flow_bpc);
-  const int per_layer = d.nb[0] + d.nb[1] + d.nb[2] + d.nb[3] + d.nb[4];
-  const int grid = c.n_layers * per_layer + (mode != 0 ? d.nb[kPhLm] : 0);
-  hipLaunchKernelGGL(((void (*)(FlowArgs))ctx->flow_fn), dim3(grid), dim3(kBlock), ctx->flow_lds, ctx->stream, d);
-  HIP_TRY(ctx, hipGetLastError());
+  d.base = ctx->step_base;
+  d.parity = ctx->step_launches & 1u;
+  ctx->step_base += kStepPhaseStride;
+  ctx->step_launches++;
+  void* args[] = {&d};
+  HIP_TRY(ctx, hipLaunchCooperativeKernel(atto ? ctx->step_fn_atto : ctx->step_fn, dim3(nb), dim3(kStepThreads), args,
+                                          0, ctx->stream));
   if (ctx->stats && mode != 0) HIP_TRY(ctx, hipEventRecord(ctx->ev1, ctx->stream));  // the kernel alone
   if (mode == 1)
     HIP_TRY(ctx, hipMemcpyAsync(ctx->logits_host, ctx->logits, (size_t)c.vocab_size * sizeof(float),
                                 hipMemcpyDeviceToHost, ctx->stream));
   else if (mode == 2)
-    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host, ctx->argmax_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
-  if (mode != 0)  // wait time-out flag, checked after the caller's synchronisation
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 2, ctx->step_keys + d.parity, 8, hipMemcpyDeviceToHost, ctx->stream));
+  if (mode != 0)  // wait time-out word, checked after the caller's synchronisation
     HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 1, ctx->sync + kSyncAbort, sizeof(int), hipMemcpyDeviceToHost,
                                 ctx->stream));
   return YHIP_OK;
@@ -701,9 +702,9 @@ int check_step_abort(yhip_ctx* ctx) {
 int check_flow_status(yhip_ctx* ctx) {
   if (!ctx->use_flow || ctx->argmax_host[1] == 0) return YHIP_OK;
   ctx->argmax_host[1] = 0;
-  hipMemsetAsync(ctx->sync, 0, (size_t)flow_sync_words(ctx->c.n_layers) * sizeof(unsigned), ctx->stream);
+  reset_step_sync(ctx);
   hipStreamSynchronize(ctx->stream);
-  return fail(ctx, YHIP_EDEVICE, "single-launch decode: a dependency wait timed out");
+  return fail(ctx, YHIP_EDEVICE, "single-launch decode: a grid barrier wait timed out");
 }
 
 int run_step_inner(yhip_ctx* ctx, int token, int pos, int mode);
@@ -1186,9 +1187,8 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
                a_lg = atake(V * 4), a_part = atake((size_t)c.n_heads * 64 * (c.head_dim + 2) * 4),
                a_tk = atake(64 * 4), a_am = atake(64), a_key = atake(64), a_par = atake(sizeof(StepParams)),
                a_if = atake((size_t)c.head_dim / 2 * 4), a_cs = atake((size_t)c.head_dim * 4),
-               a_sync = atake((size_t)flow_sync_words(c.n_layers) * sizeof(unsigned)),
-               a_kvc = atake(kvd * 2 * sizeof(uint16_t)), a_bv = atake((size_t)ctx->num_cus * 64 * 4),
-               a_bi = atake((size_t)ctx->num_cus * 64 * 4), a_sa = atake(256), a_racc = atake(dim * sizeof(unsigned long long)),
+               a_sync = atake((size_t)kSyncWords * sizeof(unsigned)), a_skey = atake(2 * sizeof(unsigned long long)),
+               a_sa = atake(256), a_racc = atake(dim * sizeof(unsigned long long)),
                a_ovf = atake(dim * sizeof(float));
   if (hipMalloc(&ctx->abase, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "out of device memory"));
   if (hipMemset(ctx->abase, 0, ab) != hipSuccess) return bail(fail(nullptr, YHIP_EDEVICE, "memset failed"));
@@ -1205,9 +1205,7 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   ctx->inv_freq = (float*)(ctx->abase + a_if);
   ctx->rope_cs = (float*)(ctx->abase + a_cs);
   ctx->sync = (unsigned*)(ctx->abase + a_sync);
-  ctx->kvcur = (uint32_t*)(ctx->abase + a_kvc);
-  ctx->best_v = (float*)(ctx->abase + a_bv);
-  ctx->best_i = (int*)(ctx->abase + a_bi);
+  ctx->step_keys = (unsigned long long*)(ctx->abase + a_skey);
   ctx->step_abort = (unsigned*)(ctx->abase + a_sa);
   ctx->rowacc = (unsigned long long*)(ctx->abase + a_racc);
   ctx->rowovf = (float*)(ctx->abase + a_ovf);
@@ -1224,13 +1222,17 @@ extern "C" int yhip_create(const yhip_config* cfg, int device_ordinal, yhip_ctx*
   // Single-launch decode: one workgroup per CU, all co-resident (cooperative launch).
   ctx->layout = LayerLayout{ctx->wbase, (long)per_layer, (long)o_qkv, (long)o_wo, (long)o_w1, (long)o_w3,
                             (long)o_w2, (long)o_ra, (long)o_rf, ctx->kv, (long)ctx->kv_elems};
-  ctx->flow_fn = select_flow_kernel(c);
-  if (ctx->flow_fn) {
-    const size_t kmax = std::max({(size_t)c.dim, (size_t)c.hidden_dim, (size_t)ctx->q_dim()});
-    ctx->flow_lds = std::max((16 + kmax + (size_t)c.head_dim) * sizeof(float), attn_smem_bytes(c.head_dim, c.n_heads / c.n_kv_heads));
-    // available as an option; the per-op graph is the default (measured faster on MI355X)
-    if (ctx->flow_lds > 65536) ctx->flow_fn = nullptr;
+  // every (kv head, KV slice) of the attention phase needs a workgroup of the grid
+  if (ctx->num_cus <= kStepMaxBlocks && ctx->num_cus >= c.n_kv_heads) {
+    ctx->step_fn = select_step_kernel(c, ctx->q_dim(), false);
+    ctx->step_fn_atto = select_step_kernel(c, ctx->q_dim(), true);
   }
+  for (const void** fn : {&ctx->step_fn, &ctx->step_fn_atto}) {  // one resident workgroup per CU at least
+    int per_cu = 0;
+    if (*fn && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, *fn, kStepThreads, 0) != hipSuccess || per_cu < 1))
+      *fn = nullptr;
+  }
+  if (!ctx->step_fn) ctx->step_fn_atto = nullptr;  // available as an option; the per-op graph is the default
   *out = ctx;
   return YHIP_OK;
 }
@@ -1389,7 +1391,7 @@ extern "C" int yhip_forward_argmax(yhip_ctx* ctx, int token, int pos, int* next_
   collect_stats(ctx);
   if (int rc = check_flow_status(ctx)) return rc;
   if (int rc = check_step_abort(ctx)) return rc;
-  if (!ctx->use_flow && ctx->c.vocab_size % 2 == 0) {  // the fused lm_head's packed key (argmax_key)
+  if (ctx->c.vocab_size % 2 == 0) {  // the fused lm_head's packed key (argmax_key, or the single launch's)
     unsigned long long key;
     memcpy(&key, ctx->argmax_host + 2, sizeof(key));
     *next_token = key == 0 ? 0 : (int)~(unsigned)(key & 0xffffffffull);
@@ -1551,11 +1553,11 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
     ctx->stats_steps = 0;
     return YHIP_OK;  // graphs stay valid: the events are recorded outside them
   } else if (!strcmp(key, "single_launch")) {
-    if (value && !ctx->flow_fn) return fail(ctx, YHIP_EINVAL, "no single-launch decode kernel for this shape");
+    if (value && !ctx->step_fn) return fail(ctx, YHIP_EINVAL, "no single-launch decode kernel for this shape");
     ctx->use_flow = value != 0;
-  } else if (!strcmp(key, "flow_bpc") || !strcmp(key, "flow_bpc_w2")) {
-    if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "workgroups per CU must be in [1, 64]");
-    (!strcmp(key, "flow_bpc") ? ctx->flow_bpc : ctx->flow_bpc_w2) = value;
+  } else if (!strcmp(key, "step_atto_max")) {
+    if (value < 0) return fail(ctx, YHIP_EINVAL, "step_atto_max must be >= 0");
+    ctx->step_atto_max = value;
   } else if (!strcmp(key, "attn_splits")) {
     if (value < 1 || value > 64) return fail(ctx, YHIP_EINVAL, "attn_splits must be in [1, 64]");
     ctx->attn_splits = value;
