@@ -109,7 +109,9 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * instantiation: head_dim 128 with 4 q heads per kv head, and the test shapes, on at most 256 CUs;
  * 0 = per-op kernels, the default), "step_atto_max" (single launch: attention and the O projection
  * as one phase for steps with at most this many cached tokens, below max_seq_len, default 192;
- * 0 = always two phases), "graph" (per-op kernels: 1 = replay
+ * 0 = always two phases), "step_spin_limit" (single launch: polls before a grid barrier wait gives
+ * up and the step fails with YHIP_EDEVICE; 0 = the default, about a second; small values exercise
+ * that error path), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
  * kv head, default 3/4 of compute units / n_kv_heads clamped to [1,64]),
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for

@@ -25,11 +25,13 @@ def hip():
     return H
 
 
-# The ways a step can run: one launch per token (a dataflow of workgroups), the captured hipGraph
+# The ways a step can run: one cooperative launch per token (attention and O as one phase up to 192
+# keys, as two beyond), the same with attention and O always as two phases, the captured hipGraph
 # of per-op kernels (the default: attention and O share a launch up to 700 keys, beyond that the
 # attention's slice merge moves into the O launch), the same kernels launched directly, the graph
 # with the SIMT attention, and the graph with attention (merge included) and O in separate launches.
-PATHS = {"single": dict(single_launch=1), "graph": dict(single_launch=0, graph=1),
+PATHS = {"single": dict(single_launch=1), "single_sep": dict(single_launch=1, step_atto_max=0),
+         "graph": dict(single_launch=0, graph=1),
          "direct": dict(single_launch=0, graph=0), "graph_simt": dict(single_launch=0, graph=1, attn_mfma=0),
          "graph_sep": dict(single_launch=0, graph=1, attn_o=0, split_o=0)}
 
@@ -252,7 +254,7 @@ def test_teacher_forced_logits_and_kv(cfg_name, path):
     hm.close()
 
 
-@pytest.mark.parametrize("path", ["single", "graph", "graph_sep"])
+@pytest.mark.parametrize("path", ["single", "single_sep", "graph", "graph_sep"])
 def test_mistral_shape_two_layers(path):
     # The Mistral-7B layer shape (dim 4096, hidden 14336, 32/8 heads of 128) with two layers: the
     # instantiations the full model runs, checked teacher-forced against the oracle.
@@ -733,6 +735,34 @@ def test_bad_arguments_return_errors():
     with H.HipModel(dict(MICRO, n_kv_heads=4)) as m:  # one q head per kv head: no instantiation
         with pytest.raises(H.HipError):
             m.set_option("single_launch", 1)
+
+
+def test_single_launch_barrier_timeout_fails_the_step_and_recovers():
+    # A grid barrier wait of the single launch that gives up (forced here with a spin limit of one
+    # poll: at the Mistral layer shape the first workgroups reach the W1/W3 barrier microseconds
+    # before the last, so some wait always gives up) sets the abort word; the kernel runs to its end
+    # without waiting again and the step reports an error instead of logits. The next step at the
+    # same position, with the default limit, rewrites that position's K/V and matches the oracle.
+    H = hip()
+    cfg = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=1, n_heads=32, n_kv_heads=8,
+               max_seq_len=64, rotary_dim=128)
+    t = np_tensors(cfg, seed=61)
+    om, hm = _models(cfg, t, "single")
+    toks = [5, 900, 31000, 77]
+    for pos, tok in enumerate(toks[:3]):
+        om.forward(tok, pos)
+        hm.forward(tok, pos)
+    hm.set_option("step_spin_limit", 1)
+    with pytest.raises(H.HipError, match="grid barrier"):
+        hm.forward(toks[3], 3)
+    hm.set_option("step_spin_limit", 0)
+    lo = om.forward(toks[3], 3)
+    lh = hm.forward(toks[3], 3)
+    assert npref.rel_l2(lh, lo) < 1e-4
+    lo = om.forward(12, 4)
+    lh = hm.forward(12, 4)
+    assert npref.rel_l2(lh, lo) < 1e-4
+    hm.close()
 
 
 @pytest.mark.parametrize("opts", [dict(bpc_w13=2), dict(bpc_w13=16, bpc_qkv=1, bpc_o=3, bpc_w2=2, bpc_lm=4)])

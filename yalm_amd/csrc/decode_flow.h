@@ -81,6 +81,7 @@ struct StepArgs {
   int act;
   float eps, qkv_clip;
   unsigned base;   // flag value before this launch's first phase (increases by kStepPhaseStride)
+  unsigned spin_limit;  // polls before a barrier wait gives up (sets the abort word)
   unsigned parity; // launch parity (argmax key)
 };
 
@@ -585,9 +586,9 @@ __device__ __forceinline__ void grid_wait(const StepArgs& a, unsigned target, in
     const u32x4 newer = poll();
     if (done(older)) return;
     older = newer;
-    if ((spins & 63u) == 63u) {
+    if ((spins & 63u) == 63u || spins >= a.spin_limit) {
       const unsigned ab = __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (ab || spins >= kSpinLimit) {
+      if (ab || spins >= a.spin_limit) {
         if (lane == 0) __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
       }

@@ -148,6 +148,7 @@ struct yhip_ctx {
   unsigned long long* step_keys = nullptr;  // [2] packed argmax keys (by launch parity)
   // attention and the O projection as one phase of the single launch up to this many keys (0: never)
   int step_atto_max = 192;
+  unsigned step_spin_limit = kSpinLimit;  // polls before a grid barrier wait gives up
 
   // batched prefill workspace (grown on demand, prefill.h)
   int pf_cap = 0;
@@ -670,6 +671,7 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.eps = c.norm_eps;
   d.qkv_clip = c.qkv_clip;
   d.base = ctx->step_base;
+  d.spin_limit = ctx->step_spin_limit;
   d.parity = ctx->step_launches & 1u;
   ctx->step_base += kStepPhaseStride;
   ctx->step_launches++;
@@ -1555,6 +1557,9 @@ extern "C" int yhip_set_option(yhip_ctx* ctx, const char* key, int value) {
   } else if (!strcmp(key, "single_launch")) {
     if (value && !ctx->step_fn) return fail(ctx, YHIP_EINVAL, "no single-launch decode kernel for this shape");
     ctx->use_flow = value != 0;
+  } else if (!strcmp(key, "step_spin_limit")) {
+    if (value < 0) return fail(ctx, YHIP_EINVAL, "step_spin_limit must be >= 0");
+    ctx->step_spin_limit = value ? (unsigned)value : kSpinLimit;
   } else if (!strcmp(key, "step_atto_max")) {
     if (value < 0) return fail(ctx, YHIP_EINVAL, "step_atto_max must be >= 0");
     ctx->step_atto_max = value;
