@@ -144,8 +144,9 @@ int yhip_set_option(yhip_ctx* ctx, const char* key, int value);
 
 /* The launch plan of the decode step at `pos` under the context's current options: *variant one
  * of YHIP_STEP_*, *slices the KV slices per kv head that hold keys and *slice_len their length in
- * keys (YHIP_STEP_ATTN_O: 1 and the context length, every workgroup attends to the whole
- * context). Any output may be NULL. No reference counterpart (a test and diagnostics hook). */
+ * keys (YHIP_STEP_ATTN_O, and YHIP_STEP_SINGLE with attention and O as one phase: 1 and the
+ * context length, every workgroup attends to the whole context). Any output may be NULL. No
+ * reference counterpart (a test and diagnostics hook). */
 int yhip_step_plan(yhip_ctx* ctx, int pos, int* variant, int* slices, int* slice_len);
 
 /* Device time of the steps timed since "stats" was set: total microseconds between HIP events

@@ -664,14 +664,16 @@ def test_mfma_attention_slice_rule_across_lengths(path):
     hm.close()
 
 
-def test_attention_heavy_decode_step_at_16k_keys_matches_oracle():
+@pytest.mark.parametrize("path", ["graph", "single"])
+def test_attention_heavy_decode_step_at_16k_keys_matches_oracle(path):
     # The attention-heavy workload's own decode step on a two-layer Mistral-shape model with a
     # 16448-token context: every layer's K/V pre-filled with fp16 N(0, 1) draws on both sides
     # (reference src/infer.cpp:300-305 layout), then steps at positions 16384 .. 16449 on the
-    # default options, greedy as in the workload. Each runs the split-KV attention with its slices
-    # stored (24 slices of 704 keys on a 256-CU part) and merged by the O launch (merge_o_kernel);
-    # the last two positions lie past the context (sink mode: the two sink keys re-rotated, ring
-    # slots 2 and 3).
+    # default options, greedy as in the workload. On the graph each runs the split-KV attention with
+    # its slices stored (24 slices of 704 keys on a 256-CU part) and merged by the O launch
+    # (merge_o_kernel); the single launch runs its attention phase (the same 24 slices of 704 keys,
+    # merged by the last slice of each kv head) and then the O phase. The last two positions
+    # lie past the context (sink mode: the two sink keys re-rotated, ring slots 2 and 3).
     # Two oracles: one rotating with the device's rotary frequencies (the correctly rounded fp32
     # 1 / powf(theta, j / rotary_dim)), against which the logits agree to 1e-4 and the caches entry
     # by entry; and the reference's own expression as its -ffast-math build rounds it (25 of the 64
@@ -680,7 +682,7 @@ def test_attention_heavy_decode_step_at_16k_keys_matches_oracle():
     cfg = dict(TINY, dim=4096, hidden_dim=14336, head_dim=128, n_layers=2, n_heads=32, n_kv_heads=8,
                max_seq_len=16448, rotary_dim=128)
     t = np_tensors(cfg, seed=81, std=0.02)
-    om, hm = _models(cfg, t, "graph")
+    om, hm = _models(cfg, t, path)
     om.set_rope_freqs(hm.debug_read(5, cfg["head_dim"] // 2))
     ref = O.OracleModel(cfg, t)  # the reference's frequency expression
     prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(16384), k_scale=1.0)
@@ -692,7 +694,8 @@ def test_attention_heavy_decode_step_at_16k_keys_matches_oracle():
     worst = worst_ref = 0.0
     for pos in positions:
         variant, slices, slice_len = hm.step_plan(pos)
-        assert variant == H.STEP_SPLIT_O and 2 <= slices <= 32, (pos, variant, slices, slice_len)
+        assert variant == (H.STEP_SPLIT_O if path == "graph" else H.STEP_SINGLE), (pos, variant)
+        assert 2 <= slices <= 32, (pos, variant, slices, slice_len)
         assert slices * slice_len >= min(pos + 1, cfg["max_seq_len"]) > (slices - 1) * slice_len
         lo = om.forward(tok, pos)
         lh = hm.forward(tok, pos)

@@ -625,6 +625,22 @@ int reset_step_sync(yhip_ctx* ctx) {
   return YHIP_OK;
 }
 
+// KV slices per kv head of the single launch's attention phase: every (kv head, slice) pair needs a
+// workgroup of the grid.
+int step_nsplit(const yhip_ctx* ctx) {
+  return std::max(1, std::min({ctx->attn_splits, ctx->num_cus / ctx->c.n_kv_heads, kMaxSplits}));
+}
+
+// Whether the single launch runs attention and O as one phase at this position: every (kv head,
+// 128-row block) needs a workgroup, the row words hold up to kRowAccMaxTerms kv heads, no sink
+// rotation.
+bool step_atto(const yhip_ctx* ctx, int pos) {
+  const yhip_config& c = ctx->c;
+  const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
+  return ctx->step_fn_atto && pos < c.max_seq_len && kv_len <= ctx->step_atto_max &&
+         c.n_kv_heads <= kRowAccMaxTerms && c.n_kv_heads * ((c.dim + kAttORows - 1) / kAttORows) <= ctx->num_cus;
+}
+
 int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   const yhip_config& c = ctx->c;
   if (ctx->step_base > 0x7fffffffu - 2u * kStepPhaseStride)  // flag values stay far from wrapping
@@ -660,13 +676,8 @@ int launch_flow_step(yhip_ctx* ctx, int token, int pos, int mode) {
   d.pos = pos;
   d.mode = mode;
   const int nb = ctx->num_cus;
-  // KV slices per kv head: every (kv head, slice) pair needs a workgroup of the grid
-  d.nsplit = std::max(1, std::min({ctx->attn_splits, nb / c.n_kv_heads, kMaxSplits}));
-  // fused attention + O phase: every (kv head, 128-row block) needs a workgroup; the row words hold
-  // up to kRowAccMaxTerms kv heads; no sink rotation
-  const int kv_len = pos >= c.max_seq_len ? c.max_seq_len : pos + 1;
-  const bool atto = ctx->step_fn_atto && pos < c.max_seq_len && kv_len <= ctx->step_atto_max &&
-                    c.n_kv_heads <= kRowAccMaxTerms && c.n_kv_heads * ((c.dim + kAttORows - 1) / kAttORows) <= nb;
+  d.nsplit = step_nsplit(ctx);
+  const bool atto = step_atto(ctx, pos);
   d.act = c.act;
   d.eps = c.norm_eps;
   d.qkv_clip = c.qkv_clip;
@@ -1619,9 +1630,14 @@ extern "C" int yhip_step_plan(yhip_ctx* ctx, int pos, int* variant, int* slices,
   const int kv_len = std::min(pos + 1, ctx->c.max_seq_len);
   int v = ctx->use_flow ? YHIP_STEP_SINGLE : step_variant(ctx, pos);
   int ns = 1, len = kv_len;
-  if (v != YHIP_STEP_ATTN_O) {
-    // the same rules the launches apply: the single launch and the SIMT kernel in 64-key granules
-    const bool mfma = !ctx->use_flow && attn_uses_mfma(ctx);
+  if (ctx->use_flow) {  // the single launch: the whole context per workgroup when attention and O are one phase
+    if (!step_atto(ctx, pos)) {
+      len = attn_mfma_chunk(kv_len, step_nsplit(ctx), 0);
+      ns = (kv_len + len - 1) / len;
+    }
+  } else if (v != YHIP_STEP_ATTN_O) {
+    // the same rules the launches apply (the SIMT kernel in 64-key granules)
+    const bool mfma = attn_uses_mfma(ctx);
     const int ms = attn_min_slice_for(ctx, mfma);
     len = mfma ? attn_mfma_chunk(kv_len, ctx->attn_splits, ms) : attn_chunk(kv_len, ctx->attn_splits, ms);
     ns = (kv_len + len - 1) / len;
