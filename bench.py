@@ -280,7 +280,7 @@ def main():
                     help="one workload only (default: the decode headline with long and attn as extra keys)")
     ap.add_argument("--path", choices=["graph", "single", "direct"], default="graph",
                     help="graph: per-op kernels replayed from a captured hipGraph; single: one launch per token "
-                         "(dataflow of workgroups); direct: the per-op kernels launched one by one")
+                         "(a cooperative persistent kernel, one workgroup per CU); direct: the per-op kernels launched one by one")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode budget (0 = skip)")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--attn-min-slice", type=int, default=0, help="override the attention slice floor")
