@@ -113,7 +113,7 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * up and the step fails with YHIP_EDEVICE; 0 = the default, about a second; small values exercise
  * that error path), "graph" (per-op kernels: 1 = replay
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
- * kv head, default 3/4 of compute units / n_kv_heads clamped to [1,64]),
+ * kv head, default 7/8 of compute units / n_kv_heads clamped to [1,64]),
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for
  * the MFMA attention one slice up to 320 cached tokens, then 64 up to 1024, 128 up to 5120 and 384
  * beyond; 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode
@@ -174,7 +174,7 @@ int yhip_test_matvec(const float* x, const float* gain, float eps, const uint16_
 int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* w1, const uint16_t* w2,
                   const uint16_t* w3, int hidden_dim, int dim, int act, const float* resid, float* out);
 /* GQA attention over reference-layout caches (src/infer.cpp:218-250, 394-415); `nsplit` KV slices
- * per kv head of at least 64 keys, or 0 = the decode step's own slice plan (3/4 of the compute
+ * per kv head of at least 64 keys, or 0 = the decode step's own slice plan (7/8 of the compute
  * units over the kv heads; the MFMA kernel's length rule, as option "attn_min_slice" 0).
  * The slices are merged inside the launch (the decode step beyond 700 keys defers that merge to
  * its O launch instead). att_out [n_heads*hd]. pos >= max_seq_len exercises sink rotation, which

@@ -132,9 +132,9 @@ def test_swiglu_rows_exact_over_row_loop(hidden, bpc):
 
 
 ATTN_CASES = [
-    # hd, nh, nkv, msl, kv_len, nsplit; nsplit 0 = the decode step's own slice plan (3/4 of the CUs
+    # hd, nh, nkv, msl, kv_len, nsplit; nsplit 0 = the decode step's own slice plan (7/8 of the CUs
     # over the kv heads; on the matrix cores one slice up to 320 keys, then 64-, 128- and 384-key
-    # slices: 16417 keys as 24 slices of 704 on a 256-CU part), else nsplit slices of at least 64
+    # slices: 16417 keys as 27 slices of 608 on a 256-CU part), else nsplit slices of at least 64
     (16, 4, 2, 64, 1, 0),
     (32, 8, 2, 512, 17, 0),
     (32, 8, 2, 512, 512, 3),

@@ -529,7 +529,7 @@ SPLIT_O_SHAPES = {
 def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
     # Beyond 700 keys the split-KV attention stores every slice's partial and the O launch merges
     # them (each workgroup its kv head's slices) before its Wo block: positions across the slice
-    # rules (64/128/256/384-key slices, 1 to 24 slices), at the end of the context, and past it (sink
+    # rules (64/128/256/384-key slices, 1 to 26 slices), at the end of the context, and past it (sink
     # mode: the two sink keys re-rotated, the ring position), against the oracle on a cache
     # pre-filled from the host.
     cfg = SPLIT_O_SHAPES[shape]
@@ -670,8 +670,8 @@ def test_attention_heavy_decode_step_at_16k_keys_matches_oracle(path):
     # 16448-token context: every layer's K/V pre-filled with fp16 N(0, 1) draws on both sides
     # (reference src/infer.cpp:300-305 layout), then steps at positions 16384 .. 16449 on the
     # default options, greedy as in the workload. On the graph each runs the split-KV attention with
-    # its slices stored (24 slices of 704 keys on a 256-CU part) and merged by the O launch
-    # (merge_o_kernel); the single launch runs its attention phase (the same 24 slices of 704 keys,
+    # its slices stored (27 slices of 608 keys on a 256-CU part) and merged by the O launch
+    # (merge_o_kernel); the single launch runs its attention phase (the same 27 slices of 608 keys,
     # merged by the last slice of each kv head) and then the O phase. The last two positions
     # lie past the context (sink mode: the two sink keys re-rotated, ring slots 2 and 3).
     # Two oracles: one rotating with the device's rotary frequencies (the correctly rounded fp32

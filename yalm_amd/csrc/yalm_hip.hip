@@ -245,11 +245,14 @@ void launch_by_shape(const MatvecArgs& a, int R, int blocks, hipStream_t s) {
 
 int device_cus();  // compute units of the current device (defined with the test hooks)
 
-// KV slices per kv head of the decode attention: three quarters of a workgroup per CU over all kv
-// heads (swept on MI355X at 1K-16K keys: fewer partials to merge beat one more tile per wave; more
-// than one workgroup per CU does not fit), clamped to [1, 64].
+// KV slices per kv head of the decode attention: seven eighths of a workgroup per CU over all kv
+// heads, clamped to [1, 64]. Swept on MI355X (Mistral shape, slices merged in the O launch, µs per
+// decode step with 16 / 20 / 24 / 28 / 32 slices): equal up to 2048 keys; 3216 keys 2776 / 2772 /
+// 2784 / 2769 / 2769; 4500 2831 / 2850 / 2815 / 2816 / 2838; 8000 2982 / 2910 / 2898 / 2902 / 2897;
+// 12000 3042 / 2972 / 3049 / 2966 / 2981; 16384 3164 / 3071 / 3051 / 3026 / 3026. More than one
+// workgroup per CU does not fit.
 int default_attn_splits(int cus, int n_kv_heads) {
-  return std::max(1, std::min(64, 3 * cus / (4 * std::max(1, n_kv_heads))));
+  return std::max(1, std::min(64, 7 * cus / (8 * std::max(1, n_kv_heads))));
 }
 
 // Split-K workspace bound: tiles x splits never exceed one workgroup per CU, and a 128 x 128 tile
