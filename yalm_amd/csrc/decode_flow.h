@@ -13,8 +13,8 @@
 //
 // Rows. A matvec phase's rows come in groups of two pieces of at most 16 KB: two rows (QKV, O,
 // lm_head: the row pair p = 2i, 2i+1 that RoPE rotates together), row i of W1 and of W3 (W13), or
-// the two halves of row i (W2). Workgroup b takes the contiguous groups [b n / nb, (b + 1) n / nb)
-// (every CU gets the same share of bytes), wave w of it every eighth of those. A piece is PL
+// the two halves of row i (W2). The groups are dealt to the workgroups in turn (b, b + nb, ...)
+// and a workgroup's to its waves in turn (every CU gets the same share of bytes). A piece is PL
 // buffer loads of 16 bytes per lane (1 KB per wave instruction, streaming), and a wave holds two:
 // the next piece's loads go out before the current one is used, so each wave keeps one piece in
 // flight while it computes.
@@ -155,29 +155,18 @@ __device__ __forceinline__ void issue_group(const PhaseMap& m, int g, bool valid
   issue_piece<PL>(r.b, m.w1 + off, valid ? m.pbytes : 0, lane);
 }
 
-// The groups of wave w of workgroup b: g0, g0 + step, ... (n of them). Contiguous: the workgroup
-// takes groups [b n / nb, (b + 1) n / nb), its waves every eighth; interleaved: the workgroup takes
-// b, b + nb, b + 2 nb, ..., its waves in turn. Either way every workgroup gets the same number of
-// groups to within one.
-#ifndef YK_STEP_INTERLEAVE
-#define YK_STEP_INTERLEAVE 1
-#endif
-
+// The groups of wave w of workgroup b: g0, g0 + step, ... (n of them). The groups are dealt to the
+// workgroups in turn (b, b + nb, b + 2 nb, ...) and a workgroup's to its waves in turn, so every
+// workgroup gets the same number of groups to within one (contiguous row blocks per workgroup
+// measured 3.32 against 3.24 ms per token).
 struct WaveShare {
   int g0, step, n;
 };
 __device__ __forceinline__ WaveShare wave_share(int groups, int b, int nb, int wave) {
   WaveShare s;
-  if (YK_STEP_INTERLEAVE) {
-    s.g0 = b + nb * wave;
-    s.step = nb * kStepWaves;
-    s.n = s.g0 < groups ? (groups - 1 - s.g0) / s.step + 1 : 0;
-  } else {
-    const int lo = (int)((long)b * groups / nb), hi = (int)((long)(b + 1) * groups / nb);
-    s.g0 = lo + wave;
-    s.step = kStepWaves;
-    s.n = s.g0 < hi ? (hi - 1 - s.g0) / kStepWaves + 1 : 0;
-  }
+  s.g0 = b + nb * wave;
+  s.step = nb * kStepWaves;
+  s.n = s.g0 < groups ? (groups - 1 - s.g0) / s.step + 1 : 0;
   return s;
 }
 
