@@ -27,6 +27,9 @@ Printed JSON line extras:
                 RMSNorm + W1/W3 + SwiGLU, W2 + residual, RMSNorm + lm_head), each timed with HIP
                 events on its own stream over >= 1 GiB of rotating weight copies: microseconds,
                 GB/s of algorithmic bytes, fraction of 8 TB/s, and the recorded traffic ratio
+  tp8_shard     the same kernels at one GPU's share of an 8-way tensor-parallel split (QKV 768 rows,
+                O 4096 x 512, W1/W3 1792 rows, W2 4096 x 1792, lm_head 4000 rows) and the attention
+                of one kv head, measured on this GPU (no collectives: nothing here uses a second GPU)
   cpu_baseline  the CPU oracle (a restatement of the reference -d cpu path, OpenMP over the host
                 cores given to this process) on the same host weights, over a bounded sample of the
                 decode workload: decode tok/s, and the reference's own figure (prompt + generated
@@ -65,6 +68,12 @@ MICRO_KERNELS = [("qkv", 0, 6144, 4096, True, False), ("o", 1, 4096, 4096, False
                  ("w13", 2, 14336, 4096, True, False), ("w2", 3, 4096, 14336, False, True),
                  ("lm_head", 4, 32000, 4096, True, False)]
 MICRO_WORKING_SET = 1 << 30  # rotating weight copies per kernel: at least 4 and at least 1 GiB in total
+# One GPU's share of an 8-way tensor-parallel split of the same layer: kv head r and its 4 query
+# heads (QKV rows 768), Wo by input columns (4096 x 512, partial x), W1/W3 by rows (1792), W2 by
+# input columns (4096 x 1792, partial x), lm_head by vocabulary rows (4000)
+TP8_KERNELS = [("qkv", 0, 768, 4096, True, False), ("o", 1, 4096, 512, False, True),
+               ("w13", 2, 1792, 4096, True, False), ("w2", 3, 4096, 1792, False, True),
+               ("lm_head", 4, 4000, 4096, True, False)]
 
 
 def micro_bytes(kind, rows, cols, norm, resid):
@@ -250,11 +259,11 @@ def recorded_traffic():
         return json.load(f).get("kernels", {})
 
 
-def run_microbench(hip, reps, warmup=20):
+def run_microbench(hip, reps, warmup=20, kernels=MICRO_KERNELS, label="microbench", recorded=True):
     """Each per-layer kernel on its own stream, HIP-event timed over rotating weight copies."""
-    traffic = recorded_traffic()
+    traffic = recorded_traffic() if recorded else {}
     out = {}
-    for name, kind, rows, cols, norm, resid in MICRO_KERNELS:
+    for name, kind, rows, cols, norm, resid in kernels:
         wbytes = rows * cols * 2 * (2 if kind == 2 else 1)
         copies = max(4, -(-MICRO_WORKING_SET // wbytes))
         us = hip.bench_kernel(kind, rows, cols, copies=copies, warmup=warmup, reps=reps)
@@ -264,10 +273,32 @@ def run_microbench(hip, reps, warmup=20):
         out[name] = {"shape": f"{rows}x{cols}" + (" x2" if kind == 2 else ""), "us_per_launch": round(us, 3),
                      "bytes_per_launch": alg, "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
                      "copies": copies, "traffic_ratio_recorded": rec.get("ratio") if rec else None}
-        log(f"[bench] microbench {name} {rows}x{cols}: {us:.2f} us/launch, {gbs:.0f} GB/s "
+        log(f"[bench] {label} {name} {rows}x{cols}: {us:.2f} us/launch, {gbs:.0f} GB/s "
             f"({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
-    out["traffic_source"] = ("profiles/microbench_traffic.json: recorded rocprofv3 FETCH_SIZE / WRITE_SIZE "
-                             "passes of these launches, scaled by a plain copy's counters" if traffic else None)
+    if recorded:
+        out["traffic_source"] = ("profiles/microbench_traffic.json: recorded rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                                 "passes of these launches, scaled by a plain copy's counters" if traffic else None)
+    return out
+
+
+def run_tp8_shard(hip, reps, warmup=20):
+    """One GPU's share of an 8-way tensor-parallel decode step, measured on this GPU: the per-layer
+    kernels at their shard shapes and the attention of one kv head (4 query heads) at the three
+    workloads' context lengths; the collectives (two 16 KB all-reduces of x per layer) are not
+    measured here."""
+    out = run_microbench(hip, reps, warmup, TP8_KERNELS, "tp8 shard", recorded=False)
+    attn = {}
+    for kv in (92, 3216, 16417):
+        msl = 16448 if kv > 4096 else 4096
+        attn[str(kv)] = round(hip.bench_attention(kv, max_seq_len=msl, nsplit=0, min_slice=0, n_heads=4, n_kv_heads=1,
+                                                  warmup=warmup, reps=reps), 3)
+        log(f"[bench] tp8 shard attention, 1 kv head, kv {kv}: {attn[str(kv)]:.2f} us/launch")
+    out["attention_us_one_kv_head"] = attn
+    layer = sum(out[k]["us_per_launch"] for k in ("qkv", "o", "w13", "w2"))
+    out["layer_matvec_us"] = round(layer, 3)
+    out["token_ms_without_collectives_kv92"] = round((32 * (layer + attn["92"]) + out["lm_head"]["us_per_launch"]) / 1e3, 4)
+    out["note"] = ("kernels at one GPU's share of an 8-way split (QKV 768x4096, O 4096x512, W1/W3 1792x4096, "
+                   "W2 4096x1792, lm_head 4000x4096, attention of one kv head), each timed alone; no collectives")
     return out
 
 
@@ -380,6 +411,7 @@ def main():
     w13_gbs = W13_BYTES / (us * 1e-6) / 1e9
     log(f"[bench] fused rmsnorm+W1/W3+SwiGLU: {us:.2f} us/launch, {w13_gbs:.0f} GB/s")
     micro = run_microbench(hip, args.kernel_reps)
+    tp8 = run_tp8_shard(hip, args.kernel_reps)
 
     # what the step's launch structure allows: the same weight bytes through memory-only launches
     # of the same sizes and order (matvec access pattern), and through one launch
@@ -457,6 +489,7 @@ def main():
         "roofline": roofline,
         "w13_kernel": w13,
         "microbench": micro,
+        "tp8_shard": tp8,
         "device_us_per_step": round(step_us, 2),
         "launch_ceiling": ceiling,
         "cpu_baseline": cpu,

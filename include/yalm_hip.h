@@ -216,8 +216,10 @@ int yhip_test_argmax(const float* logits, int n, int* out);
 
 /* ---- microbenchmark: one fused decode kernel at a given shape, weights rotated over `copies`
  * device-resident copies (to keep the 256 MB last-level cache from serving them), timed with HIP
- * events on the launching stream. kind: 0 = rmsnorm+QKV+RoPE (rows = q+k+v dims), 1 = O-proj +
- * residual, 2 = rmsnorm + W1/W3 + SwiGLU, 3 = W2 + residual, 4 = rmsnorm + lm_head, 5 = plain
+ * events on the launching stream. kind: 0 = rmsnorm+QKV+RoPE (rows = q+k+v dims, head_dim 128: 8 kv
+ * heads from 2048 rows on, one below, e.g. 768 = one kv head's share of an 8-way split), 1 = O-proj +
+ * residual, 2 = rmsnorm + W1/W3 + SwiGLU, 3 = W2 + residual (row pairs below 8192 columns, even
+ * rows), 4 = rmsnorm + lm_head, 5 = plain
  * device copy of rows*cols fp16 (the reference point for hardware byte counters).
  * blocks_per_cu caps the grid at blocks_per_cu x CUs workgroups (0 = the decode path's default).
  * Writes the mean kernel time in microseconds. ---- */
@@ -237,7 +239,8 @@ int yhip_bench_stream(const yhip_config* cfg, int reps, float* ms_launches, floa
 int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int reps, float* us_per_launch);
 
 /* ---- microbenchmark of the split-KV attention kernel over `copies` rotating KV caches (random
- * fp16), at position kv_len - 1, `nsplit` slices of at least `min_slice` tokens. Mean microseconds. */
+ * fp16), at position kv_len - 1, `nsplit` slices of at least `min_slice` tokens, or nsplit 0 = the
+ * decode step's own slice plan (as yhip_test_attention). Mean microseconds. */
 int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, int max_seq_len, int kv_len, int nsplit,
                          int min_slice, int copies, int warmup, int reps, float* us_per_launch);
 

@@ -61,6 +61,33 @@ def test_matvec_parity(d, n, norm, bpc):
         assert npref.rel_l2(got_r, want + r) < RTOL
 
 
+def test_tensor_parallel_shard_kernels_match_oracle():
+    # One GPU's share of an 8-way tensor-parallel split of the Mistral-7B layer, at the shapes the
+    # benchmark times: QKV of one kv head and its 4 query heads (768 x 4096, RMSNorm in), O by input
+    # columns (4096 x 512 plus the residual), W1/W3 by rows (1792 x 4096) with SwiGLU then W2 by
+    # input columns (4096 x 1792 plus the residual) and lm_head by vocabulary rows (4000 x 4096), each
+    # against the oracle (reference src/infer.cpp:63-100, 136-146, 339-390); the shard's attention (one
+    # kv head at 16417 keys) is an attention case below.
+    rng = np.random.default_rng(8)
+    x = h2f(f16(rng.standard_normal(4096)))
+    g = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    xn = O.rmsnorm(x, g, 1e-5)
+    r = rng.standard_normal(4096).astype(np.float32)
+
+    def w(d, n):
+        return f16(rng.standard_normal((d, n), dtype=np.float32) * 0.02)
+
+    for rows in (768, 4000):
+        wm = w(rows, 4096)
+        assert npref.rel_l2(hip().matvec(x, wm, gain=g, eps=1e-5), O.matmul_f16(xn, wm)) < RTOL
+    att = h2f(f16(rng.standard_normal(512)))
+    wo = w(4096, 512)
+    assert npref.rel_l2(hip().matvec(att, wo, resid=r), O.matmul_f16(att, wo) + r) < RTOL
+    w1, w3, w2 = w(1792, 4096), w(1792, 4096), w(4096, 1792)
+    got = hip().ffn(x, w1, w2, w3, gain=g, eps=1e-5, act=1, resid=r)
+    assert npref.rel_l2(got, O.ffn(xn, w1, w2, w3, 1) + r) < RTOL
+
+
 @pytest.mark.parametrize("n", [64, 4096, 14336])
 def test_matvec_one_hot_is_exact(n):
     rng = np.random.default_rng(n)
@@ -143,6 +170,7 @@ ATTN_CASES = [
     (128, 32, 8, 4096, 3201, 0),
     (128, 32, 8, 4096, 4096, 64),
     (128, 32, 8, 16448, 16417, 0),
+    (128, 4, 1, 16448, 16417, 0),  # one kv head: a GPU's share of an 8-way tensor-parallel split
     (128, 8, 1, 1024, 700, 1),
     (64, 8, 8, 100, 99, 0),       # max_seq_len not a multiple of 8: scalar V path
     (128, 32, 8, 4096, 64, 32),   # exactly one 64-token slice

@@ -2139,8 +2139,9 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
                                  float* us_per_launch) {
   if (!us_per_launch || rows <= 0 || cols <= 0 || copies <= 0 || reps <= 0 || warmup < 0 || kind < 0 || kind > 5)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
-  if ((kind == 0 || kind == 1 || kind == 4) && rows % 2) return fail(nullptr, YHIP_EINVAL, "rows must be even");
-  const int R = (kind == 3) ? 1 : 2;
+  // W2 rows one per group when they are long (14336: two pieces of 14 KB), in pairs otherwise
+  const int R = (kind == 3 && cols >= 8192) ? 1 : 2;
+  if (kind != 2 && kind != 5 && R == 2 && rows % 2) return fail(nullptr, YHIP_EINVAL, "rows must be even");
   const int nmat = (kind == 2) ? 2 : 1;
   const size_t per = (size_t)rows * cols * nmat;
   DevBufs b;
@@ -2148,8 +2149,10 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
   float* x = b.alloc<float>(cols);
   float* g = b.alloc<float>(cols);
   float* out = b.alloc<float>(std::max(rows, 1 << 16));
-  // attention-shaped KV for the QKV epilogue: 8 kv heads of 128 at msl 4096 when rows == 6144
-  const int hd = 128, nkv = 8, msl = 4096;
+  // attention-shaped KV for the QKV epilogue: kv heads of 128 at msl 4096, 8 of them from 2048 rows
+  // on (the Mistral-7B shape at 6144 rows), else one (768 rows: one kv head and its 4 query heads,
+  // a GPU's share of an 8-way tensor-parallel split)
+  const int hd = 128, nkv = rows >= 2048 ? 8 : 1, msl = 4096;
   uint16_t* kc = b.alloc<uint16_t>((size_t)nkv * hd * msl);
   uint16_t* vc = b.alloc<uint16_t>((size_t)nkv * hd * msl);
   StepParams hp{0, 7, {0, 0}};
@@ -2198,7 +2201,7 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
         a.q_dim = rows - 2 * nkv * hd; a.kv_dim = nkv * hd; a.head_dim = hd; a.msl = msl;
         a.kcache = kc; a.vcache = vc; a.params = dp; a.rope_cs = dcs; ek = kEpiQkvRope;
-        if (a.q_dim < 0) return fail(nullptr, YHIP_EINVAL, "QKV bench needs rows >= 2048");
+        if (a.q_dim <= 0 || a.q_dim % hd) return fail(nullptr, YHIP_EINVAL, "QKV bench: rows - 2 kv heads x 128 must be whole query heads");
         break;
       case 1:
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; ek = kEpiResidual;
@@ -2208,7 +2211,7 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
         a.eps = 1e-5f; a.act = 1; ek = kEpiSwiGLU;
         break;
       case 3:
-        a.w0 = base; a.row_step = cols; a.r_step = cols; a.groups = rows; ek = kEpiResidual;
+        a.w0 = base; a.row_step = (long)R * cols; a.r_step = cols; a.groups = rows / R; ek = kEpiResidual;
         break;
       default:
         a.w0 = base; a.row_step = 2L * cols; a.r_step = cols; a.groups = rows / 2; a.gain = g; a.eps = 1e-5f;
@@ -2238,10 +2241,11 @@ extern "C" int yhip_bench_kernel(int kind, int rows, int cols, int copies, int w
 
 extern "C" int yhip_bench_attention(int head_dim, int n_heads, int n_kv_heads, int max_seq_len, int kv_len, int nsplit,
                                     int min_slice, int copies, int warmup, int reps, float* us_per_launch) {
-  if (!us_per_launch || kv_len <= 0 || kv_len > max_seq_len || copies <= 0 || reps <= 0 || warmup < 0 || nsplit < 1 ||
+  if (!us_per_launch || kv_len <= 0 || kv_len > max_seq_len || copies <= 0 || reps <= 0 || warmup < 0 || nsplit < 0 ||
       nsplit > 64 || min_slice < 0 || min_slice % 64)
     return fail(nullptr, YHIP_EINVAL, "bad argument");
   if (int rc = check_attn_shape(nullptr, head_dim, n_heads, n_kv_heads)) return rc;
+  if (nsplit == 0) hook_slice_plan(head_dim, max_seq_len, n_kv_heads, nsplit, min_slice);  // the decode step's plan
   const size_t kv = (size_t)n_kv_heads * head_dim * max_seq_len;
   DevBufs b;
   uint16_t* caches = b.alloc<uint16_t>(kv * 2 * copies);
