@@ -283,13 +283,18 @@ def test_full_depth_mistral_7b_shape_greedy_and_logits_match_oracle():
     # host weights -- the greedy contract at full depth (reference src/main.cpp:169-193) -- and the
     # teacher-forced logits of the last prompt position and the first generated ones within rel-L2
     # 2e-3 (contract 1e-2; observed 6e-4: 32 layers of fp16 cache roundings where the two sides'
-    # fp32 sums differ in order).
+    # fp32 sums differ in order). The completion loop runs on the per-op graph and again on the
+    # single launch per token, whose greedy tokens must be the same.
     from yalm_amd import host
     with host.Session.synthetic(dict(host.MISTRAL_7B), context=4096) as sess:
         cfg = sess.config()
         sess.hip(0)
         prompt = [int(v) for v in host.uniform_ids(16, 81, cfg["vocab_size"])]
         toks, _, _ = sess.generate(prompt, 32, temperature=0.0, device_argmax=True)
+        L = hip().lib()
+        assert L.yhip_set_option(sess.hip_ctx(), b"single_launch", 1) == 0
+        toks_single, _, _ = sess.generate(prompt, 32, temperature=0.0, device_argmax=True)
+        assert L.yhip_set_option(sess.hip_ctx(), b"single_launch", 0) == 0
         om = O.OracleModel(dict(cfg), sess.tensors())
         lo = None
         for i, tok in enumerate(prompt):
@@ -303,6 +308,7 @@ def test_full_depth_mistral_7b_shape_greedy_and_logits_match_oracle():
                 logits_o.append(lo)
         om.close()
         assert [int(t) for t in toks] == ref
+        assert [int(t) for t in toks_single] == ref
         # teacher-forced on the device: the same tokens rewrite the same cache entries
         seq = prompt + ref
         worst = 0.0
