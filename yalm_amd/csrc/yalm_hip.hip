@@ -161,9 +161,9 @@ struct yhip_ctx {
   float* pf_qs = nullptr;    // [n][n_heads] score factors of the scaled query heads
   uint16_t* pf_A = nullptr;  // [n][q]
   int* pf_tok = nullptr;     // [n]
-  float* pf_P = nullptr;     // split-K / stream-K partials of the prefill GEMMs
+  float* pf_P = nullptr;     // split-K partials of the prefill GEMMs (and of the split last round)
   long pf_Pn = 0;            // its capacity in floats
-  unsigned* pf_flags = nullptr;  // stream-K flags (zeroed when the workspace is allocated)
+  unsigned* pf_flags = nullptr;  // split-last-round flags (zeroed when the workspace is allocated)
 
   // device timing of synchronised steps ("stats" option)
   bool stats = false;
@@ -256,10 +256,10 @@ int default_attn_splits(int cus, int n_kv_heads) {
 }
 
 // Split-K workspace bound: tiles x splits never exceed one workgroup per CU, and a 128 x 128 tile
-// (or 128 x 64 of W1 and of W3) holds 16384 partial sums; the stream-K GEMM keeps one 256 x 256
-// fp32 slot per CU.
+// (or 128 x 64 of W1 and of W3) holds 16384 partial sums; the eight-wave GEMM's split last round
+// keeps one 256 x 256 fp32 slot per CU.
 long splitk_ws_floats(int cus) { return (long)cus * kSkSlotFloats; }
-// Stream-K flags: one word per CU slot, kSkFlagStride words apart.
+// Split-last-round flags: one word per CU slot, kSkFlagStride words apart.
 size_t sk_flag_bytes(int cus) { return (size_t)cus * kSkFlagStride * sizeof(unsigned); }
 
 // Chooses the instantiation for row length K, rows-per-group R and epilogue kind.
@@ -1095,7 +1095,7 @@ int run_prefill(yhip_ctx* ctx, const int* tokens, int n, int start, float* logit
     if ((rc = launch_gemm<kGemmResid>(ctx, g, s))) return rc;
   }
   HIP_TRY(ctx, hipGetLastError());
-  // a timed-out wait of a stream-K GEMM, checked after the next synchronisation
+  // a timed-out wait of a split-last-round GEMM, checked after the next synchronisation
   HIP_TRY(ctx, hipMemcpyAsync(ctx->argmax_host + 4, ctx->step_abort, sizeof(int), hipMemcpyDeviceToHost, s));
   if (!logits_host) return YHIP_OK;
   // last token: final rmsnorm + lm_head (reference src/infer.cpp:501-527)
@@ -2057,7 +2057,7 @@ extern "C" int yhip_test_gemm(const uint16_t* a, const uint16_t* b, const uint16
   HIP_TRY(nullptr, hipDeviceSynchronize());
   unsigned aborted = 0;
   HIP_TRY(nullptr, hipMemcpy(&aborted, dabort, sizeof(aborted), hipMemcpyDeviceToHost));
-  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm: a stream-K wait timed out");
+  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm: a split-last-round wait timed out");
   if (mode == kGemmSwiGLU) HIP_TRY(nullptr, hipMemcpy(h, dh, (size_t)M * N * 2, hipMemcpyDeviceToHost));
   else HIP_TRY(nullptr, hipMemcpy(c, dc, (size_t)M * N * 4, hipMemcpyDeviceToHost));
   return YHIP_OK;
@@ -2443,7 +2443,7 @@ extern "C" int yhip_bench_gemm(int M, int N, int K, int mode, int warmup, int re
   if (e != hipSuccess) return fail(nullptr, YHIP_EDEVICE, std::string("gemm bench: ") + hipGetErrorString(e));
   unsigned aborted = 0;
   HIP_TRY(nullptr, hipMemcpy(&aborted, dabort, sizeof(aborted), hipMemcpyDeviceToHost));
-  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm bench: a stream-K wait timed out");
+  if (aborted) return fail(nullptr, YHIP_EDEVICE, "gemm bench: a split-last-round wait timed out");
   *us_per_launch = 1000.f * ms / reps;
   return YHIP_OK;
 }
