@@ -555,6 +555,29 @@ def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
     hm.close()
 
 
+def test_slice_merge_at_the_most_slices_the_o_launch_takes():
+    # The merge + O launch takes at most 32 slices per kv head (lane s of a wave holds slice s's
+    # maximum and sum): with 32 splits a 4096-key context is 32 slices of 128 keys merged there; with
+    # 33 splits the step falls back to the attention launch's own merge and a separate O launch.
+    # Both against the oracle on a cache pre-filled from the host.
+    cfg = SPLIT_O_SHAPES["mistral"]
+    t = np_tensors(cfg, seed=63, std=0.02)
+    for splits, variant in ((32, hip().STEP_SPLIT_O), (33, hip().STEP_SEPARATE)):
+        om, hm = _models(cfg, t, "graph")
+        hm.set_option("attn_splits", splits)
+        prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(64))
+        assert hm.step_plan(4095) == (variant, 32, 128)
+        assert hm.step_plan(3967) == (variant, 31, 128)
+        tok, ran = 3, (3967, 4095)
+        for pos in ran:
+            lo = om.forward(tok, pos)
+            lh = hm.forward(tok, pos)
+            assert npref.rel_l2(lh, lo) < 1e-4, (splits, pos)
+            tok = O.argmax(lo)
+        _check_kv_prefilled(om, hm, cfg, prefill, ran)
+        hm.close()
+
+
 def test_attention_and_o_in_one_launch_is_bit_reproducible():
     # The kv heads' partial products meet in integer words per row (fixed point plus an arrival
     # count), so x does not depend on the order the workgroups finish in: two contexts running the
