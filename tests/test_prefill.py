@@ -144,6 +144,33 @@ def test_prefill_matches_sequential_hydrate(cfg_name, n):
     hm.close()
 
 
+@pytest.mark.parametrize("graph", [1, 0])
+def test_odd_vocabulary_lm_head_and_argmax(graph):
+    # An odd vocabulary streams the lm_head one row per group and takes the greedy argmax in a
+    # launch of its own (the fused argmax works on row pairs), and the single launch is not
+    # offered. Batched prefill's last-token logits and decode logits against the oracle; the
+    # device's greedy token against the reference tie rule on the device's own logits.
+    cfg = dict(TINY, vocab_size=1001)
+    t = np_tensors(cfg, seed=66, std=0.02)
+    om = O.OracleModel(cfg, t)
+    hm = hip().HipModel(cfg, t)
+    hm.set_option("graph", graph)
+    with pytest.raises(hip().HipError):
+        hm.set_option("single_launch", 1)
+    toks = np.random.default_rng(67).integers(0, cfg["vocab_size"], 40)
+    lo = _sequential(om, toks)
+    assert npref.rel_l2(hm.prefill(toks), lo) < PREFILL_LOGIT_TOL
+    tok = O.argmax(lo)
+    for pos in range(len(toks), len(toks) + 8):
+        lo = om.forward(tok, pos)
+        lh = hm.forward(tok, pos)
+        assert npref.rel_l2(lh, lo) < PREFILL_LOGIT_TOL, pos
+        nxt = hm.forward_argmax(tok, pos)  # the same step again: the same K/V entries, then the token
+        assert nxt == O.argmax(lh), pos
+        tok = nxt
+    hm.close()
+
+
 # Batched-path shapes beyond tiny: one kv head of 32 dims (the V-cache transpose covers half a
 # 64-dim tile), 2 and 8 query heads per kv head, head_dim 64 and partial rotary; prompt lengths
 # that are not multiples of the 64-position transpose tile, after a few decode steps.
