@@ -443,6 +443,30 @@ def test_sink_mode_beyond_context_matches_oracle(path, shape):
     hm.close()
 
 
+@pytest.mark.parametrize("msl", [77, 100])
+@pytest.mark.parametrize("path", ["graph", "direct"])
+def test_context_length_off_the_tile_grid_matches_oracle(msl, path):
+    # The reference takes any context length (-T): with max_seq_len not a multiple of 32 the split-KV
+    # SIMT attention runs (the MFMA one needs max_seq_len % 32 == 0), through the end of the context
+    # and on into the sink ring, with the attention's slices at and off their 64-key granules.
+    cfg = dict(MICRO, max_seq_len=msl)
+    t = np_tensors(cfg, seed=68, std=0.1)
+    om, hm = _models(cfg, t, path)
+    assert hm.step_plan(msl - 1)[0] == hip().STEP_SEPARATE
+    rng = np.random.default_rng(69)
+    for pos in range(msl + 6):
+        tok = int(rng.integers(0, cfg["vocab_size"]))
+        lo = om.forward(tok, pos)
+        lh = hm.forward(tok, pos)
+        assert npref.rel_l2(lh, lo) < 1e-3, pos
+    for layer in range(cfg["n_layers"]):
+        (kh, vh), (ko, vo) = hm.kv(layer), om.kv(layer)
+        for a, b in ((kh, ko), (vh, vo)):
+            fa, fb = h2f(a), h2f(b)
+            assert np.max(np.abs(fa - fb)) <= 5e-3 * np.max(np.abs(fb)), layer
+    hm.close()
+
+
 @pytest.mark.parametrize("path", ["single", "graph"])
 def test_kv_write_then_decode_long_context(path):
     # KV pre-filled from the host in the reference layout (the attention-heavy workload's setup).
