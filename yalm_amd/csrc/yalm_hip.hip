@@ -118,7 +118,7 @@ struct yhip_ctx {
   bool use_graph = true;
   // workgroups per CU of the decode matvecs: QKV, O, W1/W3, W2, lm_head (0: default_bpc)
   int mv_bpc[5] = {0, 0, 0, 0, 0};
-  int attn_splits = 32;
+  int attn_splits = 1;       // most KV slices per kv head; set at creation (default_attn_splits)
   int attn_min_slice = 0;  // 0: the kernel's own default (attn_min_slice_for)
   bool attn_mfma = true;  // MFMA decode attention where the shape allows it
   // captured steps: [mode: hydrate, logits, argmax][step variant: kStepSeparate, kStepAttnO,
