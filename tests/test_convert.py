@@ -258,3 +258,38 @@ def test_cli_text_prompt_on_converted_file(hf_checkpoint, tmp_path):
     sure = next((i for i, m in enumerate(margins) if m < 1e-3), len(margins))
     assert sure >= 1
     assert toks[len(TEXT_IDS):len(TEXT_IDS) + sure] == want[:sure]
+
+
+@pytest.mark.gpu
+def test_cli_perplexity_and_passkey_modes_on_converted_file(hf_checkpoint, tmp_path):
+    # yalm <file> -m perplexity -p <ids> on the HIP device (reference src/main.cpp:213-294): the
+    # perplexity of the prompt's next tokens, exp(-mean log p), and its error term, against the same
+    # sums over the oracle's logits on the converted file. Then -m passkey (src/main.cpp:296-378)
+    # runs its haystack prompt token by token and batched, and prints its greedy answer.
+    import re
+    import subprocess
+    hf_dir, _ = hf_checkpoint
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "yalm_amd", "bin", "yalm")
+    if not os.path.exists(exe):
+        pytest.skip("CLI not built")
+    out = tmp_path / "m.yalm"
+    cfg, t = converted(hf_dir, out)
+    r = subprocess.run([exe, str(out), "-m", "perplexity", "-p", ",".join(map(str, PROMPT))], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    m = re.search(r"perplexity: ([0-9.e+-]+) ± ([0-9.e+-]+)", r.stdout)
+    assert m, r.stdout
+    lg = oracle_logits(cfg, t).astype(np.float64)
+    lp = np.array([lg[p, PROMPT[p + 1]] - lg[p].max() - np.log(np.exp(lg[p] - lg[p].max()).sum())
+                   for p in range(len(PROMPT) - 1)])
+    n = len(lp)
+    ppl = float(np.exp(-lp.sum() / n))
+    err = ppl * float(np.sqrt((np.sum(lp * lp) - lp.sum() ** 2 / n) / n / n))
+    assert abs(float(m.group(1)) - ppl) <= 1e-3 * ppl, (m.group(0), ppl, err)
+    assert abs(float(m.group(2)) - err) <= 1e-2 * err + 1e-4, (m.group(0), ppl, err)
+    for batched in ("0", "1"):
+        r = subprocess.run([exe, str(out), "-m", "passkey", "-n", "4", "-l", "1", "-b", batched], capture_output=True,
+                           timeout=120)  # the answer of a random model can hold partial UTF-8 byte tokens
+        so = r.stdout.decode("utf-8", errors="replace")
+        assert r.returncode == 0, r.stderr.decode("utf-8", errors="replace")
+        assert "Passkey test:" in so and "What is the pass key? The pass key is" in so, so
