@@ -122,7 +122,7 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * of the decode matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for
  * W2; the results do not depend on it), "stats" (1 = time every synchronised step on the device
  * with HIP events and reset the totals; 0 = off), "attn_o" (1 = default: for steps with at most
- * "attn_o_max" cached tokens (default 700), below max_seq_len, on the matrix-core attention's
+ * "attn_o_max" cached tokens (default 512), below max_seq_len, on the matrix-core attention's
  * shapes with at most 8 kv heads, attention and the O projection run in one launch whose
  * workgroups each repeat their kv head's attention and combine their rows of Wo . attention in
  * per-row integer words, bit-reproducibly; 0 = separate launches), "split_o" (1 = default: beyond
@@ -176,7 +176,7 @@ int yhip_test_ffn(const float* x, const float* gain, float eps, const uint16_t* 
 /* GQA attention over reference-layout caches (src/infer.cpp:218-250, 394-415); `nsplit` KV slices
  * per kv head of at least 64 keys, or 0 = the decode step's own slice plan (7/8 of the compute
  * units over the kv heads; the MFMA kernel's length rule, as option "attn_min_slice" 0).
- * The slices are merged inside the launch (the decode step beyond 700 keys defers that merge to
+ * The slices are merged inside the launch (the decode step beyond 512 keys defers that merge to
  * its O launch instead). att_out [n_heads*hd]. pos >= max_seq_len exercises sink rotation, which
  * rewrites kcache (the updated K cache is copied back). kv_len is derived from pos. */
 int yhip_test_attention(const float* q, uint16_t* kcache, const uint16_t* vcache, int head_dim, int pos,

@@ -27,7 +27,7 @@ def hip():
 
 # The ways a step can run: one cooperative launch per token (attention and O as one phase up to 192
 # keys, as two beyond), the same with attention and O always as two phases, the captured hipGraph
-# of per-op kernels (the default: attention and O share a launch up to 700 keys, beyond that the
+# of per-op kernels (the default: attention and O share a launch up to 512 keys, beyond that the
 # attention's slice merge moves into the O launch), the same kernels launched directly, the graph
 # with the SIMT attention, and the graph with attention (merge included) and O in separate launches.
 PATHS = {"single": dict(single_launch=1), "single_sep": dict(single_launch=1, step_atto_max=0),
@@ -557,7 +557,7 @@ SPLIT_O_SHAPES = {
 @pytest.mark.parametrize("path", ["graph", "direct"])
 @pytest.mark.parametrize("shape", list(SPLIT_O_SHAPES))
 def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
-    # Beyond 700 keys the split-KV attention stores every slice's partial and the O launch merges
+    # Beyond 512 keys the split-KV attention stores every slice's partial and the O launch merges
     # them (each workgroup its kv head's slices) before its Wo block: positions across the slice
     # rules (64/128/256/384-key slices, 1 to 26 slices), at the end of the context, and past it (sink
     # mode: the two sink keys re-rotated, the ring position), against the oracle on a cache
@@ -568,7 +568,7 @@ def test_slice_merge_in_the_o_launch_matches_oracle(path, shape):
     prefill = _prefill_kv(om, hm, cfg, np.random.default_rng(62))
     msl = cfg["max_seq_len"]
     tok = 3
-    ran = [pos for pos in (700, 701, 1023, 1024, 1536, 1537, 2047, 3216, msl - 1, msl, msl + 1, msl + 5)
+    ran = [pos for pos in (511, 512, 700, 701, 1023, 1024, 1536, 1537, 2047, 3216, msl - 1, msl, msl + 1, msl + 5)
            if pos <= msl + 5]
     for pos in ran:
         lo = om.forward(tok, pos)

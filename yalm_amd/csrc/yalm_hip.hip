@@ -126,10 +126,11 @@ struct yhip_ctx {
   hipGraphExec_t graph[3][3] = {};
 
   // attention and the O projection in one launch (attn_o_kernel) for contexts up to attn_o_max
-  // tokens: 108-119 us less per token than the separate launches up to 350 keys, 60 at 500, 17 at
-  // 700, slower from ~800 on (Mistral-7B shape on MI355X)
+  // tokens. Against the split-KV attention with its slice merge in the O launch (merge_o_kernel),
+  // µs per decode step (Mistral-7B shape on MI355X, same box): 100 keys 2512 / 2648, 300 2573 /
+  // 2689, 430 2617 / 2636, 490 2635 / 2638, 520 2643 / 2639, 580 2662 / 2643, 690 2676 / 2645
   bool attn_o = true;
-  int attn_o_max = 700;
+  int attn_o_max = 512;
   // beyond that, the split-KV attention leaves its slice merge to merge_o_kernel, which merges and
   // runs the O projection in one launch
   bool split_o = true;
