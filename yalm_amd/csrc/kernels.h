@@ -757,14 +757,15 @@ __host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int m
 //     per layer with two 256-key slices);
 //   - up to 1024 keys slices of 64: the merge of many short slices costs less than two or three
 //     long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1);
-//   - up to 5120 keys slices of 128 (the slice merge runs in the O launch there: µs per decode
+//   - up to 6144 keys slices of 128 (the slice merge runs in the O launch there: µs per decode
 //     step against 256-key slices, 1600 keys 2683 / 2735, 2400: 2704 / 2748, 3216: 2766 / 2775;
-//     against 384-key slices at 4500: 2797 / 2818), beyond that 384 (6000: equal, 8000: 2853
-//     against 2865 with 128); from ~8K keys the slice count (nsplit) decides.
+//     with 28 slices per kv head against 384-key ones, 4500: 2821 / 2821, 5200: 2836 / 2870,
+//     5600: 2850 / 2875, 6000: 2856 / 2876), beyond that 384 (6500: 2913 / 2882, 7500: 2889 /
+//     2894, 9000: 2924 / 2919); from ~10K keys the slice count (nsplit) decides.
 __host__ __device__ __forceinline__ int attn_mfma_chunk(int kv_len, int nsplit, int min_slice) {
   if (min_slice > 0) return attn_chunk(kv_len, nsplit, min_slice, 32);
   if (kv_len <= 320) return (kv_len + 31) / 32 * 32;
-  return attn_chunk(kv_len, nsplit, kv_len <= 1024 ? 64 : (kv_len <= 5120 ? 128 : 384), 32);
+  return attn_chunk(kv_len, nsplit, kv_len <= 1024 ? 64 : (kv_len <= 6144 ? 128 : 384), 32);
 }
 
 // Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the
