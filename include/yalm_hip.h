@@ -115,8 +115,9 @@ int yhip_kv_fill_normal(yhip_ctx* ctx, int n_positions, unsigned long long seed)
  * a captured hipGraph per step, default; 0 = direct launches), "attn_splits" (most KV slices per
  * kv head, default 7/8 of compute units / n_kv_heads clamped to [1,64]),
  * "attn_min_slice" (fewest tokens per KV slice, a multiple of 64; 0 = the kernel's default: for
- * the MFMA attention one slice up to 320 cached tokens, then 64 up to 1024, 128 up to 6144 and 384
- * beyond; 64 for the SIMT one; at least 128 from 1024 cached tokens on), "attn_mfma" (1 = decode
+ * the MFMA attention one slice up to 320 cached tokens, then 64 up to 2048, 128 up to 6144 and 384
+ * beyond; 64 for the SIMT one; a set floor, and the SIMT one's, at least 128 from 1024 cached
+ * tokens on), "attn_mfma" (1 = decode
  * attention on the matrix cores where head_dim % 32 == 0 and max_seq_len % 32 == 0, default;
  * 0 = the SIMT kernel), "bpc_qkv" / "bpc_o" / "bpc_w13" / "bpc_w2" / "bpc_lm" (workgroups per CU
  * of the decode matvecs, 0..16; 0 = the default: 2 for QKV, O and the lm_head, 12 for W1/W3, 1 for

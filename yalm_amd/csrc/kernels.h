@@ -755,8 +755,10 @@ __host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int m
 // length, from sweeps on MI355X (Mistral shape, 24 slices per kv head):
 //   - up to 320 keys one slice per kv head, no cross-workgroup merge (300 keys: 7.8 against 9.7 µs
 //     per layer with two 256-key slices);
-//   - up to 1024 keys slices of 64: the merge of many short slices costs less than two or three
-//     long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1);
+//   - up to 2048 keys slices of 64: the merge of many short slices costs less than two or three
+//     long ones (400 keys: 8.4 against 9.7; 1024: 8.9 against 10.1 µs per layer; with the merge in
+//     the O launch, µs per decode step against 128-key slices at 1100 / 1300 / 1500 / 2000 keys:
+//     2672 / 2682 / 2693 / 2715 against 2684 / 2691 / 2695 / 2719);
 //   - up to 6144 keys slices of 128 (the slice merge runs in the O launch there: µs per decode
 //     step against 256-key slices, 1600 keys 2683 / 2735, 2400: 2704 / 2748, 3216: 2766 / 2775;
 //     with 28 slices per kv head against 384-key ones, 4500: 2821 / 2821, 5200: 2836 / 2870,
@@ -765,7 +767,9 @@ __host__ __device__ __forceinline__ int attn_chunk(int kv_len, int nsplit, int m
 __host__ __device__ __forceinline__ int attn_mfma_chunk(int kv_len, int nsplit, int min_slice) {
   if (min_slice > 0) return attn_chunk(kv_len, nsplit, min_slice, 32);
   if (kv_len <= 320) return (kv_len + 31) / 32 * 32;
-  return attn_chunk(kv_len, nsplit, kv_len <= 1024 ? 64 : (kv_len <= 6144 ? 128 : 384), 32);
+  const int floor = kv_len <= 2048 ? 64 : (kv_len <= 6144 ? 128 : 384);
+  const int chunk = ((kv_len + nsplit - 1) / nsplit + 31) / 32 * 32;
+  return chunk < floor ? floor : chunk;
 }
 
 // Sum over groups of N adjacent lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a group gets the
